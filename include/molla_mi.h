@@ -1,0 +1,186 @@
+/*
+ * molla_mi.h -- C ABI of the MI355X (gfx950) decode hot path for molla.
+ *
+ * A drop-in for molla's device matvec / decoder-layer entry points.  molla's
+ * Mojo host reaches these through `external_call` (pointers cross as Int,
+ * as in /root/reference/src/molla/sys/thread.mojo:104-161).  Every pointer
+ * argument that names tensor data is a DEVICE pointer unless stated; shapes
+ * are int32 as in the reference kernels (src/molla/nn/gpu.mojo:1558-1559),
+ * byte strides int64.
+ *
+ * Conventions shared by every entry point:
+ *  - Weights are raw GGUF blocks (ggml `block_q*` byte layout), rows back to
+ *    back with no padding: row r of a (rows x cols) tensor starts at
+ *    w + r * row_bytes, row_bytes = cols / block_elements * block_bytes.
+ *    The reference device path repacks into its own "planar" layout first
+ *    (src/molla/nn/repack.mojo:692); this library reads file bytes directly.
+ *  - Everything is queued on the caller's stream and NOT synchronized, as in
+ *    the reference (gpu.mojo:2178-2180).  mi_sync() waits.
+ *  - Nothing allocates device memory per call.  Scratch comes from the
+ *    caller as a workspace (size from the matching *_workspace call), the
+ *    way the reference sizes its DeviceScratch once per session
+ *    (src/molla/nn/gpu_block.mojo:495-622).  A workspace may not be shared by
+ *    two calls in flight on different streams.
+ *  - Return value: MI_OK (0) or a negative MI_ERR_* code.  A refused call
+ *    launches nothing (the reference's pre-launch refusals,
+ *    gpu.mojo:2070-2111); mi_last_error() then describes why (thread-local).
+ *    There is no CPU fallback anywhere.
+ */
+#ifndef MOLLA_MI_H
+#define MOLLA_MI_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* mi_stream; /* a hipStream_t; NULL is the default stream */
+
+enum {
+  MI_OK = 0,
+  MI_ERR_ARG = -1,       /* null pointer, negative size, bad flag */
+  MI_ERR_KIND = -2,      /* ggml type without a device kernel */
+  MI_ERR_SHAPE = -3,     /* cols not a whole number of blocks, row_bytes mismatch, too large */
+  MI_ERR_WORKSPACE = -4, /* workspace missing or too small */
+  MI_ERR_DEVICE = -5,    /* HIP runtime error (launch, sync) */
+  MI_ERR_ALIGN = -6      /* pointer alignment the kernels require is not met */
+};
+
+/* ggml type numbers (src/molla/nn/quant.mojo:47-57).  Device kernels exist for
+ * the four quant kinds; F32 is accepted by the embedding lookup only. */
+enum { MI_F32 = 0, MI_F16 = 1, MI_Q4_0 = 2, MI_Q8_0 = 8, MI_Q4_K = 12, MI_Q6_K = 14 };
+
+/* Matvec epilogues, same integers and meaning as src/molla/nn/gpu.mojo:781-803:
+ *   NONE: y = dot          BIAS: y = dot + aux[r]
+ *   ADD:  y = y + dot      GLU:  y = act(dot) * aux[t*rows + r]  (act = silu,
+ *                                or gelu-tanh with MI_ACT_GELU)
+ * BIAS or GLU may be combined with ADD, as in the reference. */
+enum { MI_EPI_NONE = 0, MI_EPI_BIAS = 1, MI_EPI_ADD = 2, MI_EPI_GLU = 4, MI_ACT_GELU = 8 };
+
+/* ---- library ------------------------------------------------------------- */
+
+int mi_version(void);                 /* (major << 16) | minor */
+const char* mi_last_error(void);      /* last refusal / HIP error on this thread */
+int mi_sync(mi_stream stream);        /* hipStreamSynchronize; ctx.synchronize() in the reference */
+int mi_block_elements(int kind);      /* quant.mojo:78 */
+int mi_block_bytes(int kind);         /* quant.mojo:97 */
+int64_t mi_row_bytes(int kind, int32_t cols); /* tensor.mojo:204-229 row geometry, -1 if invalid */
+
+/* ---- bit-exact dequant ----------------------------------------------------
+ * out[i] = value i of the run of `count` values at w (count a whole number
+ * of blocks).  Bit-identical to src/molla/nn/quant.mojo:412 dequant_run. */
+int mi_dequant(mi_stream stream, int kind, const void* w, int64_t count, float* out);
+
+/* ---- matvec (src/molla/nn/gpu.mojo:2148 device_matvec_into and
+ *      :2945 device_matmul_into) -------------------------------------------
+ * For t < tokens, r < rows:  dot = row r of W . x[t*cols : (t+1)*cols]
+ * and y[t*rows + r] is written through the epilogue.  `y` is already offset
+ * by the caller (the reference's `at`, gpu.mojo:201-223).  aux may be NULL
+ * unless epi has BIAS or GLU.  tokens 1..8 (batch-1 decode up to the batch-8
+ * head of the configs).  Activations are carried as 23-bit block fixed point
+ * per 32 values (three int8 limbs), so every product is an exact integer dot;
+ * the result agrees with the fp32 host path to ~1e-7 relative.
+ * Workspace: mi_matvec_workspace(cols, tokens) bytes, 256-byte aligned. */
+size_t mi_matvec_workspace(int32_t cols, int32_t tokens);
+int mi_matvec(mi_stream stream, int kind, const void* w, int64_t row_bytes,
+              int32_t rows, int32_t cols, const float* x, int32_t tokens,
+              float* y, int32_t epi, const float* aux, void* work, size_t work_bytes);
+
+/* The two halves of mi_matvec, for callers that reuse one quantized
+ * activation across several matrices (q/k/v share the normed input; gate and
+ * up share it too).  xq holds mi_matvec_workspace(cols, tokens) bytes. */
+int mi_quantize(mi_stream stream, const float* x, int32_t cols, int32_t tokens, void* xq);
+int mi_matvec_xq(mi_stream stream, int kind, const void* w, int64_t row_bytes,
+                 int32_t rows, int32_t cols, const void* xq, int32_t tokens,
+                 float* y, int32_t epi, const float* aux);
+
+/* ---- block ops (src/molla/nn/gpu_ops.mojo) --------------------------------
+ * rms_norm: out[t] = x[t] * rsqrt(mean(x[t]^2) + eps) * gain, sum of squares in
+ * float64 as the host does (kernel.mojo:432-467).  If xq is non-NULL the
+ * normalised row is also quantized for a following mi_matvec_xq. */
+int mi_rms_norm(mi_stream stream, const float* x, const float* gain, int32_t n,
+                int32_t tokens, float eps, float* out, void* xq);
+
+/* Host-side helper (no device work): the rope frequency step per pair,
+ * f32(exp(f64(-2p/dim) * log(base))) -- src/molla/nn/rope.mojo:230 step_table.
+ * steps_host has dim/2 floats. */
+void mi_rope_steps(float* steps_host, int32_t dim, float base);
+
+/* Rotate `heads` heads of head_dim laid end to end in x (rows of row_stride
+ * floats, one per token) at positions pos[t] (device int32), adjacent pairs
+ * when neox == 0 (Llama).  cos/sin are taken in float64 of the float32 angle
+ * pos*step, as rope.mojo:253-285 does.  steps: device f32[dim/2]. */
+int mi_rope(mi_stream stream, float* x, int32_t heads, int32_t head_dim, int32_t dim,
+            int32_t neox, const float* steps, const int32_t* pos, int32_t tokens,
+            int64_t row_stride);
+
+/* f32 k/v rows -> f16 cache rows at slot: cache[slot*kv_width + i] = half(src[i]).
+ * gpu_ops.mojo:1491 store_kv_kernel. */
+int mi_store_kv(mi_stream stream, const float* k, const float* v, int32_t kv_width,
+                uint16_t* k_cache, uint16_t* v_cache, int32_t slot);
+
+/* One query (heads*head_dim f32) against `count` cached positions (f16,
+ * [pos][kv_heads][head_dim]); GQA with group = heads/kv_heads; scores scaled,
+ * softmax with the maximum subtracted, weighted sum of values.
+ * attention.mojo:144 attend; split over key slices with a flash-style merge
+ * like gpu_ops.mojo:929/1104.  Workspace: mi_attend_workspace(heads, head_dim, count). */
+size_t mi_attend_workspace(int32_t heads, int32_t head_dim, int32_t count);
+int mi_attend(mi_stream stream, const float* q, const uint16_t* k_cache,
+              const uint16_t* v_cache, int32_t heads, int32_t kv_heads,
+              int32_t head_dim, float scale, int32_t count, float* out,
+              void* work, size_t work_bytes);
+
+/* Index of the maximum of x[t*n : (t+1)*n] for each t, ties to the lower
+ * index (kernel.mojo:571 argmax, gpu_ops.mojo:408). out: device int32[tokens]. */
+int mi_argmax(mi_stream stream, const float* x, int32_t n, int32_t tokens, int32_t* out);
+
+/* out[t] = row ids[t] of an f32 embedding (model.mojo:102 embed). */
+int mi_embed(mi_stream stream, const float* embedding, int32_t vocab, int32_t width,
+             const int32_t* ids, int32_t tokens, float* out);
+
+/* ---- decoder layer (src/molla/nn/gpu_block.mojo:899 device_layer) -------- */
+
+typedef struct {
+  const void* data; /* device pointer to GGUF blocks */
+  int32_t kind;
+  int32_t rows;
+  int32_t cols;
+  int64_t row_bytes;
+} mi_weight;
+
+typedef struct {
+  int32_t width;    /* residual stream, 4096 for an 8B */
+  int32_t hidden;   /* MLP inner width, 14336 */
+  int32_t heads, kv_heads, head_dim; /* 32, 8, 128 */
+  int32_t rope_dim; /* rotated elements per head, usually head_dim */
+  int32_t neox;     /* 0 = adjacent pairs (Llama), 1 = half-split pairs */
+  float eps;        /* RMSNorm epsilon */
+  float attn_scale; /* usually 1/sqrt(head_dim) */
+  const float* attn_norm; /* device f32[width] */
+  const float* ffn_norm;  /* device f32[width] */
+  const float* rope_steps; /* device f32[rope_dim/2] from mi_rope_steps */
+  mi_weight wq, wk, wv, wo, gate, up, down;
+} mi_layer_desc;
+
+/* One Llama layer for `tokens` independent sequences (batch decode, one token
+ * each), in place on resid[t*width ...].  Sequence t owns k_cache/v_cache at
+ * t * cache_stride halves, laid out [slot][kv_heads*head_dim].  Its token sits
+ * at position pos[t] (device int32[tokens], read by the kernels so a captured
+ * graph can be replayed for the next token), which is also its cache slot (a
+ * contiguous cache, where the reference's `slot` equals `pos`): the rotated key
+ * and the value are written at slot pos[t] and attention runs over slots
+ * 0..pos[t].  max_count bounds pos[t] + 1 and sizes the attention grid.
+ * Order as block.mojo:466 layer: norm, q/k/v, rope q/k, store, attend,
+ * wo (+residual), norm, up, gate (+silu gate), down (+residual). */
+size_t mi_layer_workspace(const mi_layer_desc* desc, int32_t max_count, int32_t tokens);
+int mi_decoder_layer(mi_stream stream, const mi_layer_desc* desc, float* resid,
+                     uint16_t* k_cache, uint16_t* v_cache, int64_t cache_stride,
+                     const int32_t* pos, int32_t max_count, int32_t tokens,
+                     void* work, size_t work_bytes);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MOLLA_MI_H */

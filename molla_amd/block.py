@@ -1,0 +1,155 @@
+"""Host-side mirror of molla's device decoder layer and decode step.
+
+Mirrors src/molla/nn/gpu_block.mojo: DeviceLayer (:301), device_layer (:899),
+device_forward (:1644) and the engine's DeviceSession.step / generate
+(src/molla/engine/device.mojo:859 / :922) for a Llama stack with an f32
+embedding and a quantized head.  Every launch is one call into
+libmolla_mi.so; nothing here computes on the CPU.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+from dataclasses import dataclass
+
+import torch
+
+from . import gpu
+from ._lib import MiLayerDesc, check, lib
+
+
+@dataclass
+class BlockSpec:
+    """block.mojo:61 BlockSpec for a gated-silu Llama layer."""
+
+    width: int = 4096
+    hidden: int = 14336
+    heads: int = 32
+    kv_heads: int = 8
+    head_dim: int = 128
+    rope_dim: int = 128
+    rope_base: float = 500000.0
+    neox: bool = False  # Llama pairs adjacent elements (arch.mojo:146-152)
+    eps: float = 1e-5
+
+    @property
+    def attn_scale(self) -> float:
+        # attention.mojo:112: f32(1 / sqrt(f64(head_dim)))
+        return float(torch.tensor(1.0 / math.sqrt(self.head_dim), dtype=torch.float32))
+
+    def q_width(self) -> int:
+        return self.heads * self.head_dim
+
+    def kv_width(self) -> int:
+        return self.kv_heads * self.head_dim
+
+
+class DeviceLayer:
+    """One layer's device-resident weights (gpu_block.mojo:301)."""
+
+    NAMES = ("wq", "wk", "wv", "wo", "gate", "up", "down")
+
+    def __init__(self, spec: BlockSpec, attn_norm: torch.Tensor, ffn_norm: torch.Tensor, weights: dict,
+                 rope_steps: torch.Tensor):
+        self.spec = spec
+        self.attn_norm = attn_norm
+        self.ffn_norm = ffn_norm
+        self.weights = weights  # name -> gpu.Tensor
+        self.rope_steps = rope_steps
+        d = MiLayerDesc()
+        d.width, d.hidden = spec.width, spec.hidden
+        d.heads, d.kv_heads, d.head_dim = spec.heads, spec.kv_heads, spec.head_dim
+        d.rope_dim, d.neox = spec.rope_dim, int(spec.neox)
+        d.eps, d.attn_scale = spec.eps, spec.attn_scale
+        d.attn_norm, d.ffn_norm, d.rope_steps = attn_norm.data_ptr(), ffn_norm.data_ptr(), rope_steps.data_ptr()
+        for n in self.NAMES:
+            setattr(d, n, weights[n].weight())
+        self.desc = d
+
+    def weight_bytes(self) -> int:
+        return sum(w.rows * w.row_bytes() for w in self.weights.values())
+
+
+def layer_workspace(layer: DeviceLayer, max_count: int, tokens: int) -> int:
+    return lib().mi_layer_workspace(ctypes.byref(layer.desc), max_count, tokens)
+
+
+def device_layer(ctx: gpu.DeviceContext, layer: DeviceLayer, x: torch.Tensor, k_cache: torch.Tensor,
+                 v_cache: torch.Tensor, cache_stride: int, pos: torch.Tensor, max_count: int, tokens: int = 1,
+                 work: torch.Tensor | None = None) -> None:
+    """gpu_block.mojo:899 device_layer, in place on x ([tokens, width] f32).
+
+    pos: device int32[tokens], the position (= cache slot) of each sequence's
+    token; max_count bounds pos + 1."""
+    need = layer_workspace(layer, max_count, tokens)
+    if work is None:
+        work = ctx.workspace(need)
+    check(lib().mi_decoder_layer(ctx.handle, ctypes.byref(layer.desc), x.data_ptr(), k_cache.data_ptr(),
+                                 v_cache.data_ptr(), cache_stride, pos.data_ptr(), max_count, tokens,
+                                 work.data_ptr(), work.numel()))
+
+
+class DeviceModel:
+    """A Llama stack on the device: f32 embedding, layers, final norm, head."""
+
+    def __init__(self, spec: BlockSpec, embedding: torch.Tensor, layers: list, output_norm: torch.Tensor,
+                 output: gpu.Tensor):
+        self.spec = spec
+        self.embedding = embedding
+        self.layers = layers
+        self.output_norm = output_norm
+        self.output = output
+
+    @property
+    def vocab(self) -> int:
+        return self.output.rows
+
+    def weight_bytes(self) -> int:
+        return sum(l.weight_bytes() for l in self.layers) + self.output.rows * self.output.row_bytes()
+
+
+class DeviceSession:
+    """KV caches and scratch for `batch` sequences decoding together
+    (engine/device.mojo:194 DeviceKvCache + :809 DeviceSession)."""
+
+    def __init__(self, ctx: gpu.DeviceContext, model: DeviceModel, batch: int, context: int):
+        self.ctx, self.model, self.batch, self.context = ctx, model, batch, context
+        s = model.spec
+        kvw = s.kv_width()
+        self.cache_stride = context * kvw
+        dev = ctx.device
+        self.k = [torch.empty(batch * self.cache_stride, dtype=torch.float16, device=dev) for _ in model.layers]
+        self.v = [torch.empty(batch * self.cache_stride, dtype=torch.float16, device=dev) for _ in model.layers]
+        self.x = torch.empty(batch * s.width, dtype=torch.float32, device=dev)
+        self.logits = torch.empty(batch * model.vocab, dtype=torch.float32, device=dev)
+        self.pos = torch.zeros(batch, dtype=torch.int32, device=dev)
+        self.ids = torch.zeros(batch, dtype=torch.int32, device=dev)
+        self.picks = torch.zeros(batch, dtype=torch.int32, device=dev)
+        need = max(layer_workspace(l, context, batch) for l in model.layers)
+        need = max(need, lib().mi_matvec_workspace(s.width, batch))
+        self.work = torch.empty(need + 256, dtype=torch.uint8, device=dev)
+
+    def step(self) -> None:
+        """One token for every sequence: embed ids, every layer at pos, final
+        norm, head, argmax into picks (engine/device.mojo:859 step + :917 pick).
+        Queued, not synchronized; reads ids and pos from device memory."""
+        m, s, c = self.model, self.model.spec, self.ctx
+        L = lib()
+        check(L.mi_embed(c.handle, m.embedding.data_ptr(), m.embedding.shape[0], s.width, self.ids.data_ptr(),
+                         self.batch, self.x.data_ptr()))
+        for i, layer in enumerate(m.layers):
+            check(L.mi_decoder_layer(c.handle, ctypes.byref(layer.desc), self.x.data_ptr(), self.k[i].data_ptr(),
+                                     self.v[i].data_ptr(), self.cache_stride, self.pos.data_ptr(), self.context,
+                                     self.batch, self.work.data_ptr(), self.work.numel()))
+        xq = self.work.data_ptr()
+        check(L.mi_rms_norm(c.handle, self.x.data_ptr(), m.output_norm.data_ptr(), s.width, self.batch, s.eps,
+                            None, xq))
+        check(L.mi_matvec_xq(c.handle, m.output.kind, m.output.address, m.output.row_bytes(), m.output.rows,
+                             m.output.cols, xq, self.batch, self.logits.data_ptr(), gpu.EPI_NONE, None))
+        check(L.mi_argmax(c.handle, self.logits.data_ptr(), m.vocab, self.batch, self.picks.data_ptr()))
+
+    def advance(self) -> None:
+        """Greedy decode bookkeeping on the device: next ids = picks, pos += 1."""
+        self.ids.copy_(self.picks)
+        self.pos.add_(1)

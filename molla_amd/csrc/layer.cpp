@@ -1,0 +1,163 @@
+// layer.cpp -- one Llama decoder layer on the device, as a sequence of
+// launches on the caller's stream (src/molla/nn/gpu_block.mojo:899
+// device_layer, whose host twin is src/molla/nn/block.mojo:466 layer):
+//
+//   rms_norm(attn_norm) -> xq                       (norm writes the matvec input form)
+//   q | k | v = W{q,k,v} . xq                        (three projections, one fused row)
+//   rope q, k; k, v -> f16 cache at slot pos[t]
+//   attend over slots 0..pos[t] -> xq                (split-K + merge; merge writes xq)
+//   resid += Wo . xq                                 (EPI_ADD)
+//   rms_norm(ffn_norm) -> xq
+//   up = Wup . xq;  gate = silu(Wgate . xq) * up     (EPI_GLU)
+//   gate -> xq;  resid += Wdown . xq                 (EPI_ADD)
+//
+// Workspace (mi_layer_workspace), every piece 256-byte aligned:
+//   xq     4 * max(width, q_width, hidden) * tokens   activation in matvec form
+//   qkv    (q_width + 2 * kv_width) * tokens floats
+//   up     hidden * tokens floats
+//   gate   hidden * tokens floats
+//   attn   attention slices (attend_workspace)
+#include <algorithm>
+
+#include "mi_internal.h"
+
+namespace mi {
+int check_weight(const char* name, int kind, const void* w, int64_t row_bytes, int32_t rows, int32_t cols);
+}
+
+using namespace mi;
+
+namespace {
+
+size_t up256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+struct Carve {
+  size_t xq, qkv, up, gate, attn, total;
+};
+
+Carve carve(const mi_layer_desc* d, int32_t max_count, int32_t tokens) {
+  const int64_t qw = (int64_t)d->heads * d->head_dim, kvw = (int64_t)d->kv_heads * d->head_dim;
+  const int64_t widest = std::max<int64_t>({d->width, qw, d->hidden});
+  Carve c;
+  size_t at = 0;
+  c.xq = at;
+  at += up256((size_t)xq_token_bytes((int32_t)widest) * tokens);
+  c.qkv = at;
+  at += up256(sizeof(float) * (size_t)(qw + 2 * kvw) * tokens);
+  c.up = at;
+  at += up256(sizeof(float) * (size_t)d->hidden * tokens);
+  c.gate = at;
+  at += up256(sizeof(float) * (size_t)d->hidden * tokens);
+  c.attn = at;
+  at += up256(attend_workspace(d->heads, d->head_dim, max_count, tokens));
+  c.total = at;
+  return c;
+}
+
+int check_desc(const mi_layer_desc* d) {
+  if (!d) return fail(MI_ERR_ARG, "layer: null descriptor");
+  if (d->width <= 0 || d->hidden <= 0 || d->width % 256 || d->hidden % 256)
+    return fail(MI_ERR_SHAPE, "layer: width %d / hidden %d must be positive multiples of 256", d->width,
+                d->hidden);
+  if (d->heads <= 0 || d->kv_heads <= 0 || d->heads % d->kv_heads)
+    return fail(MI_ERR_SHAPE, "layer: %d query heads over %d key heads", d->heads, d->kv_heads);
+  const int group = d->heads / d->kv_heads;
+  if (group != 1 && group != 2 && group != 4 && group != 8)
+    return fail(MI_ERR_SHAPE, "layer: %d query heads per key head is not 1, 2, 4 or 8", group);
+  if (d->head_dim <= 0 || d->head_dim % 32 || d->head_dim > 512)
+    return fail(MI_ERR_SHAPE, "layer: head_dim %d", d->head_dim);
+  if (d->rope_dim <= 0 || d->rope_dim % 2 || d->rope_dim > d->head_dim)
+    return fail(MI_ERR_SHAPE, "layer: rope_dim %d in heads of %d", d->rope_dim, d->head_dim);
+  if (!(d->eps > 0.0f)) return fail(MI_ERR_ARG, "layer: a norm epsilon has to be positive");
+  if (!d->attn_norm || !d->ffn_norm || !d->rope_steps) return fail(MI_ERR_ARG, "layer: null norm or rope table");
+  const int32_t qw = d->heads * d->head_dim, kvw = d->kv_heads * d->head_dim;
+  struct {
+    const char* name;
+    const mi_weight& w;
+    int32_t rows, cols;
+  } want[] = {{"wq", d->wq, qw, d->width},       {"wk", d->wk, kvw, d->width},
+              {"wv", d->wv, kvw, d->width},      {"wo", d->wo, d->width, qw},
+              {"gate", d->gate, d->hidden, d->width}, {"up", d->up, d->hidden, d->width},
+              {"down", d->down, d->width, d->hidden}};
+  for (auto& e : want) {
+    // block.mojo:230-247 _shape: a projection of the wrong size is refused.
+    if (e.w.rows != e.rows || e.w.cols != e.cols)
+      return fail(MI_ERR_SHAPE, "layer: %s is %d x %d where the layer wants %d x %d", e.name, e.w.rows,
+                  e.w.cols, e.rows, e.cols);
+    int rc = check_weight(e.name, e.w.kind, e.w.data, e.w.row_bytes, e.w.rows, e.w.cols);
+    if (rc) return rc;
+  }
+  return MI_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t mi_layer_workspace(const mi_layer_desc* desc, int32_t max_count, int32_t tokens) {
+  if (!desc || max_count <= 0 || tokens <= 0) return 0;
+  return carve(desc, max_count, tokens).total;
+}
+
+int mi_decoder_layer(mi_stream stream, const mi_layer_desc* d, float* resid, uint16_t* k_cache,
+                     uint16_t* v_cache, int64_t cache_stride, const int32_t* pos, int32_t max_count,
+                     int32_t tokens, void* work, size_t work_bytes) {
+  int rc = check_desc(d);
+  if (rc) return rc;
+  if (!resid || !k_cache || !v_cache || !pos) return fail(MI_ERR_ARG, "layer: null pointer");
+  if (tokens < 1 || tokens > kMaxTokens) return fail(MI_ERR_ARG, "layer: tokens %d outside 1..8", tokens);
+  if (max_count <= 0) return fail(MI_ERR_SHAPE, "layer: max_count must be positive");
+  const int64_t kvw = (int64_t)d->kv_heads * d->head_dim;
+  if (tokens > 1 && cache_stride < (int64_t)max_count * kvw)
+    return fail(MI_ERR_SHAPE, "layer: cache stride %lld holds fewer than %d slots", (long long)cache_stride,
+                max_count);
+  const Carve c = carve(d, max_count, tokens);
+  if (!work || ((uintptr_t)work & 255) || work_bytes < c.total)
+    return fail(MI_ERR_WORKSPACE, "layer: workspace of %zu bytes (256-aligned), %zu needed", work_bytes, c.total);
+
+  hipStream_t s = (hipStream_t)stream;
+  char* base = (char*)work;
+  void* xq = base + c.xq;
+  float* qkv = (float*)(base + c.qkv);
+  float* up = (float*)(base + c.up);
+  float* gate = (float*)(base + c.gate);
+  void* attn = base + c.attn;
+  const int32_t qw = d->heads * d->head_dim;
+  const int64_t qkv_stride = qw + 2 * kvw;
+
+  // attention_layer (block.mojo:319)
+  if ((rc = launch_rms_norm(s, resid, d->attn_norm, d->width, tokens, d->eps, nullptr, xq))) return rc;
+  if ((rc = launch_matvec(s, d->wq.kind, d->wq.data, d->wq.row_bytes, qw, d->width, xq, tokens, qkv,
+                          qkv_stride, MI_EPI_NONE, nullptr)))
+    return rc;
+  if ((rc = launch_matvec(s, d->wk.kind, d->wk.data, d->wk.row_bytes, (int32_t)kvw, d->width, xq, tokens,
+                          qkv + qw, qkv_stride, MI_EPI_NONE, nullptr)))
+    return rc;
+  if ((rc = launch_matvec(s, d->wv.kind, d->wv.data, d->wv.row_bytes, (int32_t)kvw, d->width, xq, tokens,
+                          qkv + qw + kvw, qkv_stride, MI_EPI_NONE, nullptr)))
+    return rc;
+  if ((rc = launch_rope_store(s, qkv, d->heads, d->kv_heads, d->head_dim, d->rope_dim, d->neox, d->rope_steps,
+                              pos, tokens, qkv_stride, k_cache, v_cache, cache_stride)))
+    return rc;
+  // count = pos + 1 per sequence: the attention kernels read pos and add one.
+  if ((rc = launch_attend(s, qkv, qkv_stride, k_cache, v_cache, cache_stride, d->heads, d->kv_heads,
+                          d->head_dim, d->attn_scale, pos, -1, max_count, tokens, nullptr, xq, attn)))
+    return rc;
+  if ((rc = launch_matvec(s, d->wo.kind, d->wo.data, d->wo.row_bytes, d->width, qw, xq, tokens, resid,
+                          d->width, MI_EPI_ADD, nullptr)))
+    return rc;
+
+  // mlp_layer (block.mojo:429), gated silu
+  if ((rc = launch_rms_norm(s, resid, d->ffn_norm, d->width, tokens, d->eps, nullptr, xq))) return rc;
+  if ((rc = launch_matvec(s, d->up.kind, d->up.data, d->up.row_bytes, d->hidden, d->width, xq, tokens, up,
+                          d->hidden, MI_EPI_NONE, nullptr)))
+    return rc;
+  if ((rc = launch_matvec(s, d->gate.kind, d->gate.data, d->gate.row_bytes, d->hidden, d->width, xq, tokens,
+                          gate, d->hidden, MI_EPI_GLU, up)))
+    return rc;
+  if ((rc = launch_quantize(s, gate, d->hidden, tokens, xq))) return rc;
+  return launch_matvec(s, d->down.kind, d->down.data, d->down.row_bytes, d->width, d->hidden, xq, tokens,
+                       resid, d->width, MI_EPI_ADD, nullptr);
+}
+
+}  // extern "C"

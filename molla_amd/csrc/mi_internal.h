@@ -1,0 +1,92 @@
+// mi_internal.h -- shared definitions of the gfx950 decode kernels.
+//
+// Activation format ("xq").  Every matvec multiplies packed GGUF integers by
+// activations held as block fixed point: each run of 32 values (a "group",
+// the sub-block size every supported quant kind divides into) gets a power of
+// two scale 2^e, chosen so the largest |x| maps below 2^22, and each value
+// becomes the integer X = rint(x / 2^e), split into three signed bytes
+// X = L1*65536 + L2*256 + L3.  A weight dot is then three exact int8 dot
+// products (v_dot4c_i32_i8) per four weights, recombined in float once per
+// group.  The error against float32 x is at most 2^-23 of the group maximum
+// per value, the same order as float32 rounding of x itself.
+//
+// Layout per token, G = cols/32 groups, eight planes of G 16-byte entries:
+//   plane 2*j + hh (j = limb 0..2 most significant first, hh = which 16 of the
+//   group's 32 values): the 16 limb bytes of those values, in value order.
+//   plane 6: {float scale, float xsum, int lsum1[0], int lsum1[1]}
+//   plane 7: {int lsum23[0], int lsum23[1], 0, 0}
+// where xsum = scale * sum(X) over the group, lsum1[hh] = sum of L1 over the
+// 16 values of half hh, lsum23[hh] = sum of (L2*256 + L3) over the same 16.
+// A token's activations take 128*G = 4*cols bytes.
+#pragma once
+
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/molla_mi.h"
+
+namespace mi {
+
+constexpr int kWave = 64;
+constexpr int kPlanes = 8;
+constexpr int kMaxTokens = 8;
+
+__host__ __device__ inline int64_t xq_token_bytes(int32_t cols) { return (int64_t)cols * 4; }
+
+struct XMeta {
+  float scale;
+  float xsum;
+  int lsum1[2];
+};
+
+// ---- error state (shim.cpp) ----------------------------------------------
+int fail(int code, const char* fmt, ...);
+int hip_check(hipError_t e, const char* what);
+
+// ---- launchers (no validation beyond what the kernel itself assumes; the
+// ---- C-ABI layer in shim.cpp checks shapes before calling these) ----------
+int launch_dequant(hipStream_t s, int kind, const void* w, int64_t count, float* out);
+int launch_quantize(hipStream_t s, const float* x, int32_t cols, int32_t tokens, void* xq);
+int launch_matvec(hipStream_t s, int kind, const void* w, int64_t row_bytes, int32_t rows,
+                  int32_t cols, const void* xq, int32_t tokens, float* y, int64_t ldy, int32_t epi,
+                  const float* aux);
+int launch_rms_norm(hipStream_t s, const float* x, const float* gain, int32_t n, int32_t tokens,
+                    float eps, float* out, void* xq);
+int launch_rope(hipStream_t s, float* x, int32_t heads, int32_t head_dim, int32_t dim, int32_t neox,
+                const float* steps, const int32_t* pos, int32_t tokens, int64_t row_stride);
+int launch_store_kv(hipStream_t s, const float* k, const float* v, int32_t kv_width,
+                    uint16_t* k_cache, uint16_t* v_cache, const int32_t* slot_dev, int32_t slot_host,
+                    int32_t tokens, int64_t src_stride, int64_t cache_stride);
+// Rotate q and k heads of a fused qkv row and store k (rotated) and v into
+// the half caches at slot pos[t]; q is rotated in place.
+int launch_rope_store(hipStream_t s, float* qkv, int32_t heads, int32_t kv_heads, int32_t head_dim,
+                      int32_t dim, int32_t neox, const float* steps, const int32_t* pos,
+                      int32_t tokens, int64_t row_stride, uint16_t* k_cache, uint16_t* v_cache,
+                      int64_t cache_stride);
+size_t attend_workspace(int32_t heads, int32_t head_dim, int32_t max_count, int32_t tokens);
+int launch_attend(hipStream_t s, const float* q, int64_t q_stride, const uint16_t* k_cache,
+                  const uint16_t* v_cache, int64_t cache_stride, int32_t heads, int32_t kv_heads,
+                  int32_t head_dim, float scale, const int32_t* pos_dev, int32_t count_host,
+                  int32_t max_count, int32_t tokens, float* out, void* xq_out, void* work);
+int launch_argmax(hipStream_t s, const float* x, int32_t n, int32_t tokens, int32_t* out);
+int launch_embed(hipStream_t s, const float* emb, int32_t vocab, int32_t width, const int32_t* ids,
+                 int32_t tokens, float* out);
+
+// ---- small device helpers -----------------------------------------------
+
+__device__ __forceinline__ float half_bits_to_float(uint32_t h16) {
+  return __half2float(__ushort_as_half((unsigned short)(h16 & 0xFFFFu)));
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+  v += __shfl_xor(v, 32);
+  v += __shfl_xor(v, 16);
+  v += __shfl_xor(v, 8);
+  v += __shfl_xor(v, 4);
+  v += __shfl_xor(v, 2);
+  v += __shfl_xor(v, 1);
+  return v;
+}
+
+}  // namespace mi

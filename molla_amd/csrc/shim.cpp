@@ -1,0 +1,234 @@
+// shim.cpp -- the C ABI (include/molla_mi.h): argument checks, refusals and
+// error strings, then the launchers.  Every refusal happens before anything
+// is queued, mirroring the reference's check_matvec / check_matvec_shapes
+// (src/molla/nn/gpu.mojo:2056-2111).
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+
+#include <algorithm>
+
+#include "mi_internal.h"
+
+namespace mi {
+
+static thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof g_err, fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int hip_check(hipError_t e, const char* what) {
+  if (e == hipSuccess) return MI_OK;
+  return fail(MI_ERR_DEVICE, "%s: %s", what, hipGetErrorString(e));
+}
+
+static bool quant_kind(int kind) {
+  return kind == MI_Q4_0 || kind == MI_Q8_0 || kind == MI_Q4_K || kind == MI_Q6_K;
+}
+
+// The row geometry the kernels assume, checked once here.
+int check_weight(const char* name, int kind, const void* w, int64_t row_bytes, int32_t rows,
+                 int32_t cols) {
+  if (!quant_kind(kind)) return fail(MI_ERR_KIND, "%s: ggml type %d has no device matvec", name, kind);
+  if (!w) return fail(MI_ERR_ARG, "%s: null weight pointer", name);
+  if (rows <= 0 || cols <= 0) return fail(MI_ERR_SHAPE, "%s: %d x %d is not a matrix", name, rows, cols);
+  const int unit = kind == MI_Q6_K ? 128 : (kind == MI_Q4_K ? 256 : 64);
+  if (cols % unit != 0)
+    return fail(MI_ERR_SHAPE, "%s: %d columns is not a whole number of %d-value units for type %d", name,
+                cols, unit, kind);
+  if (kind == MI_Q6_K && cols % 256 != 0)
+    return fail(MI_ERR_SHAPE, "%s: %d columns is not a whole number of q6_k superblocks", name, cols);
+  const int64_t want = (int64_t)cols / mi_block_elements(kind) * mi_block_bytes(kind);
+  if (row_bytes != want)
+    return fail(MI_ERR_SHAPE, "%s: row_bytes %lld, but %d columns of type %d take %lld", name,
+                (long long)row_bytes, cols, kind, (long long)want);
+  const uintptr_t a = (uintptr_t)w;
+  if (kind == MI_Q4_K ? (a & 15) != 0 : (a & 3) != 0)
+    return fail(MI_ERR_ALIGN, "%s: weight pointer %p is not %d-byte aligned", name, w,
+                kind == MI_Q4_K ? 16 : 4);
+  return MI_OK;
+}
+
+}  // namespace mi
+
+using namespace mi;
+
+extern "C" {
+
+int mi_version(void) { return (0 << 16) | 1; }
+
+const char* mi_last_error(void) { return g_err; }
+
+int mi_sync(mi_stream stream) { return hip_check(hipStreamSynchronize((hipStream_t)stream), "sync"); }
+
+int mi_block_elements(int kind) {
+  switch (kind) {
+    case MI_F32: case MI_F16: return 1;
+    case MI_Q4_0: case MI_Q8_0: return 32;
+    case MI_Q4_K: case MI_Q6_K: return 256;
+  }
+  return 0;
+}
+
+int mi_block_bytes(int kind) {
+  switch (kind) {
+    case MI_F32: return 4;
+    case MI_F16: return 2;
+    case MI_Q4_0: return 18;
+    case MI_Q8_0: return 34;
+    case MI_Q4_K: return 144;
+    case MI_Q6_K: return 210;
+  }
+  return 0;
+}
+
+int64_t mi_row_bytes(int kind, int32_t cols) {
+  const int per = mi_block_elements(kind);
+  if (per == 0 || cols <= 0 || cols % per != 0) return -1;
+  return (int64_t)(cols / per) * mi_block_bytes(kind);
+}
+
+int mi_dequant(mi_stream stream, int kind, const void* w, int64_t count, float* out) {
+  if (!quant_kind(kind)) return fail(MI_ERR_KIND, "dequant: ggml type %d has no device decoder", kind);
+  if (!w || !out) return fail(MI_ERR_ARG, "dequant: null pointer");
+  const int per = mi_block_elements(kind);
+  if (count < 0 || count % per != 0)
+    return fail(MI_ERR_SHAPE, "dequant: %lld values is not a whole number of %d-value blocks",
+                (long long)count, per);
+  if (((uintptr_t)out & 15) != 0) return fail(MI_ERR_ALIGN, "dequant: output must be 16-byte aligned");
+  return launch_dequant((hipStream_t)stream, kind, w, count, out);
+}
+
+size_t mi_matvec_workspace(int32_t cols, int32_t tokens) {
+  if (cols <= 0 || tokens <= 0) return 0;
+  return (size_t)xq_token_bytes(cols) * (size_t)tokens;
+}
+
+static int check_xq(const char* name, const void* xq, int32_t cols, int32_t tokens) {
+  if (!xq) return fail(MI_ERR_WORKSPACE, "%s: null activation workspace", name);
+  if (((uintptr_t)xq & 255) != 0) return fail(MI_ERR_ALIGN, "%s: workspace must be 256-byte aligned", name);
+  if (cols <= 0 || cols % 32 != 0) return fail(MI_ERR_SHAPE, "%s: %d values is not a whole number of 32", name, cols);
+  if (tokens < 1 || tokens > kMaxTokens) return fail(MI_ERR_ARG, "%s: tokens %d outside 1..8", name, tokens);
+  return MI_OK;
+}
+
+int mi_quantize(mi_stream stream, const float* x, int32_t cols, int32_t tokens, void* xq) {
+  if (!x) return fail(MI_ERR_ARG, "quantize: null input");
+  int rc = check_xq("quantize", xq, cols, tokens);
+  if (rc) return rc;
+  return launch_quantize((hipStream_t)stream, x, cols, tokens, xq);
+}
+
+int mi_matvec_xq(mi_stream stream, int kind, const void* w, int64_t row_bytes, int32_t rows,
+                 int32_t cols, const void* xq, int32_t tokens, float* y, int32_t epi, const float* aux) {
+  int rc = check_weight("matvec", kind, w, row_bytes, rows, cols);
+  if (rc) return rc;
+  if ((rc = check_xq("matvec", xq, cols, tokens))) return rc;
+  if (!y) return fail(MI_ERR_ARG, "matvec: null output");
+  if (epi & ~(MI_EPI_BIAS | MI_EPI_ADD | MI_EPI_GLU | MI_ACT_GELU))
+    return fail(MI_ERR_ARG, "matvec: unknown epilogue bits 0x%x", epi);
+  if ((epi & MI_EPI_BIAS) && (epi & MI_EPI_GLU)) return fail(MI_ERR_ARG, "matvec: BIAS and GLU together");
+  if ((epi & (MI_EPI_BIAS | MI_EPI_GLU)) && !aux) return fail(MI_ERR_ARG, "matvec: epilogue needs aux");
+  return launch_matvec((hipStream_t)stream, kind, w, row_bytes, rows, cols, xq, tokens, y, rows, epi, aux);
+}
+
+int mi_matvec(mi_stream stream, int kind, const void* w, int64_t row_bytes, int32_t rows, int32_t cols,
+              const float* x, int32_t tokens, float* y, int32_t epi, const float* aux, void* work,
+              size_t work_bytes) {
+  int rc = check_weight("matvec", kind, w, row_bytes, rows, cols);
+  if (rc) return rc;
+  if (!x) return fail(MI_ERR_ARG, "matvec: null input");
+  if ((rc = check_xq("matvec", work, cols, tokens))) return rc;
+  if (work_bytes < mi_matvec_workspace(cols, tokens))
+    return fail(MI_ERR_WORKSPACE, "matvec: workspace of %zu bytes, %zu needed", work_bytes,
+                mi_matvec_workspace(cols, tokens));
+  if ((rc = mi_quantize(stream, x, cols, tokens, work))) return rc;
+  return mi_matvec_xq(stream, kind, w, row_bytes, rows, cols, work, tokens, y, epi, aux);
+}
+
+int mi_rms_norm(mi_stream stream, const float* x, const float* gain, int32_t n, int32_t tokens, float eps,
+                float* out, void* xq) {
+  if (!x || !gain || (!out && !xq)) return fail(MI_ERR_ARG, "rms_norm: null pointer");
+  if (n <= 0 || tokens <= 0) return fail(MI_ERR_SHAPE, "rms_norm: bad shape %d x %d", tokens, n);
+  if (!(eps > 0.0f)) return fail(MI_ERR_ARG, "rms_norm: epsilon must be positive");
+  if (xq) {
+    int rc = check_xq("rms_norm", xq, n, tokens);
+    if (rc) return rc;
+  }
+  return launch_rms_norm((hipStream_t)stream, x, gain, n, tokens, eps, out, xq);
+}
+
+// rope.mojo:230 step_table: f32(exp(f64(y) * log(f64(base)))), y = f32(-2p) / f32(dim).
+void mi_rope_steps(float* steps_host, int32_t dim, float base) {
+  for (int32_t pair = 0; pair < dim / 2; pair++) {
+    const float y = -2.0f * (float)pair / (float)dim;
+    steps_host[pair] = base <= 0.0f ? 0.0f : (float)exp((double)y * log((double)base));
+  }
+}
+
+int mi_rope(mi_stream stream, float* x, int32_t heads, int32_t head_dim, int32_t dim, int32_t neox,
+            const float* steps, const int32_t* pos, int32_t tokens, int64_t row_stride) {
+  if (!x || !steps || !pos) return fail(MI_ERR_ARG, "rope: null pointer");
+  if (heads <= 0 || tokens <= 0 || dim <= 0 || dim % 2 || dim > head_dim)
+    return fail(MI_ERR_SHAPE, "rope: rotary dimension %d in heads of %d", dim, head_dim);
+  if (row_stride < (int64_t)heads * head_dim) return fail(MI_ERR_SHAPE, "rope: row stride too small");
+  return launch_rope((hipStream_t)stream, x, heads, head_dim, dim, neox, steps, pos, tokens, row_stride);
+}
+
+int mi_store_kv(mi_stream stream, const float* k, const float* v, int32_t kv_width, uint16_t* k_cache,
+                uint16_t* v_cache, int32_t slot) {
+  if (!k || !v || !k_cache || !v_cache) return fail(MI_ERR_ARG, "store_kv: null pointer");
+  if (kv_width <= 0 || slot < 0) return fail(MI_ERR_SHAPE, "store_kv: bad width or slot");
+  return launch_store_kv((hipStream_t)stream, k, v, kv_width, k_cache, v_cache, nullptr, slot, 1, kv_width, 0);
+}
+
+size_t mi_attend_workspace(int32_t heads, int32_t head_dim, int32_t count) {
+  if (heads <= 0 || head_dim <= 0 || count <= 0) return 0;
+  return attend_workspace(heads, head_dim, count, 1);
+}
+
+static int check_attn(const char* name, int32_t heads, int32_t kv_heads, int32_t head_dim) {
+  if (heads <= 0 || kv_heads <= 0 || heads % kv_heads)
+    return fail(MI_ERR_SHAPE, "%s: %d query heads over %d key heads", name, heads, kv_heads);
+  const int group = heads / kv_heads;
+  if (group != 1 && group != 2 && group != 4 && group != 8)
+    return fail(MI_ERR_SHAPE, "%s: %d query heads per key head is not 1, 2, 4 or 8", name, group);
+  if (head_dim <= 0 || head_dim % 32 || head_dim > 512)
+    return fail(MI_ERR_SHAPE, "%s: head_dim %d is not a multiple of 32 up to 512", name, head_dim);
+  return MI_OK;
+}
+
+int mi_attend(mi_stream stream, const float* q, const uint16_t* k_cache, const uint16_t* v_cache,
+              int32_t heads, int32_t kv_heads, int32_t head_dim, float scale, int32_t count, float* out,
+              void* work, size_t work_bytes) {
+  if (!q || !k_cache || !v_cache || !out) return fail(MI_ERR_ARG, "attend: null pointer");
+  int rc = check_attn("attend", heads, kv_heads, head_dim);
+  if (rc) return rc;
+  if (count <= 0) return fail(MI_ERR_SHAPE, "attention needs at least one key to look at");
+  if (!work || work_bytes < mi_attend_workspace(heads, head_dim, count))
+    return fail(MI_ERR_WORKSPACE, "attend: workspace of %zu bytes, %zu needed", work_bytes,
+                mi_attend_workspace(heads, head_dim, count));
+  return launch_attend((hipStream_t)stream, q, (int64_t)heads * head_dim, k_cache, v_cache, 0, heads,
+                       kv_heads, head_dim, scale, nullptr, count, count, 1, out, nullptr, work);
+}
+
+int mi_argmax(mi_stream stream, const float* x, int32_t n, int32_t tokens, int32_t* out) {
+  if (!x || !out) return fail(MI_ERR_ARG, "argmax: null pointer");
+  if (n <= 0 || tokens <= 0) return fail(MI_ERR_SHAPE, "argmax: empty row");
+  return launch_argmax((hipStream_t)stream, x, n, tokens, out);
+}
+
+int mi_embed(mi_stream stream, const float* embedding, int32_t vocab, int32_t width, const int32_t* ids,
+             int32_t tokens, float* out) {
+  if (!embedding || !ids || !out) return fail(MI_ERR_ARG, "embed: null pointer");
+  if (vocab <= 0 || width <= 0 || width % 4 || tokens <= 0)
+    return fail(MI_ERR_SHAPE, "embed: bad shape vocab %d width %d", vocab, width);
+  return launch_embed((hipStream_t)stream, embedding, vocab, width, ids, tokens, out);
+}
+
+}  // extern "C"
