@@ -1,0 +1,234 @@
+"""Benchmark: Q4_K matvec HBM GB/s on MI355X (+ the 8B Q4_K decode step).
+
+Workload: Q4_K 14336 x 4096 matvec at batch 1 on
+synthetic GGUF blocks (seeded), x fp32 ~ N(0,1).  A "step" is one matvec:
+quantize x into the kernels' activation form, then the fused
+dequantize-and-dot over the 33,030,144 weight bytes.  Weights are rotated over
+enough distinct copies (>= 2 GiB) that every step reads cold HBM, past the
+256 MB Infinity Cache.  Timing: HIP events on the launch stream around exactly
+K steps after W warmup steps, bracketed by synchronize.
+
+`value` = algorithmic bytes (weights + x + y) per step / wall time per step.
+`roofline` = the matvec kernel alone: bytes / its average duration measured
+with per-launch HIP event pairs on the same stream.  `cpu_baseline` = the CPU
+oracle (a C restatement of molla's serial host matvec, kernel.mojo:316) on the
+same bytes, single thread, over a bounded number of repetitions.
+
+--decode also runs config 5 (synthetic 8B: 32 Q4_K layers, Q6_K head, f32
+embedding; prefill then greedy decode) and reports tokens/s in "decode".
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+ROWS, COLS = 14336, 4096
+PEAK_GBS = 8000.0
+
+
+def _algo_bytes(rows, cols, tokens, wbytes):
+    return wbytes + 4 * tokens * (cols + rows)
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--decode", action="store_true", help="also time the synthetic 8B decode step")
+    ap.add_argument("--decode-tokens", type=int, default=64)
+    ap.add_argument("--prompt", type=int, default=2048)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}).",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    from molla_amd import gpu, synth
+    from molla_amd._lib import check, lib
+
+    torch.cuda.init()
+    ctx = gpu.DeviceContext(0)
+    L = lib()
+    kind = gpu.Q_Q4_K
+    rb = gpu.row_bytes(kind, COLS)
+    wbytes = ROWS * rb
+    copies = max(2, int((2 << 30) // wbytes) + 1)
+    base = synth.quant_tensor(kind, ROWS, COLS, 20240101, device="cuda")
+    ws = [base] + [base.clone() for _ in range(copies - 1)]
+    x = synth.normal(COLS, 7, device="cuda")
+    y = torch.empty(ROWS, dtype=torch.float32, device="cuda")
+    xq = torch.empty(L.mi_matvec_workspace(COLS, 1), dtype=torch.uint8, device="cuda")
+    h = ctx.handle
+
+    def step(i):
+        w = ws[i % copies]
+        check(L.mi_quantize(h, x.data_ptr(), COLS, 1, xq.data_ptr()))
+        check(L.mi_matvec_xq(h, kind, w.data_ptr(), rb, ROWS, COLS, xq.data_ptr(), 1, y.data_ptr(), 0, None))
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    stream = torch.cuda.current_stream()
+    e0.record(stream)
+    for i in range(args.steps):
+        step(args.warmup + i)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms_per_step = e0.elapsed_time(e1) / args.steps
+    algo = _algo_bytes(ROWS, COLS, 1, wbytes)
+    value = algo / (ms_per_step * 1e-3) / 1e9
+
+    # dominant kernel alone: per-launch event pairs on the launch stream
+    n_k = min(args.steps, 100)
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(n_k)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(n_k)]
+    check(L.mi_quantize(h, x.data_ptr(), COLS, 1, xq.data_ptr()))
+    for i in range(n_k):
+        w = ws[i % copies]
+        starts[i].record(stream)
+        check(L.mi_matvec_xq(h, kind, w.data_ptr(), rb, ROWS, COLS, xq.data_ptr(), 1, y.data_ptr(), 0, None))
+        ends[i].record(stream)
+    torch.cuda.synchronize()
+    k_ms = sorted(s.elapsed_time(e) for s, e in zip(starts, ends))
+    k_avg_ms = sum(k_ms) / len(k_ms)
+    achieved = algo / (k_avg_ms * 1e-3) / 1e9
+
+    line = {
+        "metric": "Q4_K matvec HBM GB/s (% of peak); 8B Q4_K decode tokens/sec at batch 1",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "q4_k x int8-limb activations, int32/fp32 accumulate",
+        "data": "synthetic (seeded GGUF Q4_K blocks, x ~ N(0,1)), weights rotated over "
+                f"{copies} copies ({copies * wbytes / 2**30:.1f} GiB) so every step reads cold HBM",
+        "config": {"workload": "Q4_K matvec 14336x4096, batch 1 (BASELINE configs[1], ffn gate/up)",
+                   "rows": ROWS, "cols": COLS, "tokens": 1, "weight_bytes": wbytes,
+                   "algorithmic_bytes_per_step": algo, "parallelism": "single GPU"},
+        "pct_of_hbm_peak": round(100 * value / PEAK_GBS, 1),
+        "roofline": {"bound": "hbm", "kernel": "matvec_kernel<Q4_K>",
+                     "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / PEAK_GBS, 4), "traffic": _traffic_from_profile(),
+                     "kernel_avg_us": round(k_avg_ms * 1e3, 3),
+                     "kernel_min_us": round(k_ms[0] * 1e3, 3)},
+    }
+
+    if not args.no_cpu:
+        line["cpu_baseline"] = _cpu_baseline(base, kind, rb, x)
+    if args.decode:
+        line["decode"] = _decode(ctx, args)
+    print(json.dumps(line), flush=True)
+
+
+def _traffic_from_profile():
+    """HBM bytes per launch from the committed rocprofv3 --pmc summary
+    (FETCH_SIZE + WRITE_SIZE, scaled by a copy kernel's reading), or None."""
+    p = os.path.join(ROOT, "profiles", "q4k_matvec_14336x4096_traffic.json")
+    if os.path.exists(p):
+        with open(p) as f:
+            return json.load(f).get("bytes_per_launch")
+    return None
+
+
+def _cpu_baseline(w_dev, kind, rb, x_dev):
+    """The CPU oracle (serial C restatement of kernel.mojo:316 matvec) on the
+    same bytes, single thread; bounded to ~10 s of work."""
+    import numpy as np
+
+    import oracle
+
+    blob = w_dev.cpu().numpy()
+    x = x_dev.cpu().numpy()
+    t0 = time.perf_counter()
+    reps = 0
+    while True:
+        oracle.matvec(kind, blob, ROWS, COLS, x, threads=1)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el > 10.0 or reps >= 200:
+            break
+    per = el / reps
+    gbs = _algo_bytes(ROWS, COLS, 1, ROWS * rb) / per / 1e9
+    return {"value": round(gbs, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"{reps} full Q4_K 14336x4096 matvecs (same bytes), {per * 1e3:.1f} ms each",
+            "gpu_speedup": None}
+
+
+def _decode(ctx, args):
+    """Config 5: synthetic 8B (32 layers, Q4_K, Q6_K head, f32 embedding)."""
+    import torch
+
+    from molla_amd import block, gpu, synth
+
+    spec = block.BlockSpec()
+    vocab = 128256
+    dev = "cuda"
+    steps = torch.from_numpy(gpu.rope_steps(spec.rope_dim, spec.rope_base)).to(dev)
+    layers = []
+    seed = 1000
+    qw, kvw = spec.q_width(), spec.kv_width()
+    shapes = {"wq": (qw, spec.width), "wk": (kvw, spec.width), "wv": (kvw, spec.width), "wo": (spec.width, qw),
+              "gate": (spec.hidden, spec.width), "up": (spec.hidden, spec.width), "down": (spec.width, spec.hidden)}
+    for li in range(32):
+        ws = {}
+        for n, (r, c) in shapes.items():
+            seed += 1
+            ws[n] = gpu.Tensor.from_bytes(synth.quant_tensor(gpu.Q_Q4_K, r, c, seed, device=dev), gpu.Q_Q4_K, c, r)
+        an = synth.normal(spec.width, seed + 7, device=dev, mean=1.0, std=0.1)
+        fn = synth.normal(spec.width, seed + 8, device=dev, mean=1.0, std=0.1)
+        layers.append(block.DeviceLayer(spec, an, fn, ws, steps))
+    emb = synth.normal(vocab * spec.width, 77, device=dev).view(vocab, spec.width)
+    onorm = synth.normal(spec.width, 78, device=dev, mean=1.0, std=0.1)
+    head = gpu.Tensor.from_bytes(synth.quant_tensor(gpu.Q_Q6_K, vocab, spec.width, 79, device=dev), gpu.Q_Q6_K,
+                                 spec.width, vocab)
+    model = block.DeviceModel(spec, emb, layers, onorm, head)
+    ctxlen = args.prompt + args.decode_tokens + 1
+    sess = block.DeviceSession(ctx, model, batch=1, context=ctxlen)
+    prompt = synth.tokens(args.prompt, vocab, 5, device=dev)
+    sess.pos.zero_()
+    t0 = time.perf_counter()
+    for p in range(args.prompt):  # host-side prefill one token at a time (engine/session.mojo:119)
+        sess.ids.copy_(prompt[p:p + 1])
+        sess.step()
+        sess.pos.add_(1)
+    torch.cuda.synchronize()
+    prefill_s = time.perf_counter() - t0
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    sess.ids.copy_(sess.picks)
+    e0.record()
+    for _ in range(args.decode_tokens):
+        sess.step()
+        sess.advance()
+    e1.record()
+    torch.cuda.synchronize()
+    ms_tok = e0.elapsed_time(e1) / args.decode_tokens
+    wb = model.weight_bytes()
+    return {"metric": "8B Q4_K decode tokens/sec at batch 1", "tokens_per_s": round(1000 / ms_tok, 2),
+            "ms_per_token": round(ms_tok, 3), "prompt": args.prompt, "generated": args.decode_tokens,
+            "weight_bytes_per_token": wb, "weight_stream_gbs": round(wb / (ms_tok * 1e-3) / 1e9, 1),
+            "frac_of_weight_roofline": round(wb / (ms_tok * 1e-3) / 1e9 / PEAK_GBS, 4),
+            "prefill_s": round(prefill_s, 2)}
+
+
+if __name__ == "__main__":
+    main()
