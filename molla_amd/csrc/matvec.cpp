@@ -1,0 +1,31 @@
+// matvec.hip -- routes mi_matvec / mi_matvec_xq to the kernel for its kind
+// and batch: the batch-1 Q4_K kernel of matvec_rows.hip, else the general
+// kernel of matvec_kernel.h, instantiated per kind in matvec_<kind>.hip.
+#include "mi_internal.h"
+
+namespace mi {
+
+int launch_matvec_q4k(hipStream_t, const void*, int64_t, int32_t, int32_t, const void*, int32_t, float*, int64_t,
+                      int32_t, const float*);
+int launch_matvec_q6k(hipStream_t, const void*, int64_t, int32_t, int32_t, const void*, int32_t, float*, int64_t,
+                      int32_t, const float*);
+int launch_matvec_q40(hipStream_t, const void*, int64_t, int32_t, int32_t, const void*, int32_t, float*, int64_t,
+                      int32_t, const float*);
+int launch_matvec_q80(hipStream_t, const void*, int64_t, int32_t, int32_t, const void*, int32_t, float*, int64_t,
+                      int32_t, const float*);
+
+int launch_matvec(hipStream_t s, int kind, const void* w, int64_t row_bytes, int32_t rows,
+                  int32_t cols, const void* xq, int32_t tokens, float* y, int64_t ldy, int32_t epi,
+                  const float* aux) {
+  if (tokens == 1 && kind == MI_Q4_K && q4k_rows_fits(cols))
+    return launch_q4k_rows(s, w, row_bytes, rows, cols, xq, y, epi, aux);
+  switch (kind) {
+    case MI_Q4_K: return launch_matvec_q4k(s, w, row_bytes, rows, cols, xq, tokens, y, ldy, epi, aux);
+    case MI_Q6_K: return launch_matvec_q6k(s, w, row_bytes, rows, cols, xq, tokens, y, ldy, epi, aux);
+    case MI_Q4_0: return launch_matvec_q40(s, w, row_bytes, rows, cols, xq, tokens, y, ldy, epi, aux);
+    case MI_Q8_0: return launch_matvec_q80(s, w, row_bytes, rows, cols, xq, tokens, y, ldy, epi, aux);
+  }
+  return fail(MI_ERR_KIND, "matvec: ggml type %d has no device kernel", kind);
+}
+
+}  // namespace mi

@@ -1,4 +1,6 @@
-// matvec.hip -- fused dequantize-and-dot over raw GGUF blocks, gfx950.
+// matvec_kernel.h -- fused dequantize-and-dot over raw GGUF blocks, gfx950.
+// Included once per quant kind (matvec_<kind>.hip) so the kinds compile in
+// parallel; matvec.hip routes a call to its kind.
 //
 // Replaces the reference's planar_matvec_kernel / planar_matmul_kernel
 // (src/molla/nn/gpu.mojo:1533, :1809) for Q8_0, Q4_0, Q4_K and Q6_K.
@@ -19,6 +21,8 @@
 // whole number of 16-byte pieces).  The other kinds only need 4-byte aligned
 // rows; their 18/34/210-byte blocks are realigned in registers with
 // v_alignbyte_b32.
+#pragma once
+
 #include "matvec_units.h"
 
 namespace mi {
@@ -130,17 +134,4 @@ int launch_kind(hipStream_t s, const void* w, int64_t rb, int rows, int cols, co
 }
 
 }  // namespace
-
-int launch_matvec(hipStream_t s, int kind, const void* w, int64_t row_bytes, int32_t rows,
-                  int32_t cols, const void* xq, int32_t tokens, float* y, int64_t ldy, int32_t epi,
-                  const float* aux) {
-  switch (kind) {
-    case MI_Q4_K: return launch_kind<MI_Q4_K>(s, w, row_bytes, rows, cols, xq, tokens, y, ldy, epi, aux);
-    case MI_Q6_K: return launch_kind<MI_Q6_K>(s, w, row_bytes, rows, cols, xq, tokens, y, ldy, epi, aux);
-    case MI_Q4_0: return launch_kind<MI_Q4_0>(s, w, row_bytes, rows, cols, xq, tokens, y, ldy, epi, aux);
-    case MI_Q8_0: return launch_kind<MI_Q8_0>(s, w, row_bytes, rows, cols, xq, tokens, y, ldy, epi, aux);
-  }
-  return fail(MI_ERR_KIND, "matvec: ggml type %d has no device kernel", kind);
-}
-
 }  // namespace mi

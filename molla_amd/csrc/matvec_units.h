@@ -55,6 +55,7 @@ struct Q4KUnit {
     // the byte shift is 16*(h&1) + 8e for both packings.
     const uint32_t sh = 16u * (h & 1);
     const bool high = h >= 2;
+    const uint32_t hs2 = 2u * (uint32_t)(h >> 1);
     float dsc[R][2], dmn[R][2];
 #pragma unroll
     for (int r = 0; r < R; r++) {
@@ -62,14 +63,17 @@ struct Q4KUnit {
 #pragma unroll
       for (int e = 0; e < 2; e++) {
         const uint32_t s = sh + 8u * e;
-        uint32_t sc, m;
-        if (high) {
-          sc = __builtin_amdgcn_ubfe(hdr[r].w, s, 4) | (__builtin_amdgcn_ubfe(hdr[r].y, s + 6, 2) << 4);
-          m = __builtin_amdgcn_ubfe(hdr[r].w, s + 4, 4) | (__builtin_amdgcn_ubfe(hdr[r].z, s + 6, 2) << 4);
-        } else {
-          sc = __builtin_amdgcn_ubfe(hdr[r].y, s, 6);
-          m = __builtin_amdgcn_ubfe(hdr[r].z, s, 6);
-        }
+        // One formula for both packings: the low four bits come from
+        // scales[j] / scales[j+4] (low groups) or scales[j+8] (high groups),
+        // the top two from bits 4-5 (low) or 6-7 (high) of scales[j] /
+        // scales[j+4].  Only a register is selected per lane, never a
+        // computation: a lane-divergent branch here makes the compiler hoist
+        // this row's scale work (and its wait for this row's loads) above
+        // earlier rows' dots.
+        const uint32_t sc = __builtin_amdgcn_ubfe(high ? hdr[r].w : hdr[r].y, s, 4) |
+                            (__builtin_amdgcn_ubfe(hdr[r].y, s + 4 + hs2, 2) << 4);
+        const uint32_t m = __builtin_amdgcn_ubfe(high ? hdr[r].w : hdr[r].z, s + 2 * hs2, 4) |
+                           (__builtin_amdgcn_ubfe(hdr[r].z, s + 4 + hs2, 2) << 4);
         dsc[r][e] = d * (float)sc;
         dmn[r][e] = dmin * (float)m;
       }

@@ -48,6 +48,10 @@ int hip_check(hipError_t e, const char* what);
 // ---- C-ABI layer in shim.cpp checks shapes before calling these) ----------
 int launch_dequant(hipStream_t s, int kind, const void* w, int64_t count, float* out);
 int launch_quantize(hipStream_t s, const float* x, int32_t cols, int32_t tokens, void* xq);
+// Batch-1 Q4_K matvec (matvec_rows.hip); launch_matvec routes there itself.
+bool q4k_rows_fits(int32_t cols);
+int launch_q4k_rows(hipStream_t s, const void* w, int64_t row_bytes, int32_t rows, int32_t cols, const void* xq,
+                    float* y, int32_t epi, const float* aux);
 int launch_matvec(hipStream_t s, int kind, const void* w, int64_t row_bytes, int32_t rows,
                   int32_t cols, const void* xq, int32_t tokens, float* y, int64_t ldy, int32_t epi,
                   const float* aux);
