@@ -20,6 +20,7 @@
 #include <algorithm>
 
 #include "mi_internal.h"
+#include "matvec_rows.h"
 
 namespace mi {
 int check_weight(const char* name, int kind, const void* w, int64_t row_bytes, int32_t rows, int32_t cols);
@@ -105,6 +106,8 @@ int mi_decoder_layer(mi_stream stream, const mi_layer_desc* d, float* resid, uin
   int rc = check_desc(d);
   if (rc) return rc;
   if (!resid || !k_cache || !v_cache || !pos) return fail(MI_ERR_ARG, "layer: null pointer");
+  if (((uintptr_t)k_cache | (uintptr_t)v_cache) & 15 || cache_stride % 8)
+    return fail(MI_ERR_ALIGN, "layer: caches must be 16-byte aligned with a stride of a multiple of 8 halves");
   if (tokens < 1 || tokens > kMaxTokens) return fail(MI_ERR_ARG, "layer: tokens %d outside 1..8", tokens);
   if (max_count <= 0) return fail(MI_ERR_SHAPE, "layer: max_count must be positive");
   const int64_t kvw = (int64_t)d->kv_heads * d->head_dim;
@@ -127,15 +130,33 @@ int mi_decoder_layer(mi_stream stream, const mi_layer_desc* d, float* resid, uin
 
   // attention_layer (block.mojo:319)
   if ((rc = launch_rms_norm(s, resid, d->attn_norm, d->width, tokens, d->eps, nullptr, xq))) return rc;
-  if ((rc = launch_matvec(s, d->wq.kind, d->wq.data, d->wq.row_bytes, qw, d->width, xq, tokens, qkv,
-                          qkv_stride, MI_EPI_NONE, nullptr)))
-    return rc;
-  if ((rc = launch_matvec(s, d->wk.kind, d->wk.data, d->wk.row_bytes, (int32_t)kvw, d->width, xq, tokens,
-                          qkv + qw, qkv_stride, MI_EPI_NONE, nullptr)))
-    return rc;
-  if ((rc = launch_matvec(s, d->wv.kind, d->wv.data, d->wv.row_bytes, (int32_t)kvw, d->width, xq, tokens,
-                          qkv + qw + kvw, qkv_stride, MI_EPI_NONE, nullptr)))
-    return rc;
+  const bool fused_qkv = tokens == 1 && d->wq.kind == MI_Q4_K && d->wk.kind == MI_Q4_K &&
+                         d->wv.kind == MI_Q4_K && q4k_rows_fits(d->width);
+  if (fused_qkv) {
+    // q, k and v in one launch, straight into the fused row
+    RowSegs sg{};
+    sg.w[0] = (const uint8_t*)d->wq.data;
+    sg.w[1] = (const uint8_t*)d->wk.data;
+    sg.w[2] = (const uint8_t*)d->wv.data;
+    sg.rb[0] = d->wq.row_bytes;
+    sg.rb[1] = d->wk.row_bytes;
+    sg.rb[2] = d->wv.row_bytes;
+    sg.end[0] = qw;
+    sg.end[1] = qw + (int32_t)kvw;
+    sg.end[2] = qw + 2 * (int32_t)kvw;
+    sg.nseg = 3;
+    if ((rc = launch_q4k_rows_segs(s, sg, d->width, xq, qkv))) return rc;
+  } else {
+    if ((rc = launch_matvec(s, d->wq.kind, d->wq.data, d->wq.row_bytes, qw, d->width, xq, tokens, qkv,
+                            qkv_stride, MI_EPI_NONE, nullptr)))
+      return rc;
+    if ((rc = launch_matvec(s, d->wk.kind, d->wk.data, d->wk.row_bytes, (int32_t)kvw, d->width, xq, tokens,
+                            qkv + qw, qkv_stride, MI_EPI_NONE, nullptr)))
+      return rc;
+    if ((rc = launch_matvec(s, d->wv.kind, d->wv.data, d->wv.row_bytes, (int32_t)kvw, d->width, xq, tokens,
+                            qkv + qw + kvw, qkv_stride, MI_EPI_NONE, nullptr)))
+      return rc;
+  }
   if ((rc = launch_rope_store(s, qkv, d->heads, d->kv_heads, d->head_dim, d->rope_dim, d->neox, d->rope_steps,
                               pos, tokens, qkv_stride, k_cache, v_cache, cache_stride)))
     return rc;
@@ -149,12 +170,20 @@ int mi_decoder_layer(mi_stream stream, const mi_layer_desc* d, float* resid, uin
 
   // mlp_layer (block.mojo:429), gated silu
   if ((rc = launch_rms_norm(s, resid, d->ffn_norm, d->width, tokens, d->eps, nullptr, xq))) return rc;
-  if ((rc = launch_matvec(s, d->up.kind, d->up.data, d->up.row_bytes, d->hidden, d->width, xq, tokens, up,
-                          d->hidden, MI_EPI_NONE, nullptr)))
-    return rc;
-  if ((rc = launch_matvec(s, d->gate.kind, d->gate.data, d->gate.row_bytes, d->hidden, d->width, xq, tokens,
-                          gate, d->hidden, MI_EPI_GLU, up)))
-    return rc;
+  if (tokens == 1 && d->gate.kind == MI_Q4_K && d->up.kind == MI_Q4_K && d->gate.row_bytes == d->up.row_bytes &&
+      q4k_rows_fits(d->width)) {
+    // gate and up in one launch, silu(gate) * up written directly
+    if ((rc = launch_q4k_glu(s, d->gate.data, d->up.data, d->gate.row_bytes, d->hidden, d->width, xq, gate,
+                             MI_EPI_NONE)))
+      return rc;
+  } else {
+    if ((rc = launch_matvec(s, d->up.kind, d->up.data, d->up.row_bytes, d->hidden, d->width, xq, tokens, up,
+                            d->hidden, MI_EPI_NONE, nullptr)))
+      return rc;
+    if ((rc = launch_matvec(s, d->gate.kind, d->gate.data, d->gate.row_bytes, d->hidden, d->width, xq, tokens,
+                            gate, d->hidden, MI_EPI_GLU, up)))
+      return rc;
+  }
   if ((rc = launch_quantize(s, gate, d->hidden, tokens, xq))) return rc;
   return launch_matvec(s, d->down.kind, d->down.data, d->down.row_bytes, d->width, d->hidden, xq, tokens,
                        resid, d->width, MI_EPI_ADD, nullptr);

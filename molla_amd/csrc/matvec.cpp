@@ -1,5 +1,6 @@
 // matvec.hip -- routes mi_matvec / mi_matvec_xq to the kernel for its kind
-// and batch: the batch-1 Q4_K kernel of matvec_rows.hip, else the general
+// and batch: the batch-1 Q4_K kernel of matvec_rows.hip, the batch-1 Q6_K
+// kernel of matvec_q6k_rows.hip, else the general
 // kernel of matvec_kernel.h, instantiated per kind in matvec_<kind>.hip.
 #include "mi_internal.h"
 
@@ -19,6 +20,8 @@ int launch_matvec(hipStream_t s, int kind, const void* w, int64_t row_bytes, int
                   const float* aux) {
   if (tokens == 1 && kind == MI_Q4_K && q4k_rows_fits(cols))
     return launch_q4k_rows(s, w, row_bytes, rows, cols, xq, y, epi, aux);
+  if (tokens == 1 && kind == MI_Q6_K && q6k_rows_fits(cols, row_bytes) && ((uintptr_t)w & 3) == 0)
+    return launch_q6k_rows(s, w, row_bytes, rows, cols, xq, y, epi, aux);
   switch (kind) {
     case MI_Q4_K: return launch_matvec_q4k(s, w, row_bytes, rows, cols, xq, tokens, y, ldy, epi, aux);
     case MI_Q6_K: return launch_matvec_q6k(s, w, row_bytes, rows, cols, xq, tokens, y, ldy, epi, aux);

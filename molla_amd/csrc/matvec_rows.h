@@ -1,0 +1,135 @@
+// matvec_rows.h -- the batch-1 Q4_K matvec kernel (the decode hot loop),
+// gfx950; launched from matvec_rows.hip.
+//
+// Same arithmetic as matvec_kernel<MI_Q4_K, R, 1> (matvec_units.h Q4KUnit),
+// organised for a single token, where the whole cost is streaming the
+// weights once:
+//
+//  * A wave owns RPW consecutive rows and one K-slice of at most 64 units
+//    (4096 values): lane l keeps the activation of unit u0 + l in registers
+//    for the whole wave (loaded once, before any weight), so the activation
+//    is never re-read per row.
+//  * All of the wave's weight loads are issued up front, straight-line; rows
+//    are then computed in order, each waiting only for its own loads (the
+//    compiler's vmcnt counts down row by row), so compute of one row overlaps
+//    the arrival of the next rows and of every other wave's data.
+//  * No LDS staging and few enough VGPRs that every wave of a 14336-row
+//    matrix is resident at once; single-wave blocks are handed out evenly
+//    over the CUs (multi-wave blocks left whole CUs with an extra block).
+//  * cols > 4096 splits K over KS waves of one block (the down projection,
+//    14336 = 4 x 3584); their partial sums meet in LDS and wave 0 adds them
+//    in a fixed order, so results do not depend on timing.
+//  * Rows may come from up to three matrices laid end to end in the output
+//    (q, k and v of a layer in one launch), and in GLU mode each wave takes
+//    the same rows of two matrices (gate, up) and writes act(gate) * up.
+//
+// Replaces the reference's planar_matvec_kernel (src/molla/nn/gpu.mojo:1533)
+// for Q4_K at batch 1; the epilogue is gpu.mojo:1005 write_epilogue.
+#pragma once
+
+#include "matvec_units.h"
+
+namespace mi {
+
+// Up to three row-major GGUF matrices of the same width whose rows are
+// numbered consecutively: rows [end[s-1], end[s]) come from w[s].
+struct RowSegs {
+  const uint8_t* w[3];
+  int64_t rb[3];
+  int32_t end[3];
+  int32_t nseg;
+};
+
+namespace rows {
+using namespace mv;
+
+// Activation of one lane's 64-value unit (groups 2u and 2u + 1).
+struct XUnitRegs {
+  uint4 l[2][3][2];
+  XMeta m[2];
+  __device__ __forceinline__ uint4 limb(int, int j, int hh, int g) const { return l[g & 1][j][hh]; }
+  __device__ __forceinline__ XMeta meta(int, int g) const { return m[g & 1]; }
+};
+
+// Row `row` of the segmented matrix: base address of its blocks.
+__device__ __forceinline__ const uint8_t* seg_row(const RowSegs& sg, int row) {
+  const int s = row < sg.end[0] ? 0 : (row < sg.end[1] ? 1 : 2);
+  const int start = s == 0 ? 0 : sg.end[s - 1];
+  return sg.w[s] + (int64_t)(row - start) * sg.rb[s];
+}
+
+// GLU: sg.w[0] = gate, sg.w[1] = up, both with sg.end[0] rows.
+template <int RPW, int KS, bool GLU>
+__global__ __launch_bounds__(KS * 64) void q4k_rows_kernel(const RowSegs sg, int cols,
+                                                           const uint8_t* __restrict__ xq,
+                                                           float* __restrict__ y, int epi,
+                                                           const float* __restrict__ aux) {
+  constexpr int NR = GLU ? 2 * RPW : RPW;
+  __shared__ float part[KS > 1 ? KS * NR : 1];
+  const int lane = threadIdx.x & 63;
+  const int ks = KS > 1 ? (threadIdx.x >> 6) : 0;
+  const int rows = GLU ? sg.end[0] : sg.end[sg.nseg - 1];
+  const int row0 = blockIdx.x * RPW;
+  const int units = cols >> 6;
+  const int u0 = ks * units / KS, u1 = (ks + 1) * units / KS;
+  const bool act = u0 + lane < u1;
+  const int u = act ? u0 + lane : u1 - 1;
+
+  XUnitRegs xr;
+  const XAcc xa{xq, 4 * (int64_t)cols, (int64_t)(cols >> 5) * 16};
+#pragma unroll
+  for (int e = 0; e < 2; e++) {
+#pragma unroll
+    for (int j = 0; j < 3; j++)
+#pragma unroll
+      for (int hh = 0; hh < 2; hh++) xr.l[e][j][hh] = xa.limb(0, j, hh, 2 * u + e);
+    xr.m[e] = xa.meta(0, 2 * u + e);
+  }
+  Q4KUnit<1> un[NR];
+#pragma unroll
+  for (int r = 0; r < NR; r++) {
+    const int row = min(row0 + (GLU ? r % RPW : r), rows - 1);
+    const uint8_t* base = GLU ? sg.w[r / RPW] + (int64_t)row * sg.rb[r / RPW] : seg_row(sg, row);
+    un[r].load(base, 0, 0, 0, u);
+  }
+
+  float acc[NR];
+#pragma unroll
+  for (int r = 0; r < NR; r++) {
+    float a[1][1] = {{0.0f}};
+    un[r].template compute<1>(xr, u, a);
+    acc[r] = act ? a[0][0] : 0.0f;
+    // keep row r's work ahead of row r+1's (and its wait for row r+1's loads)
+    __builtin_amdgcn_sched_barrier(0);
+  }
+#pragma unroll
+  for (int r = 0; r < NR; r++) acc[r] = wave_sum(acc[r]);
+
+  // lane r holds matrix-row r of this wave (GLU: r < RPW gate, r >= RPW up)
+  float v = acc[0];
+#pragma unroll
+  for (int r = 1; r < NR; r++)
+    if (lane == r) v = acc[r];
+  if constexpr (KS > 1) {
+    if (ks > 0 && lane < NR) part[ks * NR + lane] = v;
+    __syncthreads();
+    if (ks > 0) return;
+#pragma unroll
+    for (int k = 1; k < KS; k++)
+      if (lane < NR) v += part[k * NR + lane];
+  }
+  if constexpr (GLU) {
+    const float upv = __shfl_down(v, RPW);
+    if (lane < RPW && row0 + lane < rows) {
+      const float g = (epi & MI_ACT_GELU) ? gelu(v) : silu(v);
+      const float o = g * upv;
+      if (epi & MI_EPI_ADD) y[row0 + lane] += o;
+      else y[row0 + lane] = o;
+    }
+  } else {
+    if (lane < RPW && row0 + lane < rows) epilogue(y, aux, epi, row0 + lane, row0 + lane, v);
+  }
+}
+
+}  // namespace rows
+}  // namespace mi

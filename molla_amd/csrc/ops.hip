@@ -16,42 +16,55 @@ namespace {
 
 // ---- RMSNorm ---------------------------------------------------------------
 // kernel.mojo:432-467: float64 sum of squares, scale = f32(1/sqrt(sum/n+eps)),
-// out = x * scale * gain.  One block per token.
-constexpr int kNormThreads = 1024;
+// out = x * scale * gain.  A token's row is spread over `parts` blocks of
+// 256 threads.  Every block sums the whole row (16 KB for n = 4096, an L2
+// read) in the same order, so all blocks derive the identical scale with no
+// cross-block communication; each then normalises and quantizes only its
+// own 256-value slice.  Spreading the slices over CUs matters: the
+// fixed-point conversion is shuffle-heavy and one CU doing a whole row was
+// the slowest part.  All loads are issued before any arithmetic.
+constexpr int kNormThreads = 256;
 
+template <int PER>
 __global__ __launch_bounds__(kNormThreads) void rms_norm_kernel(const float* __restrict__ x,
                                                                 const float* __restrict__ gain, int n,
                                                                 float eps, float* __restrict__ out,
                                                                 uint8_t* __restrict__ xq) {
 #pragma clang fp contract(off)
-  const int t = blockIdx.x;
+  const int t = blockIdx.y;
   const float* xr = x + (int64_t)t * n;
+  const int mine = blockIdx.x * kNormThreads + threadIdx.x;
+  const bool live = mine < n;
+  float xv[PER];
+#pragma unroll
+  for (int k = 0; k < PER; k++) {
+    const int i = threadIdx.x + k * kNormThreads;
+    xv[k] = i < n ? xr[i] : 0.0f;
+  }
+  const float gm = live ? gain[mine] : 0.0f;
+  // this thread's own value is one it already loaded for the sum (a second
+  // load of it measured a microsecond slower)
+  float xm = xv[0];
+#pragma unroll
+  for (int k = 1; k < PER; k++)
+    if ((int)blockIdx.x == k) xm = xv[k];
   double acc = 0.0;
-  for (int i = threadIdx.x; i < n; i += kNormThreads) acc += (double)xr[i] * (double)xr[i];
+#pragma unroll
+  for (int k = 0; k < PER; k++) acc += (double)xv[k] * (double)xv[k];
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) acc += __shfl_xor(acc, m);
   __shared__ double part[kNormThreads / kWave];
-  __shared__ float scale_s;
   if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = acc;
   __syncthreads();
-  if (threadIdx.x == 0) {
-    double sum = 0.0;
-    for (int i = 0; i < kNormThreads / kWave; i++) sum += part[i];
-    scale_s = (float)(1.0 / sqrt(sum / (double)n + (double)eps));
-  }
-  __syncthreads();
-  const float scale = scale_s;
-  const int G = n >> 5;
-  uint8_t* xt = xq ? xq + (int64_t)t * xq_token_bytes(n) : nullptr;
-  for (int base = 0; base < n; base += kNormThreads) {
-    const int i = base + threadIdx.x;
-    const bool live = i < n;
-    const float v = live ? xr[i] * scale * gain[i] : 0.0f;
-    if (out && live) out[(int64_t)t * n + i] = v;
-    // A half-wave is one 32-value group; n is a multiple of 32, so a group is
-    // either entirely live or entirely past the end.
-    if (xt) quantize_group32(v, threadIdx.x & 31, i >> 5, G, xt, live);
-  }
+  double sum = 0.0;
+#pragma unroll
+  for (int i = 0; i < kNormThreads / kWave; i++) sum += part[i];
+  const float scale = (float)(1.0 / sqrt(sum / (double)n + (double)eps));
+  const float v = xm * scale * gm;
+  if (out && live) out[(int64_t)t * n + mine] = v;
+  // A half-wave is one 32-value group; n is a multiple of 32 whenever xq
+  // is asked for, so a group is either entirely live or entirely past the end.
+  if (xq) quantize_group32(v, threadIdx.x & 31, mine >> 5, n >> 5, xq + (int64_t)t * xq_token_bytes(n), live);
 }
 
 // ---- RoPE ------------------------------------------------------------------
@@ -86,27 +99,74 @@ __global__ void rope_kernel(float* __restrict__ x, int heads, int head_dim, int 
 
 // Rotate q and k of a fused [q | k | v] row in place, then store k and v as
 // halves at the token's slot (gpu_ops.mojo:1491, narrowing by a plain cast,
-// i.e. round to nearest even).
-__global__ void rope_store_kernel(float* __restrict__ qkv, int heads, int kv_heads, int head_dim,
-                                  int dim, int neox, const float* __restrict__ steps,
-                                  const int32_t* __restrict__ pos, int64_t row_stride,
-                                  __half* __restrict__ kc, __half* __restrict__ vc,
-                                  int64_t cache_stride) {
+// i.e. round to nearest even).  The angle depends only on (position, pair),
+// so the block computes each pair's cos/sin once, in float64 as the host
+// does, into LDS; meanwhile every thread's pairs of q/k are already being
+// loaded.  Rotation then runs from registers.
+constexpr int kRopeThreads = 512;
+constexpr int kRopePer = 8;  // pairs per thread held in registers per pass
+
+__global__ __launch_bounds__(kRopeThreads) void rope_store_kernel(
+    float* __restrict__ qkv, int heads, int kv_heads, int head_dim, int dim, int neox,
+    const float* __restrict__ steps, const int32_t* __restrict__ pos, int64_t row_stride,
+    __half* __restrict__ kc, __half* __restrict__ vc, int64_t cache_stride) {
+#pragma clang fp contract(off)
+  extern __shared__ float trig[];  // [pairs][2]
   const int t = blockIdx.x;
   const int pairs = dim >> 1;
   const int p = pos[t];
   float* row = qkv + (int64_t)t * row_stride;
-  for (int i = threadIdx.x; i < (heads + kv_heads) * pairs; i += blockDim.x)
-    rotate_pair(row, head_dim, dim, neox, steps, p, i / pairs, i % pairs);
-  __syncthreads();
   const int kvw = kv_heads * head_dim;
-  const float* k = row + (int64_t)heads * head_dim;
-  const float* v = k + kvw;
   __half* kd = kc + (int64_t)t * cache_stride + (int64_t)p * kvw;
   __half* vd = vc + (int64_t)t * cache_stride + (int64_t)p * kvw;
-  for (int i = threadIdx.x; i < kvw; i += blockDim.x) {
-    kd[i] = __float2half_rn(k[i]);
-    vd[i] = __float2half_rn(v[i]);
+  const int total = (heads + kv_heads) * pairs;
+  const int lo_step = neox ? 1 : 2, hi_off = neox ? pairs : 1;
+  for (int base = 0; base < total; base += kRopeThreads * kRopePer) {
+    float a[kRopePer], b[kRopePer];
+#pragma unroll
+    for (int k = 0; k < kRopePer; k++) {
+      const int i = base + threadIdx.x + k * kRopeThreads;
+      const int h = i / pairs, q = i - h * pairs;
+      const int64_t lo = (int64_t)h * head_dim + q * lo_step;
+      a[k] = i < total ? row[lo] : 0.0f;
+      b[k] = i < total ? row[lo + hi_off] : 0.0f;
+    }
+    if (base == 0) {
+      for (int q = threadIdx.x; q < pairs; q += kRopeThreads) {
+        const float theta = (float)p * steps[q];
+        trig[2 * q] = (float)cos((double)theta);
+        trig[2 * q + 1] = (float)sin((double)theta);
+      }
+      __syncthreads();
+    }
+#pragma unroll
+    for (int k = 0; k < kRopePer; k++) {
+      const int i = base + threadIdx.x + k * kRopeThreads;
+      if (i >= total) break;
+      const int h = i / pairs, q = i - h * pairs;
+      const float c = trig[2 * q], sn = trig[2 * q + 1];
+      const float ra = a[k] * c - b[k] * sn;
+      const float rb = a[k] * sn + b[k] * c;
+      const int64_t lo = (int64_t)h * head_dim + q * lo_step;
+      row[lo] = ra;
+      row[lo + hi_off] = rb;
+      if (h >= heads) {  // a key head: straight into the cache
+        const int64_t kl = lo - (int64_t)heads * head_dim;
+        kd[kl] = __float2half_rn(ra);
+        kd[kl + hi_off] = __float2half_rn(rb);
+      }
+    }
+  }
+  // values, and any key elements past the rotary dimension
+  const float* v = row + (int64_t)(heads + kv_heads) * head_dim;
+  for (int i = threadIdx.x; i < kvw; i += kRopeThreads) vd[i] = __float2half_rn(v[i]);
+  if (dim < head_dim) {
+    const float* k = row + (int64_t)heads * head_dim;
+    const int tail = head_dim - dim;
+    for (int i = threadIdx.x; i < kv_heads * tail; i += kRopeThreads) {
+      const int h = i / tail, e = dim + (i - h * tail);
+      kd[(int64_t)h * head_dim + e] = __float2half_rn(k[(int64_t)h * head_dim + e]);
+    }
   }
 }
 
@@ -123,123 +183,161 @@ __global__ void store_kv_kernel(const float* __restrict__ k, const float* __rest
 }
 
 // ---- attention -------------------------------------------------------------
-// attention.mojo:144 attend, split over slices of kChunk keys like
-// gpu_ops.mojo:929 attend_split_kernel: a block takes one key head, one
-// slice and every query head that reads that key head (GQA), so each key and
-// value is read once per slice.  It writes the slice's running maximum, its
-// sum of exponentials and the unnormalised weighted values; the merge folds
-// slices flash-style (gpu_ops.mojo:1104).
-constexpr int kChunk = 128;
+// attention.mojo:144 attend, split over slices of keys like gpu_ops.mojo:929
+// attend_split_kernel: a block takes one key head, one slice of keys and
+// every query head that reads that key head (GQA), so each cached key and
+// value is read once.  The slice's keys and values are staged into LDS with
+// all loads in flight at once; lane k of a wave scores key k for one query
+// head; the weighted sum of values reads them back from LDS.  Each slice
+// writes its running maximum, its sum of exponentials and its unnormalised
+// weighted values; the merge folds slices flash-style (gpu_ops.mojo:1104).
+constexpr int kAttnThreads = 256;
+
+// keys per slice: at most 64 (one per lane), fewer for wide heads so the
+// block's LDS stays within 64 KB for any group of up to 8 query heads
+__host__ __device__ __forceinline__ int attn_slice(int head_dim) {
+  return head_dim <= 128 ? 64 : (head_dim <= 256 ? 32 : 16);
+}
+__host__ __device__ __forceinline__ size_t attn_lds_bytes(int head_dim, int group) {
+  const int kk = attn_slice(head_dim);
+  return (size_t)kk * (head_dim + 8) * 2 + (size_t)kk * head_dim * 2 + (size_t)group * head_dim * 4 +
+         (size_t)group * kk * 4;
+}
 
 template <int GROUP>
-__global__ __launch_bounds__(kChunk) void attend_split_kernel(
+__global__ __launch_bounds__(kAttnThreads) void attend_split_kernel(
     const float* __restrict__ q, int64_t q_stride, const __half* __restrict__ kc,
     const __half* __restrict__ vc, int64_t cache_stride, int heads, int kv_heads, int head_dim,
     float scale, const int32_t* __restrict__ pos_dev, int count_host, int max_chunks,
     float* __restrict__ part_acc, float* __restrict__ part_ml) {
   const int c = blockIdx.x, kvh = blockIdx.y, t = blockIdx.z;
   const int count = pos_dev ? pos_dev[t] + 1 : count_host;  // a position p attends over p + 1 slots
-  const int start = c * kChunk;
+  const int kk = attn_slice(head_dim);
+  const int start = c * kk;
   if (start >= count) return;
-  const int tid = threadIdx.x;
-  const int kvw = kv_heads * head_dim;
-  extern __shared__ float smem[];
-  float* qs = smem;                      // [GROUP][head_dim]
-  float* ps = smem + GROUP * head_dim;   // [GROUP][kChunk]
-  __shared__ float red[GROUP][kChunk / kWave];
-  const float* qrow = q + (int64_t)t * q_stride + (int64_t)kvh * GROUP * head_dim;
-  for (int i = tid; i < GROUP * head_dim; i += kChunk) qs[i] = qrow[i];
+  const int D = head_dim, KS = head_dim + 8;  // LDS key rows padded by 16 bytes
+  const int nk = min(kk, count - start);
+  const int kvw = kv_heads * D;
+  extern __shared__ uint4 lds4[];
+  __half* Ks = (__half*)lds4;
+  __half* Vs = Ks + kk * KS;
+  float* Qs = (float*)(Vs + kk * D);
+  float* Ps = Qs + GROUP * D;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+
+  // stage keys, values (16-byte pieces; keys past the end repeat the last
+  // live one and are masked below) and the group's queries
+  const __half* kbase = kc + (int64_t)t * cache_stride + (int64_t)kvh * D;
+  const __half* vbase = vc + (int64_t)t * cache_stride + (int64_t)kvh * D;
+  const int pieces = D >> 3;
+  const int total = kk * pieces;
+  constexpr int kBatch = 4;
+  for (int b0 = 0; b0 < total; b0 += kAttnThreads * kBatch) {
+    uint4 kv[kBatch], vv[kBatch];
+#pragma unroll
+    for (int j = 0; j < kBatch; j++) {
+      const int i = b0 + tid + j * kAttnThreads;
+      const int key = min(i / pieces, nk - 1), pc = i % pieces;
+      const int64_t off = (int64_t)(start + key) * kvw + pc * 8;
+      if (i < total) {
+        kv[j] = *(const uint4*)(kbase + off);
+        vv[j] = *(const uint4*)(vbase + off);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < kBatch; j++) {
+      const int i = b0 + tid + j * kAttnThreads;
+      const int key = i / pieces, pc = i % pieces;
+      if (i < total) {
+        *(uint4*)(Ks + key * KS + pc * 8) = kv[j];
+        *(uint4*)(Vs + key * D + pc * 8) = vv[j];
+      }
+    }
+  }
+  const float4* q4 = (const float4*)(q + (int64_t)t * q_stride + (int64_t)kvh * GROUP * D);
+  for (int i = tid; i < GROUP * D / 4; i += kAttnThreads) ((float4*)Qs)[i] = q4[i];
   __syncthreads();
 
-  const __half* kbase = kc + (int64_t)t * cache_stride + (int64_t)kvh * head_dim;
-  const __half* vbase = vc + (int64_t)t * cache_stride + (int64_t)kvh * head_dim;
-  const int key = start + tid;
-  const bool live = key < count;
-  float s[GROUP];
-#pragma unroll
-  for (int g = 0; g < GROUP; g++) s[g] = 0.0f;
-  if (live) {
-    const __half* kr = kbase + (int64_t)key * kvw;
-    for (int d = 0; d < head_dim; d += 8) {
-      const uint4 raw = *(const uint4*)(kr + d);
-      const __half2* h2 = (const __half2*)&raw;
-      float kf[8];
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const float2 f = __half22float2(h2[i]);
-        kf[2 * i] = f.x;
-        kf[2 * i + 1] = f.y;
+  const int64_t slot_base = ((int64_t)t * heads + (int64_t)kvh * GROUP) * max_chunks + c;
+  // scores and slice softmax: wave w takes query heads w, w+4, ...; lane = key
+  for (int g = wave; g < GROUP; g += kAttnThreads / kWave) {
+    float sdot = 0.0f;
+    if (lane < kk) {
+      const __half* kr = Ks + lane * KS;
+      const float* qg = Qs + g * D;
+      for (int d = 0; d < D; d += 8) {
+        const uint4 raw = *(const uint4*)(kr + d);
+        const __half2* h2 = (const __half2*)&raw;
+        const float4 qa = *(const float4*)(qg + d), qb = *(const float4*)(qg + d + 4);
+        const float2 k0 = __half22float2(h2[0]), k1 = __half22float2(h2[1]);
+        const float2 k2 = __half22float2(h2[2]), k3 = __half22float2(h2[3]);
+        sdot = fmaf(qa.x, k0.x, sdot);
+        sdot = fmaf(qa.y, k0.y, sdot);
+        sdot = fmaf(qa.z, k1.x, sdot);
+        sdot = fmaf(qa.w, k1.y, sdot);
+        sdot = fmaf(qb.x, k2.x, sdot);
+        sdot = fmaf(qb.y, k2.y, sdot);
+        sdot = fmaf(qb.z, k3.x, sdot);
+        sdot = fmaf(qb.w, k3.y, sdot);
       }
-#pragma unroll
-      for (int g = 0; g < GROUP; g++)
-#pragma unroll
-        for (int i = 0; i < 8; i++) s[g] = fmaf(qs[g * head_dim + d + i], kf[i], s[g]);
     }
-  }
-  // slice maximum per head
-  float mx[GROUP];
-#pragma unroll
-  for (int g = 0; g < GROUP; g++) {
-    s[g] = live ? s[g] * scale : -INFINITY;
-    float m = s[g];
+    const bool live = lane < nk;
+    const float sc = live ? sdot * scale : -INFINITY;
+    float m = sc;
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
-    if ((tid & 63) == 0) red[g][tid >> 6] = m;
-  }
-  __syncthreads();
-#pragma unroll
-  for (int g = 0; g < GROUP; g++) {
-    float m = red[g][0];
-    for (int i = 1; i < kChunk / kWave; i++) m = fmaxf(m, red[g][i]);
-    mx[g] = m;
-  }
-  __syncthreads();
-#pragma unroll
-  for (int g = 0; g < GROUP; g++) {
-    const float p = live ? expf(s[g] - mx[g]) : 0.0f;
-    ps[g * kChunk + tid] = p;
-    float l = p;
+    const float pr = live ? expf(sc - m) : 0.0f;
+    float l = pr;
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) l += __shfl_xor(l, o);
-    if ((tid & 63) == 0) red[g][tid >> 6] = l;
+    if (lane < kk) Ps[g * kk + lane] = pr;
+    if (lane == 0) {
+      part_ml[(slot_base + (int64_t)g * max_chunks) * 2 + 0] = m;
+      part_ml[(slot_base + (int64_t)g * max_chunks) * 2 + 1] = l;
+    }
   }
   __syncthreads();
-  const int nkeys = min(kChunk, count - start);
-  const int64_t slot_base = ((int64_t)t * heads + (int64_t)kvh * GROUP) * max_chunks + c;
-  for (int d = tid; d < head_dim; d += kChunk) {
-    float acc[GROUP];
-#pragma unroll
-    for (int g = 0; g < GROUP; g++) acc[g] = 0.0f;
-    for (int k = 0; k < nkeys; k++) {
-      const float vv = __half2float(vbase[(int64_t)(start + k) * kvw + d]);
-#pragma unroll
-      for (int g = 0; g < GROUP; g++) acc[g] = fmaf(ps[g * kChunk + k], vv, acc[g]);
+  // unnormalised weighted values: thread o takes query head g, dims 2e, 2e+1
+  const int halfD = D >> 1;
+  for (int o = tid; o < GROUP * halfD; o += kAttnThreads) {
+    const int g = o / halfD, e = o - g * halfD;
+    const float* pg = Ps + g * kk;
+    float a0 = 0.0f, a1 = 0.0f;
+    for (int k = 0; k < nk; k++) {
+      const float2 v = __half22float2(*(const __half2*)(Vs + k * D + 2 * e));
+      const float pk = pg[k];
+      a0 = fmaf(pk, v.x, a0);
+      a1 = fmaf(pk, v.y, a1);
     }
-#pragma unroll
-    for (int g = 0; g < GROUP; g++)
-      part_acc[(slot_base + (int64_t)g * max_chunks) * head_dim + d] = acc[g];
-  }
-  if (tid < GROUP) {
-    float l = 0.0f;
-    for (int i = 0; i < kChunk / kWave; i++) l += red[tid][i];
-    part_ml[(slot_base + (int64_t)tid * max_chunks) * 2 + 0] = mx[tid];
-    part_ml[(slot_base + (int64_t)tid * max_chunks) * 2 + 1] = l;
+    *(float2*)(part_acc + (slot_base + (int64_t)g * max_chunks) * D + 2 * e) = make_float2(a0, a1);
   }
 }
 
-// One block per (query head, token); thread d owns output dimension d.
+// One block per (query head, token); thread d owns output dimension d.  All
+// slices' (max, sum) pairs are loaded at once into LDS, each wave reduces
+// them (identically), then the weighted values are folded in slice order.
 __global__ void attend_merge_kernel(const float* __restrict__ part_acc, const float* __restrict__ part_ml,
                                     int heads, int head_dim, const int32_t* __restrict__ pos_dev,
                                     int count_host, int max_chunks, float* __restrict__ out,
                                     uint8_t* __restrict__ xq) {
+  extern __shared__ float mls[];  // [max_chunks][2]
   const int h = blockIdx.x, t = blockIdx.y;
   const int count = pos_dev ? pos_dev[t] + 1 : count_host;  // a position p attends over p + 1 slots
-  const int chunks = (count + kChunk - 1) / kChunk;
+  const int kk = attn_slice(head_dim);
+  const int chunks = (count + kk - 1) / kk;
   const int64_t slot = ((int64_t)t * heads + h) * max_chunks;
+  for (int c = threadIdx.x; c < chunks; c += blockDim.x)
+    *(float2*)(mls + 2 * c) = *(const float2*)(part_ml + (slot + c) * 2);
+  __syncthreads();
+  const int lane = threadIdx.x & 63;
   float M = -INFINITY;
-  for (int c = 0; c < chunks; c++) M = fmaxf(M, part_ml[(slot + c) * 2]);
+  for (int c = lane; c < chunks; c += kWave) M = fmaxf(M, mls[2 * c]);
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) M = fmaxf(M, __shfl_xor(M, o));
   float L = 0.0f;
-  for (int c = 0; c < chunks; c++) L += part_ml[(slot + c) * 2 + 1] * expf(part_ml[(slot + c) * 2] - M);
+  for (int c = lane; c < chunks; c += kWave) L += mls[2 * c + 1] * expf(mls[2 * c] - M);
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) L += __shfl_xor(L, o);
   const float inv = 1.0f / L;
   const int width = heads * head_dim;
   for (int base = 0; base < head_dim; base += blockDim.x) {
@@ -247,8 +345,16 @@ __global__ void attend_merge_kernel(const float* __restrict__ part_acc, const fl
     const bool live = d < head_dim;
     float o = 0.0f;
     if (live) {
-      for (int c = 0; c < chunks; c++)
-        o = fmaf(part_acc[(slot + c) * head_dim + d], expf(part_ml[(slot + c) * 2] - M), o);
+      const float* pa = part_acc + slot * head_dim + d;
+      int c = 0;
+      for (; c + 8 <= chunks; c += 8) {
+        float a[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) a[j] = pa[(int64_t)(c + j) * head_dim];
+#pragma unroll
+        for (int j = 0; j < 8; j++) o = fmaf(a[j], expf(mls[2 * (c + j)] - M), o);
+      }
+      for (; c < chunks; c++) o = fmaf(pa[(int64_t)c * head_dim], expf(mls[2 * c] - M), o);
       o *= inv;
       if (out) out[(int64_t)t * width + (int64_t)h * head_dim + d] = o;
     }
@@ -267,13 +373,8 @@ __device__ __forceinline__ void better(float& v, int& i, float ov, int oi) {
   }
 }
 
-__global__ __launch_bounds__(1024) void argmax_kernel(const float* __restrict__ x, int n,
-                                                      int32_t* __restrict__ out) {
-  const int t = blockIdx.x;
-  const float* xr = x + (int64_t)t * n;
-  float bv = -INFINITY;
-  int bi = n;  // sentinel: beaten by any real element
-  for (int i = threadIdx.x; i < n; i += blockDim.x) better(bv, bi, xr[i], i);
+// Reduce (value, index) over the block; thread 0 writes the winner.
+__device__ __forceinline__ void argmax_finish(float bv, int bi, int n, int32_t* __restrict__ out) {
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) {
     const float ov = __shfl_xor(bv, o);
@@ -289,8 +390,49 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const float* __restrict__ 
   __syncthreads();
   if (threadIdx.x == 0) {
     for (int w = 1; w < (int)(blockDim.x >> 6); w++) better(bv, bi, sv[w], si[w]);
-    out[t] = bi < n ? bi : 0;
+    *out = bi < n ? bi : 0;
   }
+}
+
+// Rows of any length: strided scalar loop.
+__global__ __launch_bounds__(1024) void argmax_kernel(const float* __restrict__ x, int n,
+                                                      int32_t* __restrict__ out) {
+  const int t = blockIdx.x;
+  const float* xr = x + (int64_t)t * n;
+  float bv = -INFINITY;
+  int bi = n;  // sentinel: beaten by any real element
+  for (int i = threadIdx.x; i < n; i += blockDim.x) better(bv, bi, xr[i], i);
+  argmax_finish(bv, bi, n, out + t);
+}
+
+// Rows of a multiple of 4 floats, 16-byte aligned: each thread issues all of
+// its PER float4 loads before comparing any, so the row costs one memory
+// latency (a vocabulary of 128256 is 32 loads per thread).
+template <int PER>
+__global__ __launch_bounds__(1024) void argmax4_kernel(const float* __restrict__ x, int n,
+                                                       int32_t* __restrict__ out) {
+  const int t = blockIdx.x;
+  const float4* xr = (const float4*)(x + (int64_t)t * n);
+  const int n4 = n >> 2;
+  float4 v[PER];
+#pragma unroll
+  for (int k = 0; k < PER; k++) {
+    const int j = threadIdx.x + k * 1024;
+    v[k] = j < n4 ? xr[j] : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+  }
+  float bv = -INFINITY;
+  int bi = n;
+#pragma unroll
+  for (int k = 0; k < PER; k++) {
+    const int i = 4 * (threadIdx.x + k * 1024);
+    if (i < n) {
+      better(bv, bi, v[k].x, i);
+      better(bv, bi, v[k].y, i + 1);
+      better(bv, bi, v[k].z, i + 2);
+      better(bv, bi, v[k].w, i + 3);
+    }
+  }
+  argmax_finish(bv, bi, n, out + t);
 }
 
 // ---- embedding -------------------------------------------------------------
@@ -310,8 +452,17 @@ __global__ void embed_kernel(const float* __restrict__ emb, int vocab, int width
 
 int launch_rms_norm(hipStream_t s, const float* x, const float* gain, int32_t n, int32_t tokens,
                     float eps, float* out, void* xq) {
-  hipLaunchKernelGGL(rms_norm_kernel, dim3(tokens), dim3(kNormThreads), 0, s, x, gain, n, eps, out,
-                     (uint8_t*)xq);
+  const int per = (n + kNormThreads - 1) / kNormThreads;
+  dim3 grid(per, tokens);
+#define MI_NORM(P) \
+  hipLaunchKernelGGL(rms_norm_kernel<P>, grid, dim3(kNormThreads), 0, s, x, gain, n, eps, out, (uint8_t*)xq)
+  if (per <= 4) MI_NORM(4);
+  else if (per <= 8) MI_NORM(8);
+  else if (per <= 16) MI_NORM(16);
+  else if (per <= 32) MI_NORM(32);
+  else if (per <= 64) MI_NORM(64);
+  else return fail(MI_ERR_SHAPE, "rms_norm: %d values per row is more than %d", n, 64 * kNormThreads);
+#undef MI_NORM
   return hip_check(hipGetLastError(), "rms_norm launch");
 }
 
@@ -326,9 +477,9 @@ int launch_rope_store(hipStream_t s, float* qkv, int32_t heads, int32_t kv_heads
                       int32_t dim, int32_t neox, const float* steps, const int32_t* pos,
                       int32_t tokens, int64_t row_stride, uint16_t* k_cache, uint16_t* v_cache,
                       int64_t cache_stride) {
-  hipLaunchKernelGGL(rope_store_kernel, dim3(tokens), dim3(512), 0, s, qkv, heads, kv_heads, head_dim,
-                     dim, neox, steps, pos, row_stride, (__half*)k_cache, (__half*)v_cache,
-                     cache_stride);
+  hipLaunchKernelGGL(rope_store_kernel, dim3(tokens), dim3(kRopeThreads), (size_t)dim * sizeof(float), s, qkv,
+                     heads, kv_heads, head_dim, dim, neox, steps, pos, row_stride, (__half*)k_cache,
+                     (__half*)v_cache, cache_stride);
   return hip_check(hipGetLastError(), "rope_store launch");
 }
 
@@ -342,7 +493,8 @@ int launch_store_kv(hipStream_t s, const float* k, const float* v, int32_t kv_wi
 }
 
 size_t attend_workspace(int32_t heads, int32_t head_dim, int32_t max_count, int32_t tokens) {
-  const int64_t chunks = (max_count + kChunk - 1) / kChunk;
+  const int kk = attn_slice(head_dim);
+  const int64_t chunks = (max_count + kk - 1) / kk;
   const int64_t slots = (int64_t)tokens * heads * chunks;
   const size_t acc = (size_t)slots * head_dim * sizeof(float);
   return ((acc + 255) & ~(size_t)255) + (size_t)slots * 2 * sizeof(float);
@@ -352,18 +504,19 @@ int launch_attend(hipStream_t s, const float* q, int64_t q_stride, const uint16_
                   const uint16_t* v_cache, int64_t cache_stride, int32_t heads, int32_t kv_heads,
                   int32_t head_dim, float scale, const int32_t* pos_dev, int32_t count_host,
                   int32_t max_count, int32_t tokens, float* out, void* xq_out, void* work) {
-  const int chunks = (max_count + kChunk - 1) / kChunk;
+  const int kk = attn_slice(head_dim);
+  const int chunks = (max_count + kk - 1) / kk;
   const int64_t slots = (int64_t)tokens * heads * chunks;
   float* part_acc = (float*)work;
   const size_t acc_bytes = ((size_t)slots * head_dim * sizeof(float) + 255) & ~(size_t)255;
   float* part_ml = (float*)((char*)work + acc_bytes);
   const int group = heads / kv_heads;
-  const size_t shmem = (size_t)group * (head_dim + kChunk) * sizeof(float);
+  const size_t shmem = attn_lds_bytes(head_dim, group);
   dim3 grid(chunks, kv_heads, tokens);
   const __half* kc = (const __half*)k_cache;
   const __half* vc = (const __half*)v_cache;
 #define MI_ATTEND(G)                                                                                  \
-  hipLaunchKernelGGL(attend_split_kernel<G>, grid, dim3(kChunk), shmem, s, q, q_stride, kc, vc,         \
+  hipLaunchKernelGGL(attend_split_kernel<G>, grid, dim3(kAttnThreads), shmem, s, q, q_stride, kc, vc,   \
                      cache_stride, heads, kv_heads, head_dim, scale, pos_dev, count_host, chunks,     \
                      part_acc, part_ml)
   switch (group) {
@@ -376,13 +529,24 @@ int launch_attend(hipStream_t s, const float* q, int64_t q_stride, const uint16_
 #undef MI_ATTEND
   int rc = hip_check(hipGetLastError(), "attend_split launch");
   if (rc) return rc;
-  hipLaunchKernelGGL(attend_merge_kernel, dim3(heads, tokens), dim3(head_dim < 64 ? 64 : head_dim), 0, s,
-                     part_acc, part_ml, heads, head_dim, pos_dev, count_host, chunks, out,
-                     (uint8_t*)xq_out);
+  hipLaunchKernelGGL(attend_merge_kernel, dim3(heads, tokens), dim3(head_dim < 64 ? 64 : head_dim),
+                     (size_t)chunks * 2 * sizeof(float), s, part_acc, part_ml, heads, head_dim, pos_dev,
+                     count_host, chunks, out, (uint8_t*)xq_out);
   return hip_check(hipGetLastError(), "attend_merge launch");
 }
 
 int launch_argmax(hipStream_t s, const float* x, int32_t n, int32_t tokens, int32_t* out) {
+  const int per = (n / 4 + 1023) / 1024;
+  if (n % 4 == 0 && ((uintptr_t)x & 15) == 0 && per <= 32) {
+#define MI_ARGMAX(P) hipLaunchKernelGGL(argmax4_kernel<P>, dim3(tokens), dim3(1024), 0, s, x, n, out)
+    if (per <= 1) MI_ARGMAX(1);
+    else if (per <= 4) MI_ARGMAX(4);
+    else if (per <= 8) MI_ARGMAX(8);
+    else if (per <= 16) MI_ARGMAX(16);
+    else MI_ARGMAX(32);
+#undef MI_ARGMAX
+    return hip_check(hipGetLastError(), "argmax launch");
+  }
   hipLaunchKernelGGL(argmax_kernel, dim3(tokens), dim3(1024), 0, s, x, n, out);
   return hip_check(hipGetLastError(), "argmax launch");
 }

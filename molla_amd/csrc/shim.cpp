@@ -210,6 +210,8 @@ int mi_attend(mi_stream stream, const float* q, const uint16_t* k_cache, const u
   int rc = check_attn("attend", heads, kv_heads, head_dim);
   if (rc) return rc;
   if (count <= 0) return fail(MI_ERR_SHAPE, "attention needs at least one key to look at");
+  if (((uintptr_t)q | (uintptr_t)k_cache | (uintptr_t)v_cache) & 15)
+    return fail(MI_ERR_ALIGN, "attend: the query and the caches must be 16-byte aligned");
   if (!work || work_bytes < mi_attend_workspace(heads, head_dim, count))
     return fail(MI_ERR_WORKSPACE, "attend: workspace of %zu bytes, %zu needed", work_bytes,
                 mi_attend_workspace(heads, head_dim, count));
