@@ -43,9 +43,11 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--decode", action="store_true", help="also time the synthetic 8B decode step")
-    ap.add_argument("--decode-tokens", type=int, default=64)
+    ap.add_argument("--decode-tokens", type=int, default=256)
+    ap.add_argument("--decode-batch", type=int, nargs="+", default=[1, 4])
     ap.add_argument("--prompt", type=int, default=2048)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-batched", action="store_true", help="skip the batch-4/8 matrix-core tile lines")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}).",
@@ -125,18 +127,60 @@ def main():
                    "rows": ROWS, "cols": COLS, "tokens": 1, "weight_bytes": wbytes,
                    "algorithmic_bytes_per_step": algo, "parallelism": "single GPU"},
         "pct_of_hbm_peak": round(100 * value / PEAK_GBS, 1),
-        "roofline": {"bound": "hbm", "kernel": "matvec_kernel<Q4_K>",
+        "roofline": {"bound": "hbm", "kernel": "q4k_rows_kernel<4,1> (matvec_rows.h)",
                      "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / PEAK_GBS, 4), "traffic": _traffic_from_profile(),
                      "kernel_avg_us": round(k_avg_ms * 1e3, 3),
                      "kernel_min_us": round(k_ms[0] * 1e3, 3)},
     }
 
+    if not args.no_batched:
+        line["batched"] = _batched(L, h, kind, ws, copies, rb, stream)
     if not args.no_cpu:
         line["cpu_baseline"] = _cpu_baseline(base, kind, rb, x)
     if args.decode:
         line["decode"] = _decode(ctx, args)
     print(json.dumps(line), flush=True)
+
+
+def _batched(L, h, kind, ws, copies, rb, stream, reps=100):
+    """Batch 4 and 8: the same weights against 4 / 8
+    tokens on the matrix-core tile (matvec_tile.hip).  Weights are still read
+    once per launch, so GB/s is over the same algorithmic bytes (plus the
+    larger x and y); MFMA utilisation = useful int8 ops (2 rows cols tokens,
+    times the three activation limbs) over the 5.0 POP/s dense int8 peak."""
+    import torch
+
+    from molla_amd import synth
+    from molla_amd._lib import check
+
+    out = {}
+    for tokens in (4, 8):
+        x = synth.normal(tokens * COLS, 11 + tokens, device="cuda")
+        xq = torch.empty(L.mi_matvec_workspace(COLS, tokens), dtype=torch.uint8, device="cuda")
+        y = torch.empty(tokens * ROWS, dtype=torch.float32, device="cuda")
+        check(L.mi_quantize(h, x.data_ptr(), COLS, tokens, xq.data_ptr()))
+        for i in range(10):
+            check(L.mi_matvec_xq(h, kind, ws[i % copies].data_ptr(), rb, ROWS, COLS, xq.data_ptr(), tokens,
+                                 y.data_ptr(), 0, None))
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for i in range(reps):
+            check(L.mi_matvec_xq(h, kind, ws[i % copies].data_ptr(), rb, ROWS, COLS, xq.data_ptr(), tokens,
+                                 y.data_ptr(), 0, None))
+        e1.record(stream)
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / reps
+        algo = _algo_bytes(ROWS, COLS, tokens, ROWS * rb)
+        ops = 2.0 * ROWS * COLS * tokens * 3
+        out[f"tokens_{tokens}"] = {"kernel": "q4k_tile_kernel (v_mfma_i32_32x32x32_i8)", "us_per_launch": round(us, 3),
+                                   "GB_s": round(algo / us / 1e3, 1),
+                                   "frac_hbm_peak": round(algo / us / 1e3 / PEAK_GBS, 4),
+                                   "mfma_int8_TOPs": round(ops / us / 1e6, 2),
+                                   "mfma_util_of_5POPs": round(ops / us / 1e6 / 5000.0, 5)}
+    return out
 
 
 def _traffic_from_profile():
@@ -174,7 +218,11 @@ def _cpu_baseline(w_dev, kind, rb, x_dev):
 
 
 def _decode(ctx, args):
-    """Config 5: synthetic 8B (32 layers, Q4_K, Q6_K head, f32 embedding)."""
+    """Config 5: synthetic 8B (32 layers, Q4_K, Q6_K head, f32 embedding);
+    a prompt of uniform random ids fed one position per step (prefill as the
+    reference's session does it, engine/session.mojo:119), then greedy decode,
+    at each batch size asked for (independent sequences, one token each per
+    step).  Reported per batch: tokens/s over all sequences and ms per step."""
     import torch
 
     from molla_amd import block, gpu, synth
@@ -201,33 +249,38 @@ def _decode(ctx, args):
     head = gpu.Tensor.from_bytes(synth.quant_tensor(gpu.Q_Q6_K, vocab, spec.width, 79, device=dev), gpu.Q_Q6_K,
                                  spec.width, vocab)
     model = block.DeviceModel(spec, emb, layers, onorm, head)
-    ctxlen = args.prompt + args.decode_tokens + 1
-    sess = block.DeviceSession(ctx, model, batch=1, context=ctxlen)
-    prompt = synth.tokens(args.prompt, vocab, 5, device=dev)
-    sess.pos.zero_()
-    t0 = time.perf_counter()
-    for p in range(args.prompt):  # host-side prefill one token at a time (engine/session.mojo:119)
-        sess.ids.copy_(prompt[p:p + 1])
-        sess.step()
-        sess.pos.add_(1)
-    torch.cuda.synchronize()
-    prefill_s = time.perf_counter() - t0
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
-    sess.ids.copy_(sess.picks)
-    e0.record()
-    for _ in range(args.decode_tokens):
-        sess.step()
-        sess.advance()
-    e1.record()
-    torch.cuda.synchronize()
-    ms_tok = e0.elapsed_time(e1) / args.decode_tokens
     wb = model.weight_bytes()
-    return {"metric": "8B Q4_K decode tokens/sec at batch 1", "tokens_per_s": round(1000 / ms_tok, 2),
-            "ms_per_token": round(ms_tok, 3), "prompt": args.prompt, "generated": args.decode_tokens,
-            "weight_bytes_per_token": wb, "weight_stream_gbs": round(wb / (ms_tok * 1e-3) / 1e9, 1),
-            "frac_of_weight_roofline": round(wb / (ms_tok * 1e-3) / 1e9 / PEAK_GBS, 4),
-            "prefill_s": round(prefill_s, 2)}
+    out = {"metric": "8B Q4_K decode tokens/sec", "prompt": args.prompt, "generated": args.decode_tokens,
+           "weight_bytes_per_step": wb}
+    for batch in args.decode_batch:
+        ctxlen = args.prompt + args.decode_tokens + 1
+        sess = block.DeviceSession(ctx, model, batch=batch, context=ctxlen)
+        prompt = synth.tokens(args.prompt * batch, vocab, 5 + batch, device=dev).view(args.prompt, batch)
+        sess.pos.zero_()
+        t0 = time.perf_counter()
+        for p in range(args.prompt):
+            sess.ids.copy_(prompt[p])
+            sess.step()
+            sess.pos.add_(1)
+        torch.cuda.synchronize()
+        prefill_s = time.perf_counter() - t0
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        sess.ids.copy_(sess.picks)
+        e0.record()
+        for _ in range(args.decode_tokens):
+            sess.step()
+            sess.advance()
+        e1.record()
+        torch.cuda.synchronize()
+        ms_step = e0.elapsed_time(e1) / args.decode_tokens
+        gbs = wb / (ms_step * 1e-3) / 1e9
+        out[f"batch_{batch}"] = {"tokens_per_s": round(1000 * batch / ms_step, 2), "ms_per_step": round(ms_step, 3),
+                                 "weight_stream_gbs": round(gbs, 1), "frac_of_weight_roofline": round(gbs / PEAK_GBS, 4),
+                                 "prefill_s": round(prefill_s, 2)}
+        del sess
+        torch.cuda.empty_cache()
+    return out
 
 
 if __name__ == "__main__":
