@@ -1,7 +1,7 @@
 // matvec.hip -- routes mi_matvec / mi_matvec_xq to the kernel for its kind
 // and batch: the batch-1 Q4_K kernel of matvec_rows.hip, the batch-1 Q6_K
 // kernel of matvec_q6k_rows.hip, the batched Q4_K tile of matvec_tile.hip
-// (matrix cores), else the general
+// (matrix cores) and its Q6_K sibling in matvec_tile_q6k.hip, else the general
 // kernel of matvec_kernel.h, instantiated per kind in matvec_<kind>.hip.
 #include "mi_internal.h"
 
@@ -23,6 +23,8 @@ int launch_matvec(hipStream_t s, int kind, const void* w, int64_t row_bytes, int
     return launch_q4k_rows(s, w, row_bytes, rows, cols, xq, y, epi, aux);
   if (kind == MI_Q4_K && q4k_tile_fits(cols, tokens))
     return launch_q4k_tile(s, w, row_bytes, rows, cols, xq, tokens, y, ldy, epi, aux);
+  if (kind == MI_Q6_K && q6k_tile_fits(cols, row_bytes, tokens) && ((uintptr_t)w & 1) == 0)
+    return launch_q6k_tile(s, w, row_bytes, rows, cols, xq, tokens, y, ldy, epi, aux);
   if (tokens == 1 && kind == MI_Q6_K && q6k_rows_fits(cols, row_bytes) && ((uintptr_t)w & 3) == 0)
     return launch_q6k_rows(s, w, row_bytes, rows, cols, xq, y, epi, aux);
   switch (kind) {

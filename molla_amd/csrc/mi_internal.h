@@ -58,6 +58,10 @@ struct RowSegs;
 bool q4k_tile_fits(int32_t cols, int32_t tokens);
 int launch_q4k_tile(hipStream_t s, const void* w, int64_t row_bytes, int32_t rows, int32_t cols, const void* xq,
                     int32_t tokens, float* y, int64_t ldy, int32_t epi, const float* aux);
+// Batched (2..8 tokens) Q6_K matvec on the matrix cores (matvec_tile_q6k.hip).
+bool q6k_tile_fits(int32_t cols, int64_t row_bytes, int32_t tokens);
+int launch_q6k_tile(hipStream_t s, const void* w, int64_t row_bytes, int32_t rows, int32_t cols, const void* xq,
+                    int32_t tokens, float* y, int64_t ldy, int32_t epi, const float* aux);
 // Batch-1 Q6_K matvec for up to 4096 columns (matvec_q6k_rows.hip).
 bool q6k_rows_fits(int32_t cols, int64_t row_bytes);
 int launch_q6k_rows(hipStream_t s, const void* w, int64_t row_bytes, int32_t rows, int32_t cols, const void* xq,
