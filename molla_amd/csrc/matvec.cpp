@@ -1,5 +1,5 @@
 // matvec.hip -- routes mi_matvec / mi_matvec_xq to the kernel for its kind
-// and batch: the batch-1 Q4_K kernel of matvec_rows.hip, the batch-1 Q6_K
+// and batch: the batch-1 Q4_K / Q4_0 / Q8_0 kernel of matvec_rows.hip, the batch-1 Q6_K
 // kernel of matvec_q6k_rows.hip, the batched Q4_K tile of matvec_tile.hip
 // (matrix cores) and its Q6_K sibling in matvec_tile_q6k.hip, else the general
 // kernel of matvec_kernel.h, instantiated per kind in matvec_<kind>.hip.
@@ -19,8 +19,8 @@ int launch_matvec_q80(hipStream_t, const void*, int64_t, int32_t, int32_t, const
 int launch_matvec(hipStream_t s, int kind, const void* w, int64_t row_bytes, int32_t rows,
                   int32_t cols, const void* xq, int32_t tokens, float* y, int64_t ldy, int32_t epi,
                   const float* aux) {
-  if (tokens == 1 && kind == MI_Q4_K && q4k_rows_fits(cols))
-    return launch_q4k_rows(s, w, row_bytes, rows, cols, xq, y, epi, aux);
+  if (tokens == 1 && rows_fits(kind, cols))
+    return launch_rows(s, kind, w, row_bytes, rows, cols, xq, y, epi, aux);
   if (kind == MI_Q4_K && q4k_tile_fits(cols, tokens))
     return launch_q4k_tile(s, w, row_bytes, rows, cols, xq, tokens, y, ldy, epi, aux);
   if (kind == MI_Q6_K && q6k_tile_fits(cols, row_bytes, tokens) && ((uintptr_t)w & 1) == 0)

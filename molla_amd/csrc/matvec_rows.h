@@ -1,7 +1,8 @@
-// matvec_rows.h -- the batch-1 Q4_K matvec kernel (the decode hot loop),
-// gfx950; launched from matvec_rows.hip.
+// matvec_rows.h -- the batch-1 matvec kernel (the decode hot loop) for the
+// kinds with 64-value units: Q4_K, Q4_0, Q8_0; gfx950; launched from
+// matvec_rows.hip.
 //
-// Same arithmetic as matvec_kernel<MI_Q4_K, R, 1> (matvec_units.h Q4KUnit),
+// Same arithmetic as matvec_kernel<KIND, R, 1> (matvec_units.h units),
 // organised for a single token, where the whole cost is streaming the
 // weights once:
 //
@@ -24,7 +25,7 @@
 //    the same rows of two matrices (gate, up) and writes act(gate) * up.
 //
 // Replaces the reference's planar_matvec_kernel (src/molla/nn/gpu.mojo:1533)
-// for Q4_K at batch 1; the epilogue is gpu.mojo:1005 write_epilogue.
+// at batch 1; the epilogue is gpu.mojo:1005 write_epilogue.
 #pragma once
 
 #include "matvec_units.h"
@@ -43,12 +44,16 @@ struct RowSegs {
 namespace rows {
 using namespace mv;
 
-// Activation of one lane's 64-value unit (groups 2u and 2u + 1).
+// Activation of one lane's 64-value unit (groups 2u and 2u + 1); the
+// per-half limb sums of plane 7 only for the kinds with an offset (Q4_0).
+template <bool L23>
 struct XUnitRegs {
   uint4 l[2][3][2];
   XMeta m[2];
+  int2 s23[L23 ? 2 : 1];
   __device__ __forceinline__ uint4 limb(int, int j, int hh, int g) const { return l[g & 1][j][hh]; }
   __device__ __forceinline__ XMeta meta(int, int g) const { return m[g & 1]; }
+  __device__ __forceinline__ int2 lsum23(int, int g) const { return s23[L23 ? (g & 1) : 0]; }
 };
 
 // Row `row` of the segmented matrix: base address of its blocks.
@@ -58,9 +63,10 @@ __device__ __forceinline__ const uint8_t* seg_row(const RowSegs& sg, int row) {
   return sg.w[s] + (int64_t)(row - start) * sg.rb[s];
 }
 
-// GLU: sg.w[0] = gate, sg.w[1] = up, both with sg.end[0] rows.
-template <int RPW, int KS, bool GLU>
-__global__ __launch_bounds__(KS * 64) void q4k_rows_kernel(const RowSegs sg, int cols,
+// GLU: sg.w[0] = gate, sg.w[1] = up, both with sg.end[0] rows.  KIND is
+// any kind with 64-value units (Q4_K, Q4_0, Q8_0; matvec_units.h).
+template <int KIND, int RPW, int KS, bool GLU>
+__global__ __launch_bounds__(KS * 64) void rows_kernel(const RowSegs sg, int cols,
                                                            const uint8_t* __restrict__ xq,
                                                            float* __restrict__ y, int epi,
                                                            const float* __restrict__ aux) {
@@ -75,7 +81,8 @@ __global__ __launch_bounds__(KS * 64) void q4k_rows_kernel(const RowSegs sg, int
   const bool act = u0 + lane < u1;
   const int u = act ? u0 + lane : u1 - 1;
 
-  XUnitRegs xr;
+  constexpr bool kL23 = KIND == MI_Q4_0;
+  XUnitRegs<kL23> xr;
   const XAcc xa{xq, 4 * (int64_t)cols, (int64_t)(cols >> 5) * 16};
 #pragma unroll
   for (int e = 0; e < 2; e++) {
@@ -84,8 +91,9 @@ __global__ __launch_bounds__(KS * 64) void q4k_rows_kernel(const RowSegs sg, int
 #pragma unroll
       for (int hh = 0; hh < 2; hh++) xr.l[e][j][hh] = xa.limb(0, j, hh, 2 * u + e);
     xr.m[e] = xa.meta(0, 2 * u + e);
+    if constexpr (kL23) xr.s23[e] = xa.lsum23(0, 2 * u + e);
   }
-  Q4KUnit<1> un[NR];
+  typename UnitOf<KIND, 1>::type un[NR];
 #pragma unroll
   for (int r = 0; r < NR; r++) {
     const int row = min(row0 + (GLU ? r % RPW : r), rows - 1);

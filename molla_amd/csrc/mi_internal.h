@@ -48,12 +48,23 @@ int hip_check(hipError_t e, const char* what);
 // ---- C-ABI layer in shim.cpp checks shapes before calling these) ----------
 int launch_dequant(hipStream_t s, int kind, const void* w, int64_t count, float* out);
 int launch_quantize(hipStream_t s, const float* x, int32_t cols, int32_t tokens, void* xq);
-// Batch-1 Q4_K matvec (matvec_rows.hip); launch_matvec routes there itself.
-// _segs: rows of up to three matrices of width cols numbered end to end (a
-// layer's q, k, v into one fused row).  _glu: y = act(gate . x) * (up . x)
-// for the same rows of two matrices (act = silu, or gelu with MI_ACT_GELU;
-// MI_EPI_ADD adds into y).
+// Batch-1 Q4_K / Q4_0 / Q8_0 matvec (matvec_rows.hip); launch_matvec routes
+// there itself.  _segs: rows of up to three Q4_K matrices of width cols
+// numbered end to end (a layer's q, k, v into one fused row).  _glu:
+// y = act(gate . x) * (up . x) for the same rows of two Q4_K matrices
+// (act = silu, or gelu with MI_ACT_GELU; MI_EPI_ADD adds into y).
 struct RowSegs;
+bool rows_fits(int kind, int32_t cols);
+bool q4k_rows_fits(int32_t cols);
+int launch_rows(hipStream_t s, int kind, const void* w, int64_t row_bytes, int32_t rows, int32_t cols,
+                const void* xq, float* y, int32_t epi, const float* aux);
+int launch_q4k_rows_segs(hipStream_t s, const RowSegs& sg, int32_t cols, const void* xq, float* y);
+int launch_q4k_glu(hipStream_t s, const void* gate, const void* up, int64_t row_bytes, int32_t rows,
+                   int32_t cols, const void* xq, float* y, int32_t epi);
+// Batch-1 Q6_K matvec for up to 4096 columns (matvec_q6k_rows.hip).
+bool q6k_rows_fits(int32_t cols, int64_t row_bytes);
+int launch_q6k_rows(hipStream_t s, const void* w, int64_t row_bytes, int32_t rows, int32_t cols, const void* xq,
+                    float* y, int32_t epi, const float* aux);
 // Batched (2..8 tokens) Q4_K matvec on the matrix cores (matvec_tile.hip).
 bool q4k_tile_fits(int32_t cols, int32_t tokens);
 int launch_q4k_tile(hipStream_t s, const void* w, int64_t row_bytes, int32_t rows, int32_t cols, const void* xq,
@@ -62,16 +73,8 @@ int launch_q4k_tile(hipStream_t s, const void* w, int64_t row_bytes, int32_t row
 bool q6k_tile_fits(int32_t cols, int64_t row_bytes, int32_t tokens);
 int launch_q6k_tile(hipStream_t s, const void* w, int64_t row_bytes, int32_t rows, int32_t cols, const void* xq,
                     int32_t tokens, float* y, int64_t ldy, int32_t epi, const float* aux);
-// Batch-1 Q6_K matvec for up to 4096 columns (matvec_q6k_rows.hip).
-bool q6k_rows_fits(int32_t cols, int64_t row_bytes);
-int launch_q6k_rows(hipStream_t s, const void* w, int64_t row_bytes, int32_t rows, int32_t cols, const void* xq,
-                    float* y, int32_t epi, const float* aux);
-bool q4k_rows_fits(int32_t cols);
-int launch_q4k_rows(hipStream_t s, const void* w, int64_t row_bytes, int32_t rows, int32_t cols, const void* xq,
-                    float* y, int32_t epi, const float* aux);
-int launch_q4k_rows_segs(hipStream_t s, const RowSegs& sg, int32_t cols, const void* xq, float* y);
-int launch_q4k_glu(hipStream_t s, const void* gate, const void* up, int64_t row_bytes, int32_t rows,
-                   int32_t cols, const void* xq, float* y, int32_t epi);
+// Every kind and batch: routes to the kernels above or the general
+// matvec_kernel.h.
 int launch_matvec(hipStream_t s, int kind, const void* w, int64_t row_bytes, int32_t rows,
                   int32_t cols, const void* xq, int32_t tokens, float* y, int64_t ldy, int32_t epi,
                   const float* aux);
