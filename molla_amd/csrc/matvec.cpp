@@ -1,7 +1,8 @@
 // matvec.hip -- routes mi_matvec / mi_matvec_xq to the kernel for its kind
 // and batch: the batch-1 Q4_K / Q4_0 / Q8_0 kernel of matvec_rows.hip, the batch-1 Q6_K
 // kernel of matvec_q6k_rows.hip, the batched Q4_K tile of matvec_tile.hip
-// (matrix cores) and its Q6_K sibling in matvec_tile_q6k.hip, else the general
+// (matrix cores) and its Q6_K and Q4_0 / Q8_0 siblings (matvec_tile_q6k.hip,
+// matvec_tile_b32.hip), else the general
 // kernel of matvec_kernel.h, instantiated per kind in matvec_<kind>.hip.
 #include "mi_internal.h"
 
@@ -23,6 +24,8 @@ int launch_matvec(hipStream_t s, int kind, const void* w, int64_t row_bytes, int
     return launch_rows(s, kind, w, row_bytes, rows, cols, xq, y, epi, aux);
   if (kind == MI_Q4_K && q4k_tile_fits(cols, tokens))
     return launch_q4k_tile(s, w, row_bytes, rows, cols, xq, tokens, y, ldy, epi, aux);
+  if (b32_tile_fits(kind, cols, row_bytes, tokens) && ((uintptr_t)w & 15) == 0)
+    return launch_b32_tile(s, kind, w, row_bytes, rows, cols, xq, tokens, y, ldy, epi, aux);
   if (kind == MI_Q6_K && q6k_tile_fits(cols, row_bytes, tokens) && ((uintptr_t)w & 1) == 0)
     return launch_q6k_tile(s, w, row_bytes, rows, cols, xq, tokens, y, ldy, epi, aux);
   if (tokens == 1 && kind == MI_Q6_K && q6k_rows_fits(cols, row_bytes) && ((uintptr_t)w & 3) == 0)

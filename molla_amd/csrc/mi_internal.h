@@ -73,6 +73,11 @@ int launch_q4k_tile(hipStream_t s, const void* w, int64_t row_bytes, int32_t row
 bool q6k_tile_fits(int32_t cols, int64_t row_bytes, int32_t tokens);
 int launch_q6k_tile(hipStream_t s, const void* w, int64_t row_bytes, int32_t rows, int32_t cols, const void* xq,
                     int32_t tokens, float* y, int64_t ldy, int32_t epi, const float* aux);
+// Batched (2..8 tokens) Q4_0 / Q8_0 matvec on the matrix cores
+// (matvec_tile_b32.hip).
+bool b32_tile_fits(int kind, int32_t cols, int64_t row_bytes, int32_t tokens);
+int launch_b32_tile(hipStream_t s, int kind, const void* w, int64_t row_bytes, int32_t rows, int32_t cols,
+                    const void* xq, int32_t tokens, float* y, int64_t ldy, int32_t epi, const float* aux);
 // Every kind and batch: routes to the kernels above or the general
 // matvec_kernel.h.
 int launch_matvec(hipStream_t s, int kind, const void* w, int64_t row_bytes, int32_t rows,
