@@ -33,7 +33,7 @@ namespace {
 size_t up256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 struct Carve {
-  size_t xq, qkv, up, gate, attn, total;
+  size_t xq, qkv, up, gate, attn, trig, total;
 };
 
 Carve carve(const mi_layer_desc* d, int32_t max_count, int32_t tokens) {
@@ -51,6 +51,8 @@ Carve carve(const mi_layer_desc* d, int32_t max_count, int32_t tokens) {
   at += up256(sizeof(float) * (size_t)d->hidden * tokens);
   c.attn = at;
   at += up256(attend_workspace(d->heads, d->head_dim, max_count, tokens));
+  c.trig = at;
+  at += up256(sizeof(float) * (size_t)d->rope_dim);
   c.total = at;
   return c;
 }
@@ -129,12 +131,10 @@ int mi_decoder_layer(mi_stream stream, const mi_layer_desc* d, float* resid, uin
   const int64_t qkv_stride = qw + 2 * kvw;
 
   // attention_layer (block.mojo:319)
-  if ((rc = launch_rms_norm(s, resid, d->attn_norm, d->width, tokens, d->eps, nullptr, xq))) return rc;
   const bool fused_qkv = tokens == 1 && d->wq.kind == MI_Q4_K && d->wk.kind == MI_Q4_K &&
                          d->wv.kind == MI_Q4_K && q4k_rows_fits(d->width);
+  RowSegs sg{};
   if (fused_qkv) {
-    // q, k and v in one launch, straight into the fused row
-    RowSegs sg{};
     sg.w[0] = (const uint8_t*)d->wq.data;
     sg.w[1] = (const uint8_t*)d->wk.data;
     sg.w[2] = (const uint8_t*)d->wv.data;
@@ -145,21 +145,44 @@ int mi_decoder_layer(mi_stream stream, const mi_layer_desc* d, float* resid, uin
     sg.end[1] = qw + (int32_t)kvw;
     sg.end[2] = qw + 2 * (int32_t)kvw;
     sg.nseg = 3;
-    if ((rc = launch_q4k_rows_segs(s, sg, d->width, xq, qkv))) return rc;
+  }
+  if (fused_qkv && !d->neox && q4k_qkv_rope_fits(d->width, d->head_dim, d->rope_dim)) {
+    // norm (plus this position's rope table), then q|k|v with the rope and
+    // the cache store in its epilogue: no separate rope launch
+    float* trig = (float*)(base + c.trig);
+    if ((rc = launch_rms_norm_trig(s, resid, d->attn_norm, d->width, d->eps, xq, pos, d->rope_steps,
+                                   d->rope_dim / 2, trig)))
+      return rc;
+    QkvRope rp{};
+    rp.qw = qw;
+    rp.kvw = (int)kvw;
+    rp.head_dim = d->head_dim;
+    rp.rope_dim = d->rope_dim;
+    rp.trig = (const float2*)trig;
+    rp.pos = pos;
+    rp.k_cache = (__half*)k_cache;
+    rp.v_cache = (__half*)v_cache;
+    if ((rc = launch_q4k_qkv_rope(s, sg, d->width, xq, qkv, rp))) return rc;
   } else {
-    if ((rc = launch_matvec(s, d->wq.kind, d->wq.data, d->wq.row_bytes, qw, d->width, xq, tokens, qkv,
-                            qkv_stride, MI_EPI_NONE, nullptr)))
-      return rc;
-    if ((rc = launch_matvec(s, d->wk.kind, d->wk.data, d->wk.row_bytes, (int32_t)kvw, d->width, xq, tokens,
-                            qkv + qw, qkv_stride, MI_EPI_NONE, nullptr)))
-      return rc;
-    if ((rc = launch_matvec(s, d->wv.kind, d->wv.data, d->wv.row_bytes, (int32_t)kvw, d->width, xq, tokens,
-                            qkv + qw + kvw, qkv_stride, MI_EPI_NONE, nullptr)))
+    if ((rc = launch_rms_norm(s, resid, d->attn_norm, d->width, tokens, d->eps, nullptr, xq))) return rc;
+    if (fused_qkv) {
+      // q, k and v in one launch, straight into the fused row
+      if ((rc = launch_q4k_rows_segs(s, sg, d->width, xq, qkv))) return rc;
+    } else {
+      if ((rc = launch_matvec(s, d->wq.kind, d->wq.data, d->wq.row_bytes, qw, d->width, xq, tokens, qkv,
+                              qkv_stride, MI_EPI_NONE, nullptr)))
+        return rc;
+      if ((rc = launch_matvec(s, d->wk.kind, d->wk.data, d->wk.row_bytes, (int32_t)kvw, d->width, xq, tokens,
+                              qkv + qw, qkv_stride, MI_EPI_NONE, nullptr)))
+        return rc;
+      if ((rc = launch_matvec(s, d->wv.kind, d->wv.data, d->wv.row_bytes, (int32_t)kvw, d->width, xq, tokens,
+                              qkv + qw + kvw, qkv_stride, MI_EPI_NONE, nullptr)))
+        return rc;
+    }
+    if ((rc = launch_rope_store(s, qkv, d->heads, d->kv_heads, d->head_dim, d->rope_dim, d->neox,
+                                d->rope_steps, pos, tokens, qkv_stride, k_cache, v_cache, cache_stride)))
       return rc;
   }
-  if ((rc = launch_rope_store(s, qkv, d->heads, d->kv_heads, d->head_dim, d->rope_dim, d->neox, d->rope_steps,
-                              pos, tokens, qkv_stride, k_cache, v_cache, cache_stride)))
-    return rc;
   // count = pos + 1 per sequence: the attention kernels read pos and add one.
   if ((rc = launch_attend(s, qkv, qkv_stride, k_cache, v_cache, cache_stride, d->heads, d->kv_heads,
                           d->head_dim, d->attn_scale, pos, -1, max_count, tokens, nullptr, xq, attn)))

@@ -41,6 +41,19 @@ struct RowSegs {
   int32_t nseg;
 };
 
+// The q|k|v launch's epilogue for one decoding token (Llama pairing,
+// adjacent elements): rows [0, qw) are q, rotated and written to y; rows
+// [qw, qw + kvw) are k, rotated and stored as halves into k_cache at slot
+// pos[0]; rows [qw + kvw, qw + 2 kvw) are v, stored as halves into v_cache.
+// trig holds (cos, sin) of pos * step for each pair (rms_norm wrote it).
+struct QkvRope {
+  int qw, kvw, head_dim, rope_dim;
+  const float2* trig;
+  const int32_t* pos;
+  __half* k_cache;
+  __half* v_cache;
+};
+
 namespace rows {
 using namespace mv;
 
@@ -65,11 +78,12 @@ __device__ __forceinline__ const uint8_t* seg_row(const RowSegs& sg, int row) {
 
 // GLU: sg.w[0] = gate, sg.w[1] = up, both with sg.end[0] rows.  KIND is
 // any kind with 64-value units (Q4_K, Q4_0, Q8_0; matvec_units.h).
-template <int KIND, int RPW, int KS, bool GLU>
+// ROPE: the QkvRope epilogue instead of write_epilogue (RPW even).
+template <int KIND, int RPW, int KS, bool GLU, bool ROPE = false>
 __global__ __launch_bounds__(KS * 64) void rows_kernel(const RowSegs sg, int cols,
-                                                           const uint8_t* __restrict__ xq,
-                                                           float* __restrict__ y, int epi,
-                                                           const float* __restrict__ aux) {
+                                                       const uint8_t* __restrict__ xq,
+                                                       float* __restrict__ y, int epi,
+                                                       const float* __restrict__ aux, const QkvRope rp) {
   constexpr int NR = GLU ? 2 * RPW : RPW;
   __shared__ float part[KS > 1 ? KS * NR : 1];
   const int lane = threadIdx.x & 63;
@@ -126,7 +140,28 @@ __global__ __launch_bounds__(KS * 64) void rows_kernel(const RowSegs sg, int col
     for (int k = 1; k < KS; k++)
       if (lane < NR) v += part[k * NR + lane];
   }
-  if constexpr (GLU) {
+  if constexpr (ROPE) {
+    // rope.mojo:294 rotate_scaled, adjacent pairs: (a, b) <- (a c - b s, a s + b c)
+#pragma clang fp contract(off)
+    const int row = row0 + lane;
+    const float partner = __shfl_xor(v, 1);
+    if (lane < RPW && row < rows) {
+      const bool is_q = row < rp.qw, is_k = !is_q && row < rp.qw + rp.kvw;
+      float o = v;
+      if (is_q || is_k) {
+        const int e = (is_q ? row : row - rp.qw) % rp.head_dim;
+        if (e < rp.rope_dim) {
+          const float2 cs = rp.trig[e >> 1];
+          const float a = (e & 1) ? partner : v, b = (e & 1) ? v : partner;
+          o = (e & 1) ? a * cs.y + b * cs.x : a * cs.x - b * cs.y;
+        }
+      }
+      const int64_t slot = (int64_t)rp.pos[0] * rp.kvw;
+      if (is_q) y[row] = o;
+      else if (is_k) rp.k_cache[slot + (row - rp.qw)] = __float2half_rn(o);
+      else rp.v_cache[slot + (row - rp.qw - rp.kvw)] = __float2half_rn(o);
+    }
+  } else if constexpr (GLU) {
     const float upv = __shfl_down(v, RPW);
     if (lane < RPW && row0 + lane < rows) {
       const float g = (epi & MI_ACT_GELU) ? gelu(v) : silu(v);

@@ -7,12 +7,12 @@ namespace mi {
 namespace {
 using rows::rows_kernel;
 
-template <int KIND, int RPW, int KS, bool GLU>
+template <int KIND, int RPW, int KS, bool GLU, bool ROPE = false>
 int launch_rk(hipStream_t s, const RowSegs& sg, int rows, int cols, const void* xq, float* y, int epi,
-              const float* aux) {
+              const float* aux, const QkvRope& rp = QkvRope{}) {
   const int blocks = (rows + RPW - 1) / RPW;
-  hipLaunchKernelGGL((rows_kernel<KIND, RPW, KS, GLU>), dim3(blocks), dim3(KS * 64), 0, s, sg, cols,
-                     (const uint8_t*)xq, y, epi, aux);
+  hipLaunchKernelGGL((rows_kernel<KIND, RPW, KS, GLU, ROPE>), dim3(blocks), dim3(KS * 64), 0, s, sg, cols,
+                     (const uint8_t*)xq, y, epi, aux, rp);
   return hip_check(hipGetLastError(), "matvec launch");
 }
 
@@ -69,6 +69,19 @@ int launch_rows(hipStream_t s, int kind, const void* w, int64_t row_bytes, int32
 
 int launch_q4k_rows_segs(hipStream_t s, const RowSegs& sg, int32_t cols, const void* xq, float* y) {
   return launch_any<MI_Q4_K, false>(s, sg, sg.end[sg.nseg - 1], cols, xq, y, MI_EPI_NONE, nullptr);
+}
+
+bool q4k_qkv_rope_fits(int32_t cols, int32_t head_dim, int32_t rope_dim) {
+  return q4k_rows_fits(cols) && cols <= 4096 && head_dim % 4 == 0 && rope_dim % 2 == 0;
+}
+
+int launch_q4k_qkv_rope(hipStream_t s, const RowSegs& sg, int32_t cols, const void* xq, float* q,
+                        const QkvRope& rp) {
+  const int rows = sg.end[sg.nseg - 1];
+  if (!q4k_qkv_rope_fits(cols, rp.head_dim, rp.rope_dim))
+    return fail(MI_ERR_SHAPE, "matvec: no fused rope for %d columns, head_dim %d", cols, rp.head_dim);
+  // four rows per wave: pairs never straddle a wave (head_dim is even)
+  return launch_rk<MI_Q4_K, 4, 1, false, true>(s, sg, rows, cols, xq, q, MI_EPI_NONE, nullptr, rp);
 }
 
 int launch_q4k_glu(hipStream_t s, const void* gate, const void* up, int64_t row_bytes, int32_t rows,

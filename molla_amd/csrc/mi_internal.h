@@ -59,6 +59,13 @@ bool q4k_rows_fits(int32_t cols);
 int launch_rows(hipStream_t s, int kind, const void* w, int64_t row_bytes, int32_t rows, int32_t cols,
                 const void* xq, float* y, int32_t epi, const float* aux);
 int launch_q4k_rows_segs(hipStream_t s, const RowSegs& sg, int32_t cols, const void* xq, float* y);
+// The same q|k|v launch for one token with the rope and the cache store in
+// its epilogue (QkvRope in matvec_rows.h): q rotated into `q`, k rotated and
+// v into the f16 caches at slot pos[0].  Adjacent-pair (Llama) rope only.
+struct QkvRope;
+bool q4k_qkv_rope_fits(int32_t cols, int32_t head_dim, int32_t rope_dim);
+int launch_q4k_qkv_rope(hipStream_t s, const RowSegs& sg, int32_t cols, const void* xq, float* q,
+                        const QkvRope& rp);
 int launch_q4k_glu(hipStream_t s, const void* gate, const void* up, int64_t row_bytes, int32_t rows,
                    int32_t cols, const void* xq, float* y, int32_t epi);
 // Batch-1 Q6_K matvec for up to 4096 columns (matvec_q6k_rows.hip).
@@ -83,6 +90,11 @@ int launch_b32_tile(hipStream_t s, int kind, const void* w, int64_t row_bytes, i
 int launch_matvec(hipStream_t s, int kind, const void* w, int64_t row_bytes, int32_t rows,
                   int32_t cols, const void* xq, int32_t tokens, float* y, int64_t ldy, int32_t epi,
                   const float* aux);
+// rms_norm_trig: also writes trig[p] = (cos, sin) of f32(pos[0]) * steps[p]
+// for p < pairs (float64 trig, as rope.mojo:253-285), for the fused q|k|v
+// epilogue of the same layer.
+int launch_rms_norm_trig(hipStream_t s, const float* x, const float* gain, int32_t n, float eps, void* xq,
+                         const int32_t* pos, const float* steps, int32_t pairs, float* trig);
 int launch_rms_norm(hipStream_t s, const float* x, const float* gain, int32_t n, int32_t tokens,
                     float eps, float* out, void* xq);
 int launch_rope(hipStream_t s, float* x, int32_t heads, int32_t head_dim, int32_t dim, int32_t neox,

@@ -25,13 +25,25 @@ namespace {
 // the slowest part.  All loads are issued before any arithmetic.
 constexpr int kNormThreads = 256;
 
+// With `trig`, the last block also writes (cos, sin) of f32(pos[0]) * steps[p]
+// for p < pairs, in float64 as rope.mojo:253-285, for the layer's fused q|k|v
+// rope; it has no other use for its spare threads' time.
 template <int PER>
 __global__ __launch_bounds__(kNormThreads) void rms_norm_kernel(const float* __restrict__ x,
                                                                 const float* __restrict__ gain, int n,
                                                                 float eps, float* __restrict__ out,
-                                                                uint8_t* __restrict__ xq) {
+                                                                uint8_t* __restrict__ xq,
+                                                                const int32_t* __restrict__ pos,
+                                                                const float* __restrict__ steps, int pairs,
+                                                                float2* __restrict__ trig) {
 #pragma clang fp contract(off)
   const int t = blockIdx.y;
+  if (trig && blockIdx.x == gridDim.x - 1) {
+    for (int p = threadIdx.x; p < pairs; p += kNormThreads) {
+      const float theta = (float)pos[0] * steps[p];
+      trig[p] = make_float2((float)cos((double)theta), (float)sin((double)theta));
+    }
+  }
   const float* xr = x + (int64_t)t * n;
   const int mine = blockIdx.x * kNormThreads + threadIdx.x;
   const bool live = mine < n;
@@ -450,12 +462,13 @@ __global__ void embed_kernel(const float* __restrict__ emb, int vocab, int width
 
 }  // namespace
 
-int launch_rms_norm(hipStream_t s, const float* x, const float* gain, int32_t n, int32_t tokens,
-                    float eps, float* out, void* xq) {
+static int norm_launch(hipStream_t s, const float* x, const float* gain, int32_t n, int32_t tokens, float eps,
+                       float* out, void* xq, const int32_t* pos, const float* steps, int32_t pairs, float* trig) {
   const int per = (n + kNormThreads - 1) / kNormThreads;
   dim3 grid(per, tokens);
-#define MI_NORM(P) \
-  hipLaunchKernelGGL(rms_norm_kernel<P>, grid, dim3(kNormThreads), 0, s, x, gain, n, eps, out, (uint8_t*)xq)
+#define MI_NORM(P)                                                                                      \
+  hipLaunchKernelGGL(rms_norm_kernel<P>, grid, dim3(kNormThreads), 0, s, x, gain, n, eps, out, (uint8_t*)xq, \
+                     pos, steps, pairs, (float2*)trig)
   if (per <= 4) MI_NORM(4);
   else if (per <= 8) MI_NORM(8);
   else if (per <= 16) MI_NORM(16);
@@ -464,6 +477,16 @@ int launch_rms_norm(hipStream_t s, const float* x, const float* gain, int32_t n,
   else return fail(MI_ERR_SHAPE, "rms_norm: %d values per row is more than %d", n, 64 * kNormThreads);
 #undef MI_NORM
   return hip_check(hipGetLastError(), "rms_norm launch");
+}
+
+int launch_rms_norm(hipStream_t s, const float* x, const float* gain, int32_t n, int32_t tokens, float eps,
+                    float* out, void* xq) {
+  return norm_launch(s, x, gain, n, tokens, eps, out, xq, nullptr, nullptr, 0, nullptr);
+}
+
+int launch_rms_norm_trig(hipStream_t s, const float* x, const float* gain, int32_t n, float eps, void* xq,
+                         const int32_t* pos, const float* steps, int32_t pairs, float* trig) {
+  return norm_launch(s, x, gain, n, 1, eps, nullptr, xq, pos, steps, pairs, trig);
 }
 
 int launch_rope(hipStream_t s, float* x, int32_t heads, int32_t head_dim, int32_t dim, int32_t neox,
