@@ -165,9 +165,25 @@ int mi_decoder_layer(mi_stream stream, const mi_layer_desc* d, float* resid, uin
     if ((rc = launch_q4k_qkv_rope(s, sg, d->width, xq, qkv, rp))) return rc;
   } else {
     if ((rc = launch_rms_norm(s, resid, d->attn_norm, d->width, tokens, d->eps, nullptr, xq))) return rc;
+    const bool tile_qkv = tokens > 1 && d->wq.kind == MI_Q4_K && d->wk.kind == MI_Q4_K &&
+                          d->wv.kind == MI_Q4_K && q4k_tile_fits(d->width, tokens);
     if (fused_qkv) {
       // q, k and v in one launch, straight into the fused row
       if ((rc = launch_q4k_rows_segs(s, sg, d->width, xq, qkv))) return rc;
+    } else if (tile_qkv) {
+      // the same for a batch, on the matrix-core tile
+      RowSegs tg{};
+      tg.w[0] = (const uint8_t*)d->wq.data;
+      tg.w[1] = (const uint8_t*)d->wk.data;
+      tg.w[2] = (const uint8_t*)d->wv.data;
+      tg.rb[0] = d->wq.row_bytes;
+      tg.rb[1] = d->wk.row_bytes;
+      tg.rb[2] = d->wv.row_bytes;
+      tg.end[0] = qw;
+      tg.end[1] = qw + (int32_t)kvw;
+      tg.end[2] = qw + 2 * (int32_t)kvw;
+      tg.nseg = 3;
+      if ((rc = launch_q4k_tile_segs(s, tg, d->width, xq, tokens, qkv, qkv_stride))) return rc;
     } else {
       if ((rc = launch_matvec(s, d->wq.kind, d->wq.data, d->wq.row_bytes, qw, d->width, xq, tokens, qkv,
                               qkv_stride, MI_EPI_NONE, nullptr)))
@@ -198,6 +214,11 @@ int mi_decoder_layer(mi_stream stream, const mi_layer_desc* d, float* resid, uin
     // gate and up in one launch, silu(gate) * up written directly
     if ((rc = launch_q4k_glu(s, d->gate.data, d->up.data, d->gate.row_bytes, d->hidden, d->width, xq, gate,
                              MI_EPI_NONE)))
+      return rc;
+  } else if (tokens > 1 && d->gate.kind == MI_Q4_K && d->up.kind == MI_Q4_K &&
+             d->gate.row_bytes == d->up.row_bytes && q4k_tile_fits(d->width, tokens)) {
+    if ((rc = launch_q4k_tile_glu(s, d->gate.data, d->up.data, d->gate.row_bytes, d->hidden, d->width, xq, tokens,
+                                  gate, d->hidden, MI_EPI_NONE)))
       return rc;
   } else {
     if ((rc = launch_matvec(s, d->up.kind, d->up.data, d->up.row_bytes, d->hidden, d->width, xq, tokens, up,

@@ -26,7 +26,7 @@
 //
 // Replaces the batched planar_matmul_kernel (src/molla/nn/gpu.mojo:1809) for
 // Q4_K; output y[t * ldy + r] and epilogues as gpu.mojo:1005.
-#include "matvec_units.h"
+#include "matvec_rows.h"
 
 namespace mi {
 namespace {
@@ -55,21 +55,28 @@ __device__ __forceinline__ void kscale(uint32_t y, uint32_t z, uint32_t w4, int 
 
 constexpr int kTileWaves = 8;
 
-template <int T, int SBW>
-__global__ __launch_bounds__(kTileWaves * 64) void q4k_tile_kernel(const uint8_t* __restrict__ w, int64_t rb,
-                                                                   int rows, int cols, int tn,
+// Rows come from RowSegs (one matrix, or q|k|v end to end).  GLU: sg.w[0] =
+// gate, sg.w[1] = up, both with sg.end[0] rows; every wave walks its
+// superblocks of the gate row, then of the up row, and the block writes
+// act(gate) * up.
+template <int T, int SBW, bool GLU>
+__global__ __launch_bounds__(kTileWaves * 64) void q4k_tile_kernel(const RowSegs sg, int cols, int tn,
                                                                    const uint8_t* __restrict__ xq,
                                                                    float* __restrict__ y, int64_t ldy, int epi,
                                                                    const float* __restrict__ aux) {
   constexpr int GW = 8 / T;    // groups per window
   constexpr int NW = 8 / GW;   // windows per superblock
   constexpr int NSL = GW * T;  // slots in use
+  constexpr int NP = GLU ? 2 : 1;  // passes: gate, then up
   extern __shared__ float2 meta_lds[];  // [T][G] (scale, xsum)
-  __shared__ float red[kTileWaves][T][32];
+  __shared__ float red[NP][kTileWaves][T][32];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, ks = blockDim.x >> 6;
   const int n = lane & 31, kh = lane >> 5;
-  const int row = blockIdx.x * 32 + n;
-  const uint8_t* wrow = w + (int64_t)min(row, rows - 1) * rb;
+  const int rows = GLU ? sg.end[0] : sg.end[sg.nseg - 1];
+  const int row = min(blockIdx.x * 32 + n, rows - 1);
+  const uint8_t* wrow[NP];
+  wrow[0] = GLU ? sg.w[0] + (int64_t)row * sg.rb[0] : rows::seg_row(sg, row);
+  if (GLU) wrow[NP - 1] = sg.w[1] + (int64_t)row * sg.rb[1];
   const int nsb = cols >> 8, G = cols >> 5;
   const int sb0 = wave * SBW;
   // activation offsets in 32 bits (8 tokens of 16384 values are 512 KB), so
@@ -77,10 +84,11 @@ __global__ __launch_bounds__(kTileWaves * 64) void q4k_tile_kernel(const uint8_t
   const int tok = 4 * cols, plane = (cols >> 5) * 16;
 
   // two superblocks of weights in flight: the next one's loads are issued
-  // before the current one is computed
+  // before the current one is computed; step i < SBW * NP is superblock
+  // i % SBW of pass i / SBW
   uint4 hdr[2], qp[2][4];
   auto load_w = [&](int i, int slot) {
-    const uint8_t* blk = wrow + (int64_t)min(sb0 + i, nsb - 1) * 144;
+    const uint8_t* blk = wrow[i / SBW] + (int64_t)min(sb0 + i % SBW, nsb - 1) * 144;
     hdr[slot] = ld16(blk);
 #pragma unroll
     for (int h = 0; h < 4; h++) qp[slot][h] = ld16(blk + 16 + 32 * h + 16 * kh);
@@ -93,7 +101,7 @@ __global__ __launch_bounds__(kTileWaves * 64) void q4k_tile_kernel(const uint8_t
   const int a_off = a_tok * tok + (jj * 2 + kh) * plane + a_gi * 16;
   uint4 av[2][NW];
   auto load_a = [&](int i, int slot) {
-    const int sb = min(sb0 + i, nsb - 1);
+    const int sb = min(sb0 + i % SBW, nsb - 1);
 #pragma unroll
     for (int win = 0; win < NW; win++)
       av[slot][win] = a_live ? ld16(xq + (uint32_t)(a_off + (sb * 8 + win * GW) * 16)) : make_uint4(0, 0, 0, 0);
@@ -111,86 +119,119 @@ __global__ __launch_bounds__(kTileWaves * 64) void q4k_tile_kernel(const uint8_t
   }
   __syncthreads();
 
-  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  float acc[NP][4];
 #pragma unroll
-  for (int i = 0; i < SBW; i++) {
-    const int sb = sb0 + i;
-    if (sb >= nsb) break;
+  for (int p = 0; p < NP; p++)
+#pragma unroll
+    for (int a = 0; a < 4; a++) acc[p][a] = 0.0f;
+#pragma unroll
+  for (int i = 0; i < SBW * NP; i++) {
+    const int pass = i / SBW;
+    const int sb = sb0 + i % SBW;
     const int sl = i & 1;
-    const float d = half_bits_to_float(hdr[sl].x), dmin = half_bits_to_float(hdr[sl].x >> 16);
+    if (sb < nsb) {
+      const float d = half_bits_to_float(hdr[sl].x), dmin = half_bits_to_float(hdr[sl].x >> 16);
 #pragma unroll
-    for (int win = 0; win < NW; win++) {
-      v16i C = {};
+      for (int win = 0; win < NW; win++) {
+        v16i C = {};
 #pragma unroll
-      for (int gi = 0; gi < GW; gi++) {
-        const int g = win * GW + gi;
-        const uint4 q = qp[sl][g >> 1];
-        const uint4 bq = (g & 1) ? make_uint4((q.x >> 4) & 0x0F0F0F0Fu, (q.y >> 4) & 0x0F0F0F0Fu,
-                                              (q.z >> 4) & 0x0F0F0F0Fu, (q.w >> 4) & 0x0F0F0F0Fu)
-                                 : make_uint4(q.x & 0x0F0F0F0Fu, q.y & 0x0F0F0F0Fu, q.z & 0x0F0F0F0Fu,
-                                              q.w & 0x0F0F0F0Fu);
-        const uint4 a = a_gi == gi ? av[sl][win] : make_uint4(0, 0, 0, 0);
-        C = __builtin_amdgcn_mfma_i32_32x32x32_i8(as_v4i(a), as_v4i(bq), C, 0, 0, 0);
-      }
+        for (int gi = 0; gi < GW; gi++) {
+          const int g = win * GW + gi;
+          const uint4 q = qp[sl][g >> 1];
+          const uint4 bq = (g & 1) ? make_uint4((q.x >> 4) & 0x0F0F0F0Fu, (q.y >> 4) & 0x0F0F0F0Fu,
+                                                (q.z >> 4) & 0x0F0F0F0Fu, (q.w >> 4) & 0x0F0F0F0Fu)
+                                   : make_uint4(q.x & 0x0F0F0F0Fu, q.y & 0x0F0F0F0Fu, q.z & 0x0F0F0F0Fu,
+                                                q.w & 0x0F0F0F0Fu);
+          const uint4 a = a_gi == gi ? av[sl][win] : make_uint4(0, 0, 0, 0);
+          C = __builtin_amdgcn_mfma_i32_32x32x32_i8(as_v4i(a), as_v4i(bq), C, 0, 0, 0);
+        }
 #pragma unroll
-      for (int a = 0; a < 4; a++) {
-        const int slot = 2 * a + kh;
-        const int t = slot % T;
-        if (slot < NSL && t < tn) {
-          const int g = win * GW + slot / T;
-          uint32_t sc, mn;
-          kscale(hdr[sl].y, hdr[sl].z, hdr[sl].w, g, sc, mn);
-          const float2 mt = meta_lds[t * G + sb * 8 + g];
-          const float v = limbs_to_float(C[4 * a], C[4 * a + 1] * 256 + C[4 * a + 2]);
-          acc[a] = fmaf(d * (float)sc * mt.x, v, fmaf(-dmin * (float)mn, mt.y, acc[a]));
+        for (int a = 0; a < 4; a++) {
+          const int slot = 2 * a + kh;
+          const int t = slot % T;
+          if (slot < NSL && t < tn) {
+            const int g = win * GW + slot / T;
+            uint32_t sc, mn;
+            kscale(hdr[sl].y, hdr[sl].z, hdr[sl].w, g, sc, mn);
+            const float2 mt = meta_lds[t * G + sb * 8 + g];
+            const float v = limbs_to_float(C[4 * a], C[4 * a + 1] * 256 + C[4 * a + 2]);
+            acc[pass][a] = fmaf(d * (float)sc * mt.x, v, fmaf(-dmin * (float)mn, mt.y, acc[pass][a]));
+          }
         }
       }
     }
-    if (i + 2 < SBW) {
+    if (i + 2 < SBW * NP) {
       load_w(i + 2, sl);
       load_a(i + 2, sl);
     }
   }
   // per token: the slots of this lane holding token t, then both halves
 #pragma unroll
-  for (int t = 0; t < T; t++) {
-    float v = 0.0f;
+  for (int p = 0; p < NP; p++)
 #pragma unroll
-    for (int a = 0; a < 4; a++)
-      if ((2 * a + kh) < NSL && (2 * a + kh) % T == t) v += acc[a];
-    v += __shfl_xor(v, 32);
-    if (kh == 0) red[wave][t][n] = v;
-  }
+    for (int t = 0; t < T; t++) {
+      float v = 0.0f;
+#pragma unroll
+      for (int a = 0; a < 4; a++)
+        if ((2 * a + kh) < NSL && (2 * a + kh) % T == t) v += acc[p][a];
+      v += __shfl_xor(v, 32);
+      if (kh == 0) red[p][wave][t][n] = v;
+    }
   __syncthreads();
   // 32 T outputs; a block of fewer waves than T / 2 loops
   for (int o = threadIdx.x; o < 32 * tn; o += blockDim.x) {
     const int t = o >> 5, nn = o & 31;
     float v = 0.0f;
-    for (int k = 0; k < ks; k++) v += red[k][t][nn];
+    for (int k = 0; k < ks; k++) v += red[0][k][t][nn];
     const int r = blockIdx.x * 32 + nn;
-    if (r < rows) epilogue(y, aux, epi, (int64_t)t * ldy + r, r, v);
+    if (r >= rows) continue;
+    if constexpr (GLU) {
+      float u = 0.0f;
+      for (int k = 0; k < ks; k++) u += red[NP - 1][k][t][nn];
+      const float o2 = ((epi & MI_ACT_GELU) ? gelu(v) : silu(v)) * u;
+      const int64_t at = (int64_t)t * ldy + r;
+      if (epi & MI_EPI_ADD) y[at] += o2;
+      else y[at] = o2;
+    } else {
+      epilogue(y, aux, epi, (int64_t)t * ldy + r, r, v);
+    }
   }
 }
 
-template <int T, int SBW>
-int launch_ts(hipStream_t s, const void* w, int64_t rb, int rows, int cols, int tn, const void* xq, float* y,
-              int64_t ldy, int epi, const float* aux) {
+template <int T, int SBW, bool GLU>
+int launch_ts(hipStream_t s, const RowSegs& sg, int rows, int cols, int tn, const void* xq, float* y, int64_t ldy,
+              int epi, const float* aux) {
   const int ks = (cols / 256 + SBW - 1) / SBW;
   const size_t shm = (size_t)T * (cols / 32) * sizeof(float2);
-  hipLaunchKernelGGL((q4k_tile_kernel<T, SBW>), dim3((rows + 31) / 32), dim3(ks * 64), shm, s, (const uint8_t*)w,
-                     rb, rows, cols, tn, (const uint8_t*)xq, y, ldy, epi, aux);
+  hipLaunchKernelGGL((q4k_tile_kernel<T, SBW, GLU>), dim3((rows + 31) / 32), dim3(ks * 64), shm, s, sg, cols, tn,
+                     (const uint8_t*)xq, y, ldy, epi, aux);
   return hip_check(hipGetLastError(), "matvec launch");
 }
 
 // T is the token capacity of the slot layout (2, 3, 4 or 8); tn <= T tokens
 // are live and the rest of the slots stay empty.
-template <int T>
-int launch_t(hipStream_t s, const void* w, int64_t rb, int rows, int cols, int tn, const void* xq, float* y,
+template <int T, bool GLU>
+int launch_t(hipStream_t s, const RowSegs& sg, int rows, int cols, int tn, const void* xq, float* y,
              int64_t ldy, int epi, const float* aux) {
   const int nsb = cols / 256;
-  if (nsb <= 2 * kTileWaves) return launch_ts<T, 2>(s, w, rb, rows, cols, tn, xq, y, ldy, epi, aux);
-  if (nsb <= 4 * kTileWaves) return launch_ts<T, 4>(s, w, rb, rows, cols, tn, xq, y, ldy, epi, aux);
-  return launch_ts<T, 8>(s, w, rb, rows, cols, tn, xq, y, ldy, epi, aux);
+  if (nsb <= 2 * kTileWaves) return launch_ts<T, 2, GLU>(s, sg, rows, cols, tn, xq, y, ldy, epi, aux);
+  if (nsb <= 4 * kTileWaves) return launch_ts<T, 4, GLU>(s, sg, rows, cols, tn, xq, y, ldy, epi, aux);
+  return launch_ts<T, 8, GLU>(s, sg, rows, cols, tn, xq, y, ldy, epi, aux);
+}
+
+template <bool GLU>
+int launch_g(hipStream_t s, const RowSegs& sg, int rows, int cols, const void* xq, int tokens, float* y,
+             int64_t ldy, int epi, const float* aux) {
+  switch (tokens) {
+    case 2: return launch_t<2, GLU>(s, sg, rows, cols, 2, xq, y, ldy, epi, aux);
+    case 3: return launch_t<3, GLU>(s, sg, rows, cols, 3, xq, y, ldy, epi, aux);
+    case 4: return launch_t<4, GLU>(s, sg, rows, cols, 4, xq, y, ldy, epi, aux);
+    case 5:
+    case 6:
+    case 7:
+    case 8: return launch_t<8, GLU>(s, sg, rows, cols, tokens, xq, y, ldy, epi, aux);
+  }
+  return fail(MI_ERR_ARG, "matvec: tokens %d outside 2..8 for the batched tile", tokens);
 }
 
 }  // namespace
@@ -201,16 +242,28 @@ bool q4k_tile_fits(int32_t cols, int32_t tokens) {
 
 int launch_q4k_tile(hipStream_t s, const void* w, int64_t row_bytes, int32_t rows, int32_t cols, const void* xq,
                     int32_t tokens, float* y, int64_t ldy, int32_t epi, const float* aux) {
-  switch (tokens) {
-    case 2: return launch_t<2>(s, w, row_bytes, rows, cols, 2, xq, y, ldy, epi, aux);
-    case 3: return launch_t<3>(s, w, row_bytes, rows, cols, 3, xq, y, ldy, epi, aux);
-    case 4: return launch_t<4>(s, w, row_bytes, rows, cols, 4, xq, y, ldy, epi, aux);
-    case 5:
-    case 6:
-    case 7:
-    case 8: return launch_t<8>(s, w, row_bytes, rows, cols, tokens, xq, y, ldy, epi, aux);
-  }
-  return fail(MI_ERR_ARG, "matvec: tokens %d outside 2..8 for the batched tile", tokens);
+  RowSegs sg{};
+  sg.w[0] = sg.w[1] = sg.w[2] = (const uint8_t*)w;
+  sg.rb[0] = sg.rb[1] = sg.rb[2] = row_bytes;
+  sg.end[0] = sg.end[1] = sg.end[2] = rows;
+  sg.nseg = 1;
+  return launch_g<false>(s, sg, rows, cols, xq, tokens, y, ldy, epi, aux);
+}
+
+int launch_q4k_tile_segs(hipStream_t s, const RowSegs& sg, int32_t cols, const void* xq, int32_t tokens, float* y,
+                         int64_t ldy) {
+  return launch_g<false>(s, sg, sg.end[sg.nseg - 1], cols, xq, tokens, y, ldy, MI_EPI_NONE, nullptr);
+}
+
+int launch_q4k_tile_glu(hipStream_t s, const void* gate, const void* up, int64_t row_bytes, int32_t rows,
+                        int32_t cols, const void* xq, int32_t tokens, float* y, int64_t ldy, int32_t epi) {
+  RowSegs sg{};
+  sg.w[0] = (const uint8_t*)gate;
+  sg.w[1] = sg.w[2] = (const uint8_t*)up;
+  sg.rb[0] = sg.rb[1] = sg.rb[2] = row_bytes;
+  sg.end[0] = sg.end[1] = sg.end[2] = rows;
+  sg.nseg = 2;
+  return launch_g<true>(s, sg, rows, cols, xq, tokens, y, ldy, epi, nullptr);
 }
 
 }  // namespace mi

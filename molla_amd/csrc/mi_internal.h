@@ -76,6 +76,12 @@ int launch_q6k_rows(hipStream_t s, const void* w, int64_t row_bytes, int32_t row
 bool q4k_tile_fits(int32_t cols, int32_t tokens);
 int launch_q4k_tile(hipStream_t s, const void* w, int64_t row_bytes, int32_t rows, int32_t cols, const void* xq,
                     int32_t tokens, float* y, int64_t ldy, int32_t epi, const float* aux);
+// ... with rows of up to three matrices end to end (q|k|v), and the
+// gate/up pair with the GLU applied, as the batch-1 row kernel's variants.
+int launch_q4k_tile_segs(hipStream_t s, const RowSegs& sg, int32_t cols, const void* xq, int32_t tokens, float* y,
+                         int64_t ldy);
+int launch_q4k_tile_glu(hipStream_t s, const void* gate, const void* up, int64_t row_bytes, int32_t rows,
+                        int32_t cols, const void* xq, int32_t tokens, float* y, int64_t ldy, int32_t epi);
 // Batched (2..8 tokens) Q6_K matvec on the matrix cores (matvec_tile_q6k.hip).
 bool q6k_tile_fits(int32_t cols, int64_t row_bytes, int32_t tokens);
 int launch_q6k_tile(hipStream_t s, const void* w, int64_t row_bytes, int32_t rows, int32_t cols, const void* xq,
