@@ -241,20 +241,24 @@ __global__ __launch_bounds__(kAttnThreads) void attend_split_kernel(
   // live one and are masked below) and the group's queries
   const __half* kbase = kc + (int64_t)t * cache_stride + (int64_t)kvh * D;
   const __half* vbase = vc + (int64_t)t * cache_stride + (int64_t)kvh * D;
+  // Every load of a batch is issued before any LDS store, with clamped
+  // (always valid) addresses instead of guards: a guarded load becomes a
+  // branch with its own wait, which serialised the staging.
   const int pieces = D >> 3;
   const int total = kk * pieces;
   constexpr int kBatch = 4;
+  const float4* q4 = (const float4*)(q + (int64_t)t * q_stride + (int64_t)kvh * GROUP * D);
+  const int nq4 = GROUP * D / 4;
+  const float4 qv = q4[min(tid, nq4 - 1)];
   for (int b0 = 0; b0 < total; b0 += kAttnThreads * kBatch) {
     uint4 kv[kBatch], vv[kBatch];
 #pragma unroll
     for (int j = 0; j < kBatch; j++) {
-      const int i = b0 + tid + j * kAttnThreads;
+      const int i = min(b0 + tid + j * kAttnThreads, total - 1);
       const int key = min(i / pieces, nk - 1), pc = i % pieces;
       const int64_t off = (int64_t)(start + key) * kvw + pc * 8;
-      if (i < total) {
-        kv[j] = *(const uint4*)(kbase + off);
-        vv[j] = *(const uint4*)(vbase + off);
-      }
+      kv[j] = *(const uint4*)(kbase + off);
+      vv[j] = *(const uint4*)(vbase + off);
     }
 #pragma unroll
     for (int j = 0; j < kBatch; j++) {
@@ -266,8 +270,8 @@ __global__ __launch_bounds__(kAttnThreads) void attend_split_kernel(
       }
     }
   }
-  const float4* q4 = (const float4*)(q + (int64_t)t * q_stride + (int64_t)kvh * GROUP * D);
-  for (int i = tid; i < GROUP * D / 4; i += kAttnThreads) ((float4*)Qs)[i] = q4[i];
+  if (tid < nq4) ((float4*)Qs)[tid] = qv;
+  for (int i = tid + kAttnThreads; i < nq4; i += kAttnThreads) ((float4*)Qs)[i] = q4[i];
   __syncthreads();
 
   const int64_t slot_base = ((int64_t)t * heads + (int64_t)kvh * GROUP) * max_chunks + c;
@@ -315,11 +319,22 @@ __global__ __launch_bounds__(kAttnThreads) void attend_split_kernel(
     const int g = o / halfD, e = o - g * halfD;
     const float* pg = Ps + g * kk;
     float a0 = 0.0f, a1 = 0.0f;
-    for (int k = 0; k < nk; k++) {
-      const float2 v = __half22float2(*(const __half2*)(Vs + k * D + 2 * e));
-      const float pk = pg[k];
-      a0 = fmaf(pk, v.x, a0);
-      a1 = fmaf(pk, v.y, a1);
+    // four keys per step: one float4 of weights, four value pairs (keys past
+    // nk have weight 0 and a copy of a live row, so they add exactly 0)
+    for (int k = 0; k < nk; k += 4) {
+      const float4 p4 = *(const float4*)(pg + k);
+      const float2 v0 = __half22float2(*(const __half2*)(Vs + (k + 0) * D + 2 * e));
+      const float2 v1 = __half22float2(*(const __half2*)(Vs + (k + 1) * D + 2 * e));
+      const float2 v2 = __half22float2(*(const __half2*)(Vs + (k + 2) * D + 2 * e));
+      const float2 v3 = __half22float2(*(const __half2*)(Vs + (k + 3) * D + 2 * e));
+      a0 = fmaf(p4.x, v0.x, a0);
+      a1 = fmaf(p4.x, v0.y, a1);
+      a0 = fmaf(p4.y, v1.x, a0);
+      a1 = fmaf(p4.y, v1.y, a1);
+      a0 = fmaf(p4.z, v2.x, a0);
+      a1 = fmaf(p4.z, v2.y, a1);
+      a0 = fmaf(p4.w, v3.x, a0);
+      a1 = fmaf(p4.w, v3.y, a1);
     }
     *(float2*)(part_acc + (slot_base + (int64_t)g * max_chunks) * D + 2 * e) = make_float2(a0, a1);
   }
