@@ -17,6 +17,9 @@
 //   up     hidden * tokens floats
 //   gate   hidden * tokens floats
 //   attn   attention slices (attend_workspace)
+//   trig   rope (cos, sin) of this position
+//   xq2    4 * hidden * tokens: the down projection's input, when the gate/up
+//          launch writes it (it cannot share xq, which that launch reads)
 #include <algorithm>
 
 #include "mi_internal.h"
@@ -33,7 +36,7 @@ namespace {
 size_t up256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 struct Carve {
-  size_t xq, qkv, up, gate, attn, trig, total;
+  size_t xq, qkv, up, gate, attn, trig, xq2, total;
 };
 
 Carve carve(const mi_layer_desc* d, int32_t max_count, int32_t tokens) {
@@ -53,6 +56,8 @@ Carve carve(const mi_layer_desc* d, int32_t max_count, int32_t tokens) {
   at += up256(attend_workspace(d->heads, d->head_dim, max_count, tokens));
   c.trig = at;
   at += up256(sizeof(float) * (size_t)d->rope_dim);
+  c.xq2 = at;
+  at += up256((size_t)xq_token_bytes(d->hidden) * tokens);
   c.total = at;
   return c;
 }
@@ -211,15 +216,28 @@ int mi_decoder_layer(mi_stream stream, const mi_layer_desc* d, float* resid, uin
   if ((rc = launch_rms_norm(s, resid, d->ffn_norm, d->width, tokens, d->eps, nullptr, xq))) return rc;
   if (tokens == 1 && d->gate.kind == MI_Q4_K && d->up.kind == MI_Q4_K && d->gate.row_bytes == d->up.row_bytes &&
       q4k_rows_fits(d->width)) {
-    // gate and up in one launch, silu(gate) * up written directly
+    // gate and up in one launch, silu(gate) * up written directly, and (up
+    // to 4096 columns) in matvec form for the down projection
+    if (d->width <= 4096) {
+      void* xq2 = base + c.xq2;
+      if ((rc = launch_q4k_glu(s, d->gate.data, d->up.data, d->gate.row_bytes, d->hidden, d->width, xq, gate,
+                               MI_EPI_NONE, xq2)))
+        return rc;
+      return launch_matvec(s, d->down.kind, d->down.data, d->down.row_bytes, d->width, d->hidden, xq2, tokens,
+                           resid, d->width, MI_EPI_ADD, nullptr);
+    }
     if ((rc = launch_q4k_glu(s, d->gate.data, d->up.data, d->gate.row_bytes, d->hidden, d->width, xq, gate,
                              MI_EPI_NONE)))
       return rc;
   } else if (tokens > 1 && d->gate.kind == MI_Q4_K && d->up.kind == MI_Q4_K &&
              d->gate.row_bytes == d->up.row_bytes && q4k_tile_fits(d->width, tokens)) {
+    // the tile quantizes its own output groups: no separate quantize launch
+    void* xq2 = base + c.xq2;
     if ((rc = launch_q4k_tile_glu(s, d->gate.data, d->up.data, d->gate.row_bytes, d->hidden, d->width, xq, tokens,
-                                  gate, d->hidden, MI_EPI_NONE)))
+                                  gate, d->hidden, MI_EPI_NONE, xq2)))
       return rc;
+    return launch_matvec(s, d->down.kind, d->down.data, d->down.row_bytes, d->width, d->hidden, xq2, tokens,
+                         resid, d->width, MI_EPI_ADD, nullptr);
   } else {
     if ((rc = launch_matvec(s, d->up.kind, d->up.data, d->up.row_bytes, d->hidden, d->width, xq, tokens, up,
                             d->hidden, MI_EPI_NONE, nullptr)))

@@ -79,17 +79,21 @@ __device__ __forceinline__ const uint8_t* seg_row(const RowSegs& sg, int row) {
 // GLU: sg.w[0] = gate, sg.w[1] = up, both with sg.end[0] rows.  KIND is
 // any kind with 64-value units (Q4_K, Q4_0, Q8_0; matvec_units.h).
 // ROPE: the QkvRope epilogue instead of write_epilogue (RPW even).
-template <int KIND, int RPW, int KS, bool GLU, bool ROPE = false>
-__global__ __launch_bounds__(KS * 64) void rows_kernel(const RowSegs sg, int cols,
-                                                       const uint8_t* __restrict__ xq,
-                                                       float* __restrict__ y, int epi,
-                                                       const float* __restrict__ aux, const QkvRope rp) {
+// GQ (GLU, KS == 1): a block is 32 / RPW waves owning one 32-row group, and
+// it also writes that group of y in matvec form into xq_out (the down
+// projection's input), so no quantize launch follows.
+template <int KIND, int RPW, int KS, bool GLU, bool ROPE = false, bool GQ = false>
+__global__ __launch_bounds__(GQ ? 32 / RPW * 64 : KS * 64) void rows_kernel(
+    const RowSegs sg, int cols, const uint8_t* __restrict__ xq, float* __restrict__ y, int epi,
+    const float* __restrict__ aux, const QkvRope rp, uint8_t* __restrict__ xq_out) {
+  static_assert(!GQ || (GLU && KS == 1 && 32 % RPW == 0), "GQ: GLU, one K-slice, whole groups");
   constexpr int NR = GLU ? 2 * RPW : RPW;
   __shared__ float part[KS > 1 ? KS * NR : 1];
   const int lane = threadIdx.x & 63;
   const int ks = KS > 1 ? (threadIdx.x >> 6) : 0;
   const int rows = GLU ? sg.end[0] : sg.end[sg.nseg - 1];
-  const int row0 = blockIdx.x * RPW;
+  const int wib = GQ ? (threadIdx.x >> 6) : 0;  // wave in the group block
+  const int row0 = (GQ ? blockIdx.x * (32 / RPW) + wib : blockIdx.x) * RPW;
   const int units = cols >> 6;
   const int u0 = ks * units / KS, u1 = (ks + 1) * units / KS;
   const bool act = u0 + lane < u1;
@@ -163,11 +167,16 @@ __global__ __launch_bounds__(KS * 64) void rows_kernel(const RowSegs sg, int col
     }
   } else if constexpr (GLU) {
     const float upv = __shfl_down(v, RPW);
+    const float o = ((epi & MI_ACT_GELU) ? gelu(v) : silu(v)) * upv;
     if (lane < RPW && row0 + lane < rows) {
-      const float g = (epi & MI_ACT_GELU) ? gelu(v) : silu(v);
-      const float o = g * upv;
       if (epi & MI_EPI_ADD) y[row0 + lane] += o;
       else y[row0 + lane] = o;
+    }
+    if constexpr (GQ) {
+      __shared__ float grp[32];
+      if (lane < RPW) grp[wib * RPW + lane] = o;
+      __syncthreads();
+      if (wib == 0) quantize_group32(grp[lane & 31], lane & 31, blockIdx.x, rows >> 5, xq_out, lane < 32);
     }
   } else {
     if (lane < RPW && row0 + lane < rows) epilogue(y, aux, epi, row0 + lane, row0 + lane, v);

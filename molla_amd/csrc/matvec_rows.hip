@@ -12,7 +12,7 @@ int launch_rk(hipStream_t s, const RowSegs& sg, int rows, int cols, const void* 
               const float* aux, const QkvRope& rp = QkvRope{}) {
   const int blocks = (rows + RPW - 1) / RPW;
   hipLaunchKernelGGL((rows_kernel<KIND, RPW, KS, GLU, ROPE>), dim3(blocks), dim3(KS * 64), 0, s, sg, cols,
-                     (const uint8_t*)xq, y, epi, aux, rp);
+                     (const uint8_t*)xq, y, epi, aux, rp, nullptr);
   return hip_check(hipGetLastError(), "matvec launch");
 }
 
@@ -85,13 +85,21 @@ int launch_q4k_qkv_rope(hipStream_t s, const RowSegs& sg, int32_t cols, const vo
 }
 
 int launch_q4k_glu(hipStream_t s, const void* gate, const void* up, int64_t row_bytes, int32_t rows,
-                   int32_t cols, const void* xq, float* y, int32_t epi) {
+                   int32_t cols, const void* xq, float* y, int32_t epi, void* xq_out) {
   RowSegs sg{};
   sg.w[0] = (const uint8_t*)gate;
   sg.w[1] = sg.w[2] = (const uint8_t*)up;
   sg.rb[0] = sg.rb[1] = sg.rb[2] = row_bytes;
   sg.end[0] = sg.end[1] = sg.end[2] = rows;
   sg.nseg = 2;
+  if (xq_out) {
+    if (rows % 32 || !rows_fits(MI_Q4_K, cols) || cols > 4096)
+      return fail(MI_ERR_SHAPE, "matvec: no quantized GLU output for %d x %d", rows, cols);
+    constexpr int kRpw = 4;  // 8 waves per 32-row group
+    hipLaunchKernelGGL((rows_kernel<MI_Q4_K, kRpw, 1, true, false, true>), dim3(rows / 32), dim3(32 / kRpw * 64),
+                       0, s, sg, cols, (const uint8_t*)xq, y, epi, nullptr, QkvRope{}, (uint8_t*)xq_out);
+    return hip_check(hipGetLastError(), "matvec launch");
+  }
   return launch_any<MI_Q4_K, true>(s, sg, rows, cols, xq, y, epi, nullptr);
 }
 

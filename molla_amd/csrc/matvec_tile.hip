@@ -63,7 +63,8 @@ template <int T, int SBW, bool GLU>
 __global__ __launch_bounds__(kTileWaves * 64) void q4k_tile_kernel(const RowSegs sg, int cols, int tn,
                                                                    const uint8_t* __restrict__ xq,
                                                                    float* __restrict__ y, int64_t ldy, int epi,
-                                                                   const float* __restrict__ aux) {
+                                                                   const float* __restrict__ aux,
+                                                                   uint8_t* __restrict__ xq_out) {
   constexpr int GW = 8 / T;    // groups per window
   constexpr int NW = 8 / GW;   // windows per superblock
   constexpr int NSL = GW * T;  // slots in use
@@ -192,6 +193,9 @@ __global__ __launch_bounds__(kTileWaves * 64) void q4k_tile_kernel(const RowSegs
       const int64_t at = (int64_t)t * ldy + r;
       if (epi & MI_EPI_ADD) y[at] += o2;
       else y[at] = o2;
+      // a half-wave holds one token's 32 rows of this tile: one xq group
+      // (rows % 32 == 0, so every lane of it is live)
+      if (xq_out) quantize_group32(o2, nn, r >> 5, rows >> 5, xq_out + (int64_t)t * xq_token_bytes(rows), true);
     } else {
       epilogue(y, aux, epi, (int64_t)t * ldy + r, r, v);
     }
@@ -200,11 +204,11 @@ __global__ __launch_bounds__(kTileWaves * 64) void q4k_tile_kernel(const RowSegs
 
 template <int T, int SBW, bool GLU>
 int launch_ts(hipStream_t s, const RowSegs& sg, int rows, int cols, int tn, const void* xq, float* y, int64_t ldy,
-              int epi, const float* aux) {
+              int epi, const float* aux, void* xq_out) {
   const int ks = (cols / 256 + SBW - 1) / SBW;
   const size_t shm = (size_t)T * (cols / 32) * sizeof(float2);
   hipLaunchKernelGGL((q4k_tile_kernel<T, SBW, GLU>), dim3((rows + 31) / 32), dim3(ks * 64), shm, s, sg, cols, tn,
-                     (const uint8_t*)xq, y, ldy, epi, aux);
+                     (const uint8_t*)xq, y, ldy, epi, aux, (uint8_t*)xq_out);
   return hip_check(hipGetLastError(), "matvec launch");
 }
 
@@ -212,24 +216,24 @@ int launch_ts(hipStream_t s, const RowSegs& sg, int rows, int cols, int tn, cons
 // are live and the rest of the slots stay empty.
 template <int T, bool GLU>
 int launch_t(hipStream_t s, const RowSegs& sg, int rows, int cols, int tn, const void* xq, float* y,
-             int64_t ldy, int epi, const float* aux) {
+             int64_t ldy, int epi, const float* aux, void* xq_out) {
   const int nsb = cols / 256;
-  if (nsb <= 2 * kTileWaves) return launch_ts<T, 2, GLU>(s, sg, rows, cols, tn, xq, y, ldy, epi, aux);
-  if (nsb <= 4 * kTileWaves) return launch_ts<T, 4, GLU>(s, sg, rows, cols, tn, xq, y, ldy, epi, aux);
-  return launch_ts<T, 8, GLU>(s, sg, rows, cols, tn, xq, y, ldy, epi, aux);
+  if (nsb <= 2 * kTileWaves) return launch_ts<T, 2, GLU>(s, sg, rows, cols, tn, xq, y, ldy, epi, aux, xq_out);
+  if (nsb <= 4 * kTileWaves) return launch_ts<T, 4, GLU>(s, sg, rows, cols, tn, xq, y, ldy, epi, aux, xq_out);
+  return launch_ts<T, 8, GLU>(s, sg, rows, cols, tn, xq, y, ldy, epi, aux, xq_out);
 }
 
 template <bool GLU>
 int launch_g(hipStream_t s, const RowSegs& sg, int rows, int cols, const void* xq, int tokens, float* y,
-             int64_t ldy, int epi, const float* aux) {
+             int64_t ldy, int epi, const float* aux, void* xq_out = nullptr) {
   switch (tokens) {
-    case 2: return launch_t<2, GLU>(s, sg, rows, cols, 2, xq, y, ldy, epi, aux);
-    case 3: return launch_t<3, GLU>(s, sg, rows, cols, 3, xq, y, ldy, epi, aux);
-    case 4: return launch_t<4, GLU>(s, sg, rows, cols, 4, xq, y, ldy, epi, aux);
+    case 2: return launch_t<2, GLU>(s, sg, rows, cols, 2, xq, y, ldy, epi, aux, xq_out);
+    case 3: return launch_t<3, GLU>(s, sg, rows, cols, 3, xq, y, ldy, epi, aux, xq_out);
+    case 4: return launch_t<4, GLU>(s, sg, rows, cols, 4, xq, y, ldy, epi, aux, xq_out);
     case 5:
     case 6:
     case 7:
-    case 8: return launch_t<8, GLU>(s, sg, rows, cols, tokens, xq, y, ldy, epi, aux);
+    case 8: return launch_t<8, GLU>(s, sg, rows, cols, tokens, xq, y, ldy, epi, aux, xq_out);
   }
   return fail(MI_ERR_ARG, "matvec: tokens %d outside 2..8 for the batched tile", tokens);
 }
@@ -256,14 +260,16 @@ int launch_q4k_tile_segs(hipStream_t s, const RowSegs& sg, int32_t cols, const v
 }
 
 int launch_q4k_tile_glu(hipStream_t s, const void* gate, const void* up, int64_t row_bytes, int32_t rows,
-                        int32_t cols, const void* xq, int32_t tokens, float* y, int64_t ldy, int32_t epi) {
+                        int32_t cols, const void* xq, int32_t tokens, float* y, int64_t ldy, int32_t epi,
+                        void* xq_out) {
+  if (xq_out && rows % 32) return fail(MI_ERR_SHAPE, "matvec: quantized GLU output needs rows %% 32 == 0");
   RowSegs sg{};
   sg.w[0] = (const uint8_t*)gate;
   sg.w[1] = sg.w[2] = (const uint8_t*)up;
   sg.rb[0] = sg.rb[1] = sg.rb[2] = row_bytes;
   sg.end[0] = sg.end[1] = sg.end[2] = rows;
   sg.nseg = 2;
-  return launch_g<true>(s, sg, rows, cols, xq, tokens, y, ldy, epi, nullptr);
+  return launch_g<true>(s, sg, rows, cols, xq, tokens, y, ldy, epi, nullptr, xq_out);
 }
 
 }  // namespace mi

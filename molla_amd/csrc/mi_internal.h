@@ -66,8 +66,10 @@ struct QkvRope;
 bool q4k_qkv_rope_fits(int32_t cols, int32_t head_dim, int32_t rope_dim);
 int launch_q4k_qkv_rope(hipStream_t s, const RowSegs& sg, int32_t cols, const void* xq, float* q,
                         const QkvRope& rp);
+// xq_out (rows % 32 == 0, cols <= 4096, not overlapping xq): y also written
+// in matvec form, each block quantizing the 32-row group it owns.
 int launch_q4k_glu(hipStream_t s, const void* gate, const void* up, int64_t row_bytes, int32_t rows,
-                   int32_t cols, const void* xq, float* y, int32_t epi);
+                   int32_t cols, const void* xq, float* y, int32_t epi, void* xq_out = nullptr);
 // Batch-1 Q6_K matvec for up to 4096 columns (matvec_q6k_rows.hip).
 bool q6k_rows_fits(int32_t cols, int64_t row_bytes);
 int launch_q6k_rows(hipStream_t s, const void* w, int64_t row_bytes, int32_t rows, int32_t cols, const void* xq,
@@ -80,8 +82,11 @@ int launch_q4k_tile(hipStream_t s, const void* w, int64_t row_bytes, int32_t row
 // gate/up pair with the GLU applied, as the batch-1 row kernel's variants.
 int launch_q4k_tile_segs(hipStream_t s, const RowSegs& sg, int32_t cols, const void* xq, int32_t tokens, float* y,
                          int64_t ldy);
+// xq_out (rows % 32 == 0, not overlapping xq): y also written in matvec form,
+// each tile quantizing its own 32-row groups, for the next projection.
 int launch_q4k_tile_glu(hipStream_t s, const void* gate, const void* up, int64_t row_bytes, int32_t rows,
-                        int32_t cols, const void* xq, int32_t tokens, float* y, int64_t ldy, int32_t epi);
+                        int32_t cols, const void* xq, int32_t tokens, float* y, int64_t ldy, int32_t epi,
+                        void* xq_out = nullptr);
 // Batched (2..8 tokens) Q6_K matvec on the matrix cores (matvec_tile_q6k.hip).
 bool q6k_tile_fits(int32_t cols, int64_t row_bytes, int32_t tokens);
 int launch_q6k_tile(hipStream_t s, const void* w, int64_t row_bytes, int32_t rows, int32_t cols, const void* xq,
