@@ -14,8 +14,11 @@ with per-launch HIP event pairs on the same stream.  `cpu_baseline` = the CPU
 oracle (a C restatement of molla's serial host matvec, kernel.mojo:316) on the
 same bytes, single thread, over a bounded number of repetitions.
 
---decode also runs config 5 (synthetic 8B: 32 Q4_K layers, Q6_K head, f32
-embedding; prefill then greedy decode) and reports tokens/s in "decode".
+"decode" (skipped with --no-decode) is config 5: a synthetic 8B model (32 Q4_K
+layers, Q6_K head, f32 embedding, random weights), a 2048-token prompt fed one
+position per step, then greedy decode of 256 tokens at batch 1 and 4, each
+step replayed from one captured HIP graph; tokens/s, ms per step, the eager
+(host-launched) ms per step and the weight-streaming fraction of 8 TB/s.
 """
 
 from __future__ import annotations
@@ -42,7 +45,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--decode", action="store_true", help="also time the synthetic 8B decode step")
+    ap.add_argument("--no-decode", action="store_true", help="skip the synthetic 8B decode step")
     ap.add_argument("--decode-tokens", type=int, default=256)
     ap.add_argument("--decode-batch", type=int, nargs="+", default=[1, 4])
     ap.add_argument("--prompt", type=int, default=2048)
@@ -138,7 +141,7 @@ def main():
         line["batched"] = _batched(L, h, kind, ws, copies, rb, stream)
     if not args.no_cpu:
         line["cpu_baseline"] = _cpu_baseline(base, kind, rb, x)
-    if args.decode:
+    if not args.no_decode:
         line["decode"] = _decode(ctx, args)
     print(json.dumps(line), flush=True)
 
@@ -252,32 +255,52 @@ def _decode(ctx, args):
     wb = model.weight_bytes()
     out = {"metric": "8B Q4_K decode tokens/sec", "prompt": args.prompt, "generated": args.decode_tokens,
            "weight_bytes_per_step": wb}
+    # the session's own stream: the step is captured as one HIP graph
+    # (DeviceSession.capture), which removes the host's ~10 launches per layer
+    stream = torch.cuda.Stream()
+    dctx = gpu.DeviceContext(0, stream=stream)
+    eager_n = 16
     for batch in args.decode_batch:
-        ctxlen = args.prompt + args.decode_tokens + 1
-        sess = block.DeviceSession(ctx, model, batch=batch, context=ctxlen)
-        prompt = synth.tokens(args.prompt * batch, vocab, 5 + batch, device=dev).view(args.prompt, batch)
-        sess.pos.zero_()
-        t0 = time.perf_counter()
-        for p in range(args.prompt):
-            sess.ids.copy_(prompt[p])
+        ctxlen = args.prompt + args.decode_tokens + eager_n + 1
+        with torch.cuda.stream(stream):
+            sess = block.DeviceSession(dctx, model, batch=batch, context=ctxlen)
+            prompt = synth.tokens(args.prompt * batch, vocab, 5 + batch, device=dev).view(args.prompt, batch)
+            sess.pos.zero_()
+            t0 = time.perf_counter()
+            # position 0 eagerly (every kernel loaded), the rest of the prompt
+            # through a graph of step + pos += 1 with the ids written before
+            sess.ids.copy_(prompt[0])
             sess.step()
             sess.pos.add_(1)
-        torch.cuda.synchronize()
-        prefill_s = time.perf_counter() - t0
-        e0 = torch.cuda.Event(enable_timing=True)
-        e1 = torch.cuda.Event(enable_timing=True)
-        sess.ids.copy_(sess.picks)
-        e0.record()
-        for _ in range(args.decode_tokens):
-            sess.step()
-            sess.advance()
-        e1.record()
-        torch.cuda.synchronize()
+            gp = sess.capture(advance=False)
+            for p in range(1, args.prompt):
+                sess.ids.copy_(prompt[p])
+                gp.replay()
+            stream.synchronize()
+            prefill_s = time.perf_counter() - t0
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            sess.ids.copy_(sess.picks)
+            # a few eager steps, for the host-launch cost the graph removes
+            e0.record(stream)
+            for _ in range(eager_n):
+                sess.step()
+                sess.advance()
+            e1.record(stream)
+            stream.synchronize()
+            eager_ms = e0.elapsed_time(e1) / eager_n
+            gd = sess.capture(advance=True)
+            e0.record(stream)
+            for _ in range(args.decode_tokens):
+                gd.replay()
+            e1.record(stream)
+            stream.synchronize()
         ms_step = e0.elapsed_time(e1) / args.decode_tokens
         gbs = wb / (ms_step * 1e-3) / 1e9
         out[f"batch_{batch}"] = {"tokens_per_s": round(1000 * batch / ms_step, 2), "ms_per_step": round(ms_step, 3),
                                  "weight_stream_gbs": round(gbs, 1), "frac_of_weight_roofline": round(gbs / PEAK_GBS, 4),
-                                 "prefill_s": round(prefill_s, 2)}
+                                 "eager_ms_per_step": round(eager_ms, 3), "prefill_s": round(prefill_s, 2)}
+        del gp, gd
         del sess
         torch.cuda.empty_cache()
     return out

@@ -153,3 +153,24 @@ class DeviceSession:
         """Greedy decode bookkeeping on the device: next ids = picks, pos += 1."""
         self.ids.copy_(self.picks)
         self.pos.add_(1)
+
+    def capture(self, advance: bool = True) -> "torch.cuda.CUDAGraph":
+        """Record one step() followed by advance() (or, advance=False, only
+        pos += 1, for feeding a prompt whose ids the caller writes) as one HIP
+        graph on the session's stream, so a decode loop costs one launch per
+        token instead of ~10 per layer from the host.  Every kernel of the step
+        reads ids and pos from device memory and sizes its grid by the
+        session's context, so one graph serves every position.  The stream has
+        to be a created one (graphs cannot be captured on the null stream) and
+        every kernel must have run once eagerly before (module loading is not
+        capturable): run step() once first."""
+        if self.ctx.stream == torch.cuda.default_stream(self.ctx.device):
+            raise RuntimeError("capture: the session's DeviceContext needs its own stream")
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=self.ctx.stream):
+            self.step()
+            if advance:
+                self.advance()
+            else:
+                self.pos.add_(1)
+        return g

@@ -132,3 +132,46 @@ def test_small_model_greedy_decode_matches_oracle():
         assert pick == oracle.argmax(want), p
         token = pick
         sess.advance()
+
+
+def test_graph_replay_matches_eager():
+    """The decode step captured as a HIP graph (DeviceSession.capture) gives
+    the eager step's logits and picks bit for bit, on every replay, with
+    eager work and synchronizations between the replays."""
+    from molla_amd import block, gpu
+    stream = torch.cuda.Stream()
+    ctx = gpu.DeviceContext(0, stream=stream)
+    spec = spec_of(256, 512, 4, 2, 64, base=10000.0)
+    vocab, n_layers, steps = 1000, 2, 10
+    hosts = [make_layer_weights(spec, 40 + i) for i in range(n_layers)]
+    emb = synth.normal(vocab * spec["width"], 60).numpy().reshape(vocab, spec["width"])
+    onorm = synth.normal(spec["width"], 61, mean=1.0, std=0.1).numpy()
+    head = synth.quant_tensor(oracle.Q6_K, vocab, spec["width"], 62).numpy()
+    layers = [device_layer_from(h, spec)[1] for h in hosts]
+    model = block.DeviceModel(layers[0].spec, torch.from_numpy(emb).cuda(), layers, torch.from_numpy(onorm).cuda(),
+                              gpu.Tensor.from_bytes(torch.from_numpy(head), oracle.Q6_K, spec["width"], vocab))
+    with torch.cuda.stream(stream):
+        eager = block.DeviceSession(ctx, model, batch=2, context=steps + 2)
+        graphed = block.DeviceSession(ctx, model, batch=2, context=steps + 2)
+        for s in (eager, graphed):
+            s.ids.copy_(torch.tensor([7, 11], dtype=torch.int32, device="cuda"))
+            s.pos.zero_()
+        want_logits, want_picks = [], []
+        for _ in range(steps):
+            eager.step()
+            want_logits.append(eager.logits.clone())
+            want_picks.append(eager.picks.clone())
+            eager.advance()
+        graphed.step()  # eager first position: every kernel loaded before capture
+        assert torch.equal(graphed.logits, want_logits[0])
+        graphed.advance()
+        g = graphed.capture()
+        for p in range(1, steps):
+            g.replay()
+            stream.synchronize()
+            got_logits = graphed.logits.clone()
+            assert torch.equal(got_logits, want_logits[p]), p
+            assert torch.equal(graphed.picks, want_picks[p]), p
+            # unrelated eager work between replays
+            torch.randn(4096, device="cuda").sum().item()
+        assert graphed.pos.cpu().tolist() == [steps, steps]
