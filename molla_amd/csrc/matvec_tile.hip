@@ -53,14 +53,15 @@ __device__ __forceinline__ void kscale(uint32_t y, uint32_t z, uint32_t w4, int 
   m = __builtin_amdgcn_ubfe(hi ? w4 : z, s + 4 * hi, 4) | (__builtin_amdgcn_ubfe(z, s + 4 + 2 * hi, 2) << 4);
 }
 
-constexpr int kTileWaves = 8;
+constexpr int kTileWaves = 8;  // waves per block for matrices of many tiles
+constexpr int kWideWaves = 16;  // ... and for few (<= 8192 rows): more waves split K
 
 // Rows come from RowSegs (one matrix, or q|k|v end to end).  GLU: sg.w[0] =
 // gate, sg.w[1] = up, both with sg.end[0] rows; every wave walks its
 // superblocks of the gate row, then of the up row, and the block writes
 // act(gate) * up.
-template <int T, int SBW, bool GLU>
-__global__ __launch_bounds__(kTileWaves * 64) void q4k_tile_kernel(const RowSegs sg, int cols, int tn,
+template <int T, int SBW, bool GLU, int KW>
+__global__ __launch_bounds__(KW * 64) void q4k_tile_kernel(const RowSegs sg, int cols, int tn,
                                                                    const uint8_t* __restrict__ xq,
                                                                    float* __restrict__ y, int64_t ldy, int epi,
                                                                    const float* __restrict__ aux,
@@ -70,7 +71,7 @@ __global__ __launch_bounds__(kTileWaves * 64) void q4k_tile_kernel(const RowSegs
   constexpr int NSL = GW * T;  // slots in use
   constexpr int NP = GLU ? 2 : 1;  // passes: gate, then up
   extern __shared__ float2 meta_lds[];  // [T][G] (scale, xsum)
-  __shared__ float red[NP][kTileWaves][T][32];
+  __shared__ float red[NP][KW][T][32];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, ks = blockDim.x >> 6;
   const int n = lane & 31, kh = lane >> 5;
   const int rows = GLU ? sg.end[0] : sg.end[sg.nseg - 1];
@@ -109,7 +110,7 @@ __global__ __launch_bounds__(kTileWaves * 64) void q4k_tile_kernel(const RowSegs
   };
   load_w(0, 0);
   load_a(0, 0);
-  if (SBW > 1) {
+  if (SBW * NP > 1) {  // the second step (next superblock, or the up row)
     load_w(1, 1);
     load_a(1, 1);
   }
@@ -202,12 +203,12 @@ __global__ __launch_bounds__(kTileWaves * 64) void q4k_tile_kernel(const RowSegs
   }
 }
 
-template <int T, int SBW, bool GLU>
+template <int T, int SBW, bool GLU, int KW>
 int launch_ts(hipStream_t s, const RowSegs& sg, int rows, int cols, int tn, const void* xq, float* y, int64_t ldy,
               int epi, const float* aux, void* xq_out) {
   const int ks = (cols / 256 + SBW - 1) / SBW;
   const size_t shm = (size_t)T * (cols / 32) * sizeof(float2);
-  hipLaunchKernelGGL((q4k_tile_kernel<T, SBW, GLU>), dim3((rows + 31) / 32), dim3(ks * 64), shm, s, sg, cols, tn,
+  hipLaunchKernelGGL((q4k_tile_kernel<T, SBW, GLU, KW>), dim3((rows + 31) / 32), dim3(ks * 64), shm, s, sg, cols, tn,
                      (const uint8_t*)xq, y, ldy, epi, aux, (uint8_t*)xq_out);
   return hip_check(hipGetLastError(), "matvec launch");
 }
@@ -218,9 +219,21 @@ template <int T, bool GLU>
 int launch_t(hipStream_t s, const RowSegs& sg, int rows, int cols, int tn, const void* xq, float* y,
              int64_t ldy, int epi, const float* aux, void* xq_out) {
   const int nsb = cols / 256;
-  if (nsb <= 2 * kTileWaves) return launch_ts<T, 2, GLU>(s, sg, rows, cols, tn, xq, y, ldy, epi, aux, xq_out);
-  if (nsb <= 4 * kTileWaves) return launch_ts<T, 4, GLU>(s, sg, rows, cols, tn, xq, y, ldy, epi, aux, xq_out);
-  return launch_ts<T, 8, GLU>(s, sg, rows, cols, tn, xq, y, ldy, epi, aux, xq_out);
+  // Few tiles (a 4096-row matrix is 128 blocks for 256 CUs): up to 16 waves
+  // per block split K, so the whole chip streams.
+  // (16-wave blocks have 128 registers per lane: the 8-token GLU form fits
+  // only one superblock per wave, the 8-token plain form two.)
+  constexpr int kWideSbw = T == 8 ? (GLU ? 1 : 2) : 4;
+  if (rows <= 8192 && nsb <= kWideSbw * kWideWaves) {
+    if (nsb <= kWideWaves) return launch_ts<T, 1, GLU, kWideWaves>(s, sg, rows, cols, tn, xq, y, ldy, epi, aux, xq_out);
+    if constexpr (kWideSbw >= 2)
+      if (nsb <= 2 * kWideWaves)
+        return launch_ts<T, 2, GLU, kWideWaves>(s, sg, rows, cols, tn, xq, y, ldy, epi, aux, xq_out);
+    if constexpr (kWideSbw >= 4) return launch_ts<T, 4, GLU, kWideWaves>(s, sg, rows, cols, tn, xq, y, ldy, epi, aux, xq_out);
+  }
+  if (nsb <= 2 * kTileWaves) return launch_ts<T, 2, GLU, kTileWaves>(s, sg, rows, cols, tn, xq, y, ldy, epi, aux, xq_out);
+  if (nsb <= 4 * kTileWaves) return launch_ts<T, 4, GLU, kTileWaves>(s, sg, rows, cols, tn, xq, y, ldy, epi, aux, xq_out);
+  return launch_ts<T, 8, GLU, kTileWaves>(s, sg, rows, cols, tn, xq, y, ldy, epi, aux, xq_out);
 }
 
 template <bool GLU>
