@@ -340,19 +340,32 @@ __global__ __launch_bounds__(kAttnThreads) void attend_split_kernel(
   }
 }
 
-// One block per (query head, token); thread d owns output dimension d.  All
-// slices' (max, sum) pairs are loaded at once into LDS, each wave reduces
-// them (identically), then the weighted values are folded in slice order.
+// One block per (query head, token); thread d owns output dimension d (the
+// block has max(64, head_dim) threads).  Thread d issues its loads of up to
+// 32 slices' partial values before anything else, so they overlap the
+// (max, sum) staging: the merge costs one memory latency per 32 slices.
+// Every wave reduces the (max, sum) pairs identically; the weights
+// exp(m_c - M) are computed once per slice into LDS (zero past the last
+// slice) and the values are folded in slice order.
+constexpr int kMergeBatch = 32;
 __global__ void attend_merge_kernel(const float* __restrict__ part_acc, const float* __restrict__ part_ml,
                                     int heads, int head_dim, const int32_t* __restrict__ pos_dev,
                                     int count_host, int max_chunks, float* __restrict__ out,
                                     uint8_t* __restrict__ xq) {
-  extern __shared__ float mls[];  // [max_chunks][2]
+  extern __shared__ float mls[];  // [max_chunks][2], then the weights [ceil32(max_chunks)]
   const int h = blockIdx.x, t = blockIdx.y;
   const int count = pos_dev ? pos_dev[t] + 1 : count_host;  // a position p attends over p + 1 slots
   const int kk = attn_slice(head_dim);
   const int chunks = (count + kk - 1) / kk;
+  const int padded = (chunks + kMergeBatch - 1) / kMergeBatch * kMergeBatch;
+  float* wts = mls + 2 * max_chunks;
   const int64_t slot = ((int64_t)t * heads + h) * max_chunks;
+  const int d = threadIdx.x;
+  const bool live = d < head_dim;
+  const float* pa = part_acc + slot * head_dim + min(d, head_dim - 1);
+  float a[kMergeBatch];
+#pragma unroll
+  for (int k = 0; k < kMergeBatch; k++) a[k] = pa[(int64_t)min(k, chunks - 1) * head_dim];
   for (int c = threadIdx.x; c < chunks; c += blockDim.x)
     *(float2*)(mls + 2 * c) = *(const float2*)(part_ml + (slot + c) * 2);
   __syncthreads();
@@ -361,34 +374,27 @@ __global__ void attend_merge_kernel(const float* __restrict__ part_acc, const fl
   for (int c = lane; c < chunks; c += kWave) M = fmaxf(M, mls[2 * c]);
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) M = fmaxf(M, __shfl_xor(M, o));
+  for (int c = threadIdx.x; c < padded; c += blockDim.x) wts[c] = c < chunks ? expf(mls[2 * c] - M) : 0.0f;
+  __syncthreads();
   float L = 0.0f;
-  for (int c = lane; c < chunks; c += kWave) L += mls[2 * c + 1] * expf(mls[2 * c] - M);
+  for (int c = lane; c < chunks; c += kWave) L += mls[2 * c + 1] * wts[c];
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) L += __shfl_xor(L, o);
-  const float inv = 1.0f / L;
-  const int width = heads * head_dim;
-  for (int base = 0; base < head_dim; base += blockDim.x) {
-    const int d = base + threadIdx.x;
-    const bool live = d < head_dim;
-    float o = 0.0f;
-    if (live) {
-      const float* pa = part_acc + slot * head_dim + d;
-      int c = 0;
-      for (; c + 8 <= chunks; c += 8) {
-        float a[8];
+  float o = 0.0f;
+  for (int c0 = 0; c0 < chunks; c0 += kMergeBatch) {
+    if (c0 > 0) {
 #pragma unroll
-        for (int j = 0; j < 8; j++) a[j] = pa[(int64_t)(c + j) * head_dim];
-#pragma unroll
-        for (int j = 0; j < 8; j++) o = fmaf(a[j], expf(mls[2 * (c + j)] - M), o);
-      }
-      for (; c < chunks; c++) o = fmaf(pa[(int64_t)c * head_dim], expf(mls[2 * c] - M), o);
-      o *= inv;
-      if (out) out[(int64_t)t * width + (int64_t)h * head_dim + d] = o;
+      for (int k = 0; k < kMergeBatch; k++) a[k] = pa[(int64_t)min(c0 + k, chunks - 1) * head_dim];
     }
-    if (xq)
-      quantize_group32(o, threadIdx.x & 31, (h * head_dim + d) >> 5, width >> 5,
-                       xq + (int64_t)t * xq_token_bytes(width), live);
+#pragma unroll
+    for (int k = 0; k < kMergeBatch; k++) o = fmaf(a[k], wts[c0 + k], o);
   }
+  o *= 1.0f / L;
+  const int width = heads * head_dim;
+  if (live && out) out[(int64_t)t * width + (int64_t)h * head_dim + d] = o;
+  if (xq)
+    quantize_group32(o, threadIdx.x & 31, (h * head_dim + d) >> 5, width >> 5,
+                     xq + (int64_t)t * xq_token_bytes(width), live);
 }
 
 // ---- argmax ----------------------------------------------------------------
@@ -567,8 +573,9 @@ int launch_attend(hipStream_t s, const float* q, int64_t q_stride, const uint16_
 #undef MI_ATTEND
   int rc = hip_check(hipGetLastError(), "attend_split launch");
   if (rc) return rc;
-  hipLaunchKernelGGL(attend_merge_kernel, dim3(heads, tokens), dim3(head_dim < 64 ? 64 : head_dim),
-                     (size_t)chunks * 2 * sizeof(float), s, part_acc, part_ml, heads, head_dim, pos_dev,
+  const size_t merge_lds = ((size_t)chunks * 2 + (chunks + kMergeBatch - 1) / kMergeBatch * kMergeBatch) * sizeof(float);
+  hipLaunchKernelGGL(attend_merge_kernel, dim3(heads, tokens), dim3(head_dim < 64 ? 64 : head_dim), merge_lds, s,
+                     part_acc, part_ml, heads, head_dim, pos_dev,
                      count_host, chunks, out, (uint8_t*)xq_out);
   return hip_check(hipGetLastError(), "attend_merge launch");
 }
