@@ -1,0 +1,57 @@
+"""Per-kernel summary of a rocprofv3 kernel trace (the SQLite file that
+`rocprofv3 --kernel-trace -d DIR -o NAME` writes as DIR/NAME_results.db).
+
+    python -m molla_amd.trace_summary DB            # every kernel of the run
+    python -m molla_amd.trace_summary DB --steps N  # the last N decode steps
+
+A decode step starts at an embed_kernel dispatch (DeviceSession.step), so
+--steps N keeps the dispatches from the N-th last embed_kernel on and reports
+per-step counts and times, the wall span per step and the kernel-busy time
+per step.  Used for the tables under profiles/.
+"""
+
+from __future__ import annotations
+
+import argparse
+import collections
+import re
+import sqlite3
+
+
+def short(name: str) -> str:
+    n = name.replace("void ", "").replace("mi::", "").replace("(anonymous namespace)::", "")
+    return re.sub(r"\((float|int|unsigned|__half|mi|const|long|void|signed|RowSegs|at::).*", "", n)[:64]
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("db")
+    ap.add_argument("--steps", type=int, default=0)
+    ap.add_argument("--top", type=int, default=20)
+    a = ap.parse_args()
+    rows = sqlite3.connect(a.db).execute("select name, start, end from kernels order by start").fetchall()
+    n = 1
+    if a.steps:
+        emb = [r[1] for r in rows if "embed_kernel" in r[0]]
+        t0 = emb[-a.steps]
+        rows = [r for r in rows if r[1] >= t0]
+        n = a.steps
+        span = (max(r[2] for r in rows) - t0) / 1e3
+    agg = collections.defaultdict(lambda: [0, 0.0])
+    for name, s, e in rows:
+        x = agg[short(name)]
+        x[0] += 1
+        x[1] += (e - s) / 1e3
+    busy = sum(v[1] for v in agg.values())
+    if a.steps:
+        print(f"last {n} steps: {len(rows)} dispatches, span {span / n:.1f} us/step, "
+              f"kernel-busy {busy / n:.1f} us/step")
+    unit = "per step" if a.steps else "calls"
+    print(f"| kernel | {unit} | avg us | us{'/step' if a.steps else ' total'} | share |")
+    print("|---|---|---|---|---|")
+    for k, (c, t) in sorted(agg.items(), key=lambda kv: -kv[1][1])[: a.top]:
+        print(f"| `{k}` | {c / n:g} | {t / c:.2f} | {t / n:.1f} | {100 * t / busy:.1f}% |")
+
+
+if __name__ == "__main__":
+    main()
