@@ -138,6 +138,7 @@ def main():
 
     if not args.no_batched:
         line["batched"] = _batched(L, h, kind, ws, copies, rb, stream)
+        line["kinds"] = _kinds(L, h, stream)
     if not args.no_cpu:
         line["cpu_baseline"] = _cpu_baseline(base, kind, rb, x)
     if not args.no_decode:
@@ -182,6 +183,52 @@ def _batched(L, h, kind, ws, copies, rb, stream, reps=100):
                                    "frac_hbm_peak": round(algo / us / 1e3 / PEAK_GBS, 4),
                                    "mfma_int8_TOPs": round(ops / us / 1e6, 2),
                                    "mfma_util_of_5POPs": round(ops / us / 1e6 / 5000.0, 5)}
+    return out
+
+
+def _kinds(L, h, stream, reps=100):
+    """Every other block-quantized kind at the same 14336x4096 batch-1 shape
+    (and batch 4 on the same launch path a decode step uses): weights rotated
+    over copies worth > 512 MB, twice the Infinity Cache, so reads are cold."""
+    import torch
+
+    from molla_amd import gpu, synth
+    from molla_amd._lib import check
+
+    x = synth.normal(4 * COLS, 21, device="cuda")
+    xq = torch.empty(L.mi_matvec_workspace(COLS, 4), dtype=torch.uint8, device="cuda")
+    y = torch.empty(4 * ROWS, dtype=torch.float32, device="cuda")
+    check(L.mi_quantize(h, x.data_ptr(), COLS, 4, xq.data_ptr()))
+    names = {gpu.Q_Q4_0: "q4_0", gpu.Q_Q4_1: "q4_1", gpu.Q_Q5_0: "q5_0", gpu.Q_Q5_1: "q5_1", gpu.Q_Q8_0: "q8_0",
+             gpu.Q_Q5_K: "q5_k", gpu.Q_Q6_K: "q6_k"}
+    out = {}
+    for kind, name in names.items():
+        rb = gpu.row_bytes(kind, COLS)
+        wbytes = ROWS * rb
+        n = max(2, (512 << 20) // wbytes + 1)
+        base = synth.quant_tensor(kind, ROWS, COLS, 31 + kind, device="cuda")
+        ws = [base] + [base.clone() for _ in range(n - 1)]
+        row = {}
+        for tokens in (1, 4):
+            for i in range(5):
+                check(L.mi_matvec_xq(h, kind, ws[i % n].data_ptr(), rb, ROWS, COLS, xq.data_ptr(), tokens,
+                                     y.data_ptr(), 0, None))
+            torch.cuda.synchronize()
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for i in range(reps):
+                check(L.mi_matvec_xq(h, kind, ws[i % n].data_ptr(), rb, ROWS, COLS, xq.data_ptr(), tokens,
+                                     y.data_ptr(), 0, None))
+            e1.record(stream)
+            torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) * 1e3 / reps
+            algo = _algo_bytes(ROWS, COLS, tokens, wbytes)
+            row[f"tokens_{tokens}"] = {"us": round(us, 3), "GB_s": round(algo / us / 1e3, 1),
+                                       "frac_hbm_peak": round(algo / us / 1e3 / PEAK_GBS, 4)}
+        out[name] = row
+        del ws, base
+    torch.cuda.empty_cache()
     return out
 
 

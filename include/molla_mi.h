@@ -48,9 +48,21 @@ enum {
   MI_ERR_ALIGN = -6      /* pointer alignment the kernels require is not met */
 };
 
-/* ggml type numbers (src/molla/nn/quant.mojo:47-57).  Device kernels exist for
- * the four quant kinds; F32 is accepted by the embedding lookup only. */
-enum { MI_F32 = 0, MI_F16 = 1, MI_Q4_0 = 2, MI_Q8_0 = 8, MI_Q4_K = 12, MI_Q6_K = 14 };
+/* ggml type numbers (src/molla/nn/quant.mojo:47-57).  Device dequant and
+ * matvec kernels exist for the eight block-quantized kinds; F32 is accepted
+ * by the embedding lookup only. */
+enum {
+  MI_F32 = 0,
+  MI_F16 = 1,
+  MI_Q4_0 = 2,
+  MI_Q4_1 = 3,
+  MI_Q5_0 = 6,
+  MI_Q5_1 = 7,
+  MI_Q8_0 = 8,
+  MI_Q4_K = 12,
+  MI_Q5_K = 13,
+  MI_Q6_K = 14
+};
 
 /* Matvec epilogues, same integers and meaning as src/molla/nn/gpu.mojo:781-803:
  *   NONE: y = dot          BIAS: y = dot + aux[r]

@@ -1,5 +1,6 @@
-// matvec.hip -- routes mi_matvec / mi_matvec_xq to the kernel for its kind
-// and batch: the batch-1 Q4_K / Q4_0 / Q8_0 kernel of matvec_rows.hip, the batch-1 Q6_K
+// matvec.cpp -- routes mi_matvec / mi_matvec_xq to the kernel for its kind
+// and batch: the batch-1 row kernel of matvec_rows.hip (Q4_K, Q4_0, Q8_0)
+// and matvec_rows_more.hip (Q4_1, Q5_0, Q5_1, Q5_K), the batch-1 Q6_K
 // kernel of matvec_q6k_rows.hip, the batched Q4_K tile of matvec_tile.hip
 // (matrix cores) and its Q6_K and Q4_0 / Q8_0 siblings (matvec_tile_q6k.hip,
 // matvec_tile_b32.hip), else the general
@@ -15,6 +16,14 @@ int launch_matvec_q6k(hipStream_t, const void*, int64_t, int32_t, int32_t, const
 int launch_matvec_q40(hipStream_t, const void*, int64_t, int32_t, int32_t, const void*, int32_t, float*, int64_t,
                       int32_t, const float*);
 int launch_matvec_q80(hipStream_t, const void*, int64_t, int32_t, int32_t, const void*, int32_t, float*, int64_t,
+                      int32_t, const float*);
+int launch_matvec_q41(hipStream_t, const void*, int64_t, int32_t, int32_t, const void*, int32_t, float*, int64_t,
+                      int32_t, const float*);
+int launch_matvec_q50(hipStream_t, const void*, int64_t, int32_t, int32_t, const void*, int32_t, float*, int64_t,
+                      int32_t, const float*);
+int launch_matvec_q51(hipStream_t, const void*, int64_t, int32_t, int32_t, const void*, int32_t, float*, int64_t,
+                      int32_t, const float*);
+int launch_matvec_q5k(hipStream_t, const void*, int64_t, int32_t, int32_t, const void*, int32_t, float*, int64_t,
                       int32_t, const float*);
 
 int launch_matvec(hipStream_t s, int kind, const void* w, int64_t row_bytes, int32_t rows,
@@ -35,6 +44,10 @@ int launch_matvec(hipStream_t s, int kind, const void* w, int64_t row_bytes, int
     case MI_Q6_K: return launch_matvec_q6k(s, w, row_bytes, rows, cols, xq, tokens, y, ldy, epi, aux);
     case MI_Q4_0: return launch_matvec_q40(s, w, row_bytes, rows, cols, xq, tokens, y, ldy, epi, aux);
     case MI_Q8_0: return launch_matvec_q80(s, w, row_bytes, rows, cols, xq, tokens, y, ldy, epi, aux);
+    case MI_Q4_1: return launch_matvec_q41(s, w, row_bytes, rows, cols, xq, tokens, y, ldy, epi, aux);
+    case MI_Q5_0: return launch_matvec_q50(s, w, row_bytes, rows, cols, xq, tokens, y, ldy, epi, aux);
+    case MI_Q5_1: return launch_matvec_q51(s, w, row_bytes, rows, cols, xq, tokens, y, ldy, epi, aux);
+    case MI_Q5_K: return launch_matvec_q5k(s, w, row_bytes, rows, cols, xq, tokens, y, ldy, epi, aux);
   }
   return fail(MI_ERR_KIND, "matvec: ggml type %d has no device kernel", kind);
 }

@@ -3,7 +3,7 @@
 // parallel; matvec.hip routes a call to its kind.
 //
 // Replaces the reference's planar_matvec_kernel / planar_matmul_kernel
-// (src/molla/nn/gpu.mojo:1533, :1809) for Q8_0, Q4_0, Q4_K and Q6_K.
+// (src/molla/nn/gpu.mojo:1533, :1809) for every block-quantized kind.
 //
 // Work decomposition.  A wavefront owns R consecutive output rows and walks
 // them together in "units" of 64 values (128 for Q6_K, whose bit planes

@@ -1,0 +1,11 @@
+// matvec_q50.hip -- the Q5_0 instantiations of matvec_kernel.h.
+#include "matvec_kernel.h"
+
+namespace mi {
+
+int launch_matvec_q50(hipStream_t s, const void* w, int64_t row_bytes, int32_t rows, int32_t cols,
+                     const void* xq, int32_t tokens, float* y, int64_t ldy, int32_t epi, const float* aux) {
+  return launch_kind<MI_Q5_0>(s, w, row_bytes, rows, cols, xq, tokens, y, ldy, epi, aux);
+}
+
+}  // namespace mi

@@ -99,7 +99,7 @@ __global__ __launch_bounds__(GQ ? 32 / RPW * 64 : KS * 64) void rows_kernel(
   const bool act = u0 + lane < u1;
   const int u = act ? u0 + lane : u1 - 1;
 
-  constexpr bool kL23 = KIND == MI_Q4_0;
+  constexpr bool kL23 = KIND == MI_Q4_0 || KIND == MI_Q5_0;  // kinds with a fixed offset
   XUnitRegs<kL23> xr;
   const XAcc xa{xq, 4 * (int64_t)cols, (int64_t)(cols >> 5) * 16};
 #pragma unroll
@@ -183,5 +183,57 @@ __global__ __launch_bounds__(GQ ? 32 / RPW * 64 : KS * 64) void rows_kernel(
   }
 }
 
+// ---- launchers (shared by matvec_rows.hip and matvec_rows_more.hip) ----------
+
+template <int KIND, int RPW, int KS, bool GLU, bool ROPE = false>
+int launch_rk(hipStream_t s, const RowSegs& sg, int rows, int cols, const void* xq, float* y, int epi,
+              const float* aux, const QkvRope& rp = QkvRope{}) {
+  const int blocks = (rows + RPW - 1) / RPW;
+  hipLaunchKernelGGL((rows_kernel<KIND, RPW, KS, GLU, ROPE>), dim3(blocks), dim3(KS * 64), 0, s, sg, cols,
+                     (const uint8_t*)xq, y, epi, aux, rp, nullptr);
+  return hip_check(hipGetLastError(), "matvec launch");
+}
+
+// Rows per wave: 4 keeps a 14336-row matrix resident in one round (3584
+// waves at 4 per SIMD); smaller matrices take fewer rows per wave so that
+// there are still enough waves to spread over 256 CUs.
+template <int KIND, int KS, bool GLU>
+int launch_ks(hipStream_t s, const RowSegs& sg, int rows, int cols, const void* xq, float* y, int epi,
+              const float* aux) {
+  if constexpr (GLU) {
+    return launch_rk<KIND, 2, KS, true>(s, sg, rows, cols, xq, y, epi, aux);
+  } else {
+    if (rows >= 4096) return launch_rk<KIND, 4, KS, false>(s, sg, rows, cols, xq, y, epi, aux);
+    if (rows >= 2048) return launch_rk<KIND, 2, KS, false>(s, sg, rows, cols, xq, y, epi, aux);
+    return launch_rk<KIND, 1, KS, false>(s, sg, rows, cols, xq, y, epi, aux);
+  }
+}
+
+// K split over KS = ceil(units / 64) waves of one block.
+template <int KIND, bool GLU>
+int launch_any(hipStream_t s, const RowSegs& sg, int rows, int cols, const void* xq, float* y, int epi,
+               const float* aux) {
+  if (!rows_fits(KIND, cols)) return fail(MI_ERR_SHAPE, "matvec: %d columns is beyond the batch-1 kernel", cols);
+  switch ((cols / 64 + 63) / 64) {
+    case 1: return launch_ks<KIND, 1, GLU>(s, sg, rows, cols, xq, y, epi, aux);
+    case 2: return launch_ks<KIND, 2, GLU>(s, sg, rows, cols, xq, y, epi, aux);
+    case 3: return launch_ks<KIND, 3, GLU>(s, sg, rows, cols, xq, y, epi, aux);
+    default: return launch_ks<KIND, 4, GLU>(s, sg, rows, cols, xq, y, epi, aux);
+  }
+}
+
+inline RowSegs one_matrix(const void* w, int64_t row_bytes, int32_t rows) {
+  RowSegs sg{};
+  sg.w[0] = sg.w[1] = sg.w[2] = (const uint8_t*)w;
+  sg.rb[0] = sg.rb[1] = sg.rb[2] = row_bytes;
+  sg.end[0] = sg.end[1] = sg.end[2] = rows;
+  sg.nseg = 1;
+  return sg;
+}
+
 }  // namespace rows
+
+// Batch-1 rows for Q4_1, Q5_0, Q5_1 and Q5_K (matvec_rows_more.hip).
+int launch_rows_more(hipStream_t s, int kind, const void* w, int64_t row_bytes, int32_t rows, int32_t cols,
+                     const void* xq, float* y, int32_t epi, const float* aux);
 }  // namespace mi

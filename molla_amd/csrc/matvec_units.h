@@ -32,6 +32,35 @@ __device__ __forceinline__ uint32_t align(uint32_t hi, uint32_t lo, uint32_t s) 
 // computes the current one.  X is the activation accessor (global memory or
 // a copy staged in LDS).
 
+// d * sc and dmin * m of groups 2h and 2h + 1 of a K-quant superblock whose
+// first 16 bytes (d, dmin, scales[12]) are hdr (quant.mojo:161 _k_scale):
+// the byte shift is 16*(h&1) + 8e for both packings.
+__device__ __forceinline__ void kquarter_scales(const uint4& hdr, int h, float (&dsc)[2], float (&dmn)[2]) {
+  const uint32_t sh = 16u * (h & 1);
+  const bool high = h >= 2;
+  const uint32_t hs2 = 2u * (uint32_t)(h >> 1);
+  const float d = half_bits_to_float(hdr.x), dmin = half_bits_to_float(hdr.x >> 16);
+#pragma unroll
+  for (int e = 0; e < 2; e++) {
+    const uint32_t s = sh + 8u * e;
+    // One formula for both packings: the low four bits come from
+    // scales[j] / scales[j+4] (low groups) or scales[j+8] (high groups), the
+    // top two from bits 4-5 (low) or 6-7 (high) of scales[j] / scales[j+4].
+    // Only a register is selected per lane, never a computation: a
+    // lane-divergent branch here makes the compiler hoist this row's scale
+    // work (and its wait for this row's loads) above earlier rows' dots.
+    const uint32_t sc = __builtin_amdgcn_ubfe(high ? hdr.w : hdr.y, s, 4) |
+                        (__builtin_amdgcn_ubfe(hdr.y, s + 4 + hs2, 2) << 4);
+    const uint32_t m = __builtin_amdgcn_ubfe(high ? hdr.w : hdr.z, s + 2 * hs2, 4) |
+                       (__builtin_amdgcn_ubfe(hdr.z, s + 4 + hs2, 2) << 4);
+    dsc[e] = d * (float)sc;
+    dmn[e] = dmin * (float)m;
+  }
+}
+
+// Four fifth bits (bits 0-3 of v) moved to bit 0 of four bytes.
+__device__ __forceinline__ uint32_t spread4(uint32_t v) { return (v * 0x00204081u) & 0x01010101u; }
+
 // ---- Q4_K: unit u = quarter h of superblock sb (64 values, groups 2u, 2u+1)
 template <int R>
 struct Q4KUnit {
@@ -53,31 +82,9 @@ struct Q4KUnit {
     const int h = u & 3;
     // six-bit scale/min pair for group j = 2h + e (quant.mojo:161 _k_scale):
     // the byte shift is 16*(h&1) + 8e for both packings.
-    const uint32_t sh = 16u * (h & 1);
-    const bool high = h >= 2;
-    const uint32_t hs2 = 2u * (uint32_t)(h >> 1);
     float dsc[R][2], dmn[R][2];
 #pragma unroll
-    for (int r = 0; r < R; r++) {
-      const float d = half_bits_to_float(hdr[r].x), dmin = half_bits_to_float(hdr[r].x >> 16);
-#pragma unroll
-      for (int e = 0; e < 2; e++) {
-        const uint32_t s = sh + 8u * e;
-        // One formula for both packings: the low four bits come from
-        // scales[j] / scales[j+4] (low groups) or scales[j+8] (high groups),
-        // the top two from bits 4-5 (low) or 6-7 (high) of scales[j] /
-        // scales[j+4].  Only a register is selected per lane, never a
-        // computation: a lane-divergent branch here makes the compiler hoist
-        // this row's scale work (and its wait for this row's loads) above
-        // earlier rows' dots.
-        const uint32_t sc = __builtin_amdgcn_ubfe(high ? hdr[r].w : hdr[r].y, s, 4) |
-                            (__builtin_amdgcn_ubfe(hdr[r].y, s + 4 + hs2, 2) << 4);
-        const uint32_t m = __builtin_amdgcn_ubfe(high ? hdr[r].w : hdr[r].z, s + 2 * hs2, 4) |
-                           (__builtin_amdgcn_ubfe(hdr[r].z, s + 4 + hs2, 2) << 4);
-        dsc[r][e] = d * (float)sc;
-        dmn[r][e] = dmin * (float)m;
-      }
-    }
+    for (int r = 0; r < R; r++) kquarter_scales(hdr[r], h, dsc[r], dmn[r]);
     uint32_t lo[R][8], hi[R][8];
 #pragma unroll
     for (int r = 0; r < R; r++) {
@@ -348,12 +355,245 @@ struct Q6KUnit {
   }
 };
 
+// ---- Q4_1: unit u = blocks 2u, 2u+1 (40 bytes); value = q * d + m
+template <int R>
+struct Q41Unit {
+  static constexpr int kElems = 64;
+  uint4 a[R], b[R];
+  uint32_t c[R], e[R];
+  __device__ __forceinline__ void load(const uint8_t* __restrict__ w, int64_t rb, int row0, int last_row,
+                                       int u) {
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+      const uint8_t* p = w + (int64_t)min(row0 + r, last_row) * rb + (int64_t)u * 40;
+      a[r] = ld16a4(p);
+      b[r] = ld16a4(p + 16);
+      c[r] = ld4(p + 32);
+      e[r] = ld4(p + 36);
+    }
+  }
+  template <int T, class X>
+  __device__ __forceinline__ void compute(const X& x, int u, float (&acc)[R][T]) const {
+    uint32_t lo[R][2][4], hi[R][2][4];
+    float d[R][2], m[R][2];
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+      const uint32_t W[10] = {a[r].x, a[r].y, a[r].z, a[r].w, b[r].x, b[r].y, b[r].z, b[r].w, c[r], e[r]};
+#pragma unroll
+      for (int bk = 0; bk < 2; bk++) {
+        d[r][bk] = half_bits_to_float(W[5 * bk]);
+        m[r][bk] = half_bits_to_float(W[5 * bk] >> 16);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const uint32_t q = W[5 * bk + 1 + i];
+          lo[r][bk][i] = q & 0x0F0F0F0Fu;
+          hi[r][bk][i] = (q >> 4) & 0x0F0F0F0Fu;
+        }
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < T; t++) {
+#pragma unroll
+      for (int bk = 0; bk < 2; bk++) {
+        const int g = 2 * u + bk;
+        uint4 x0[3], x1[3];
+#pragma unroll
+        for (int j = 0; j < 3; j++) {
+          x0[j] = x.limb(t, j, 0, g);
+          x1[j] = x.limb(t, j, 1, g);
+        }
+        const XMeta mt = x.meta(t, g);
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+          int s[3] = {0, 0, 0};
+#pragma unroll
+          for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int j = 0; j < 3; j++) {
+              s[j] = dot4(lo[r][bk][i], comp(x0[j], i), s[j]);
+              s[j] = dot4(hi[r][bk][i], comp(x1[j], i), s[j]);
+            }
+          const float v = limbs_to_float(s[0], s[1] * 256 + s[2]);
+          acc[r][t] = fmaf(d[r][bk] * mt.scale, v, fmaf(m[r][bk], mt.xsum, acc[r][t]));
+        }
+      }
+    }
+  }
+};
+
+// ---- Q5_0 / Q5_1: unit u = blocks 2u, 2u+1 (44 / 48 bytes); the fifth bit
+// of value l is bit l of the block's 32-bit qh.  Q5_0: (q - 16) * d, through
+// the per-half limb sums; Q5_1: q * d + m.
+template <int R, bool ONE>
+struct Q5xUnit {
+  static constexpr int kElems = 64;
+  static constexpr int kBytes = ONE ? 48 : 44;
+  static constexpr int kTail = (kBytes - 32) / 4;  // dwords after the first 32 bytes
+  uint4 a[R], b[R];
+  uint32_t c[R][kTail];
+  __device__ __forceinline__ void load(const uint8_t* __restrict__ w, int64_t rb, int row0, int last_row,
+                                       int u) {
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+      const uint8_t* p = w + (int64_t)min(row0 + r, last_row) * rb + (int64_t)u * kBytes;
+      a[r] = ld16a4(p);
+      b[r] = ld16a4(p + 16);
+#pragma unroll
+      for (int k = 0; k < kTail; k++) c[r][k] = ld4(p + 32 + 4 * k);
+    }
+  }
+  template <int T, class X>
+  __device__ __forceinline__ void compute(const X& x, int u, float (&acc)[R][T]) const {
+    uint32_t lo[R][2][4], hi[R][2][4];
+    float d[R][2], m[R][2];
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+      uint32_t W[8 + kTail] = {a[r].x, a[r].y, a[r].z, a[r].w, b[r].x, b[r].y, b[r].z, b[r].w};
+#pragma unroll
+      for (int k = 0; k < kTail; k++) W[8 + k] = c[r][k];
+#pragma unroll
+      for (int bk = 0; bk < 2; bk++) {
+        uint32_t qh, qs[4];
+        if constexpr (ONE) {  // d, m, qh, qs[16]: 24 bytes, dword aligned
+          d[r][bk] = half_bits_to_float(W[6 * bk]);
+          m[r][bk] = half_bits_to_float(W[6 * bk] >> 16);
+          qh = W[6 * bk + 1];
+#pragma unroll
+          for (int i = 0; i < 4; i++) qs[i] = W[6 * bk + 2 + i];
+        } else if (bk == 0) {  // d, qh, qs[16]: 22 bytes from byte 0
+          d[r][0] = half_bits_to_float(W[0]);
+          qh = align(W[1], W[0], 2);
+#pragma unroll
+          for (int i = 0; i < 4; i++) qs[i] = align(W[2 + i], W[1 + i], 2);
+        } else {  // from byte 22
+          d[r][1] = half_bits_to_float(W[5] >> 16);
+          qh = W[6];
+#pragma unroll
+          for (int i = 0; i < 4; i++) qs[i] = W[7 + i];
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          lo[r][bk][i] = (qs[i] & 0x0F0F0F0Fu) | (spread4((qh >> (4 * i)) & 0xFu) << 4);
+          hi[r][bk][i] = ((qs[i] >> 4) & 0x0F0F0F0Fu) | (spread4((qh >> (16 + 4 * i)) & 0xFu) << 4);
+        }
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < T; t++) {
+#pragma unroll
+      for (int bk = 0; bk < 2; bk++) {
+        const int g = 2 * u + bk;
+        uint4 x0[3], x1[3];
+#pragma unroll
+        for (int j = 0; j < 3; j++) {
+          x0[j] = x.limb(t, j, 0, g);
+          x1[j] = x.limb(t, j, 1, g);
+        }
+        const XMeta mt = x.meta(t, g);
+        int c1 = 0, c23 = 0;
+        if constexpr (!ONE) {
+          const int2 l23 = x.lsum23(t, g);
+          c1 = 16 * (mt.lsum1[0] + mt.lsum1[1]);
+          c23 = 16 * (l23.x + l23.y);
+        }
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+          int s[3] = {0, 0, 0};
+#pragma unroll
+          for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int j = 0; j < 3; j++) {
+              s[j] = dot4(lo[r][bk][i], comp(x0[j], i), s[j]);
+              s[j] = dot4(hi[r][bk][i], comp(x1[j], i), s[j]);
+            }
+          const float v = limbs_to_float(s[0] - c1, s[1] * 256 + s[2] - c23);
+          if constexpr (ONE) acc[r][t] = fmaf(d[r][bk] * mt.scale, v, fmaf(m[r][bk], mt.xsum, acc[r][t]));
+          else acc[r][t] = fmaf(d[r][bk] * mt.scale, v, acc[r][t]);
+        }
+      }
+    }
+  }
+};
+
+// ---- Q5_K: unit u = quarter h of superblock sb (64 values, groups 2u,
+// 2u+1); Q4_K's nibbles and scales plus a fifth bit per value: bit 2h of qh
+// byte l for value 64h + l, bit 2h + 1 for value 64h + 32 + l.
+template <int R>
+struct Q5KUnit {
+  static constexpr int kElems = 64;
+  uint4 hdr[R], h0[R], h1[R], a[R], b[R];
+  __device__ __forceinline__ void load(const uint8_t* __restrict__ w, int64_t rb, int row0, int last_row,
+                                       int u) {
+    const int sb = u >> 2, h = u & 3;
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+      const uint8_t* blk = w + (int64_t)min(row0 + r, last_row) * rb + (int64_t)sb * 176;
+      hdr[r] = ld16a4(blk);
+      h0[r] = ld16a4(blk + 16);
+      h1[r] = ld16a4(blk + 32);
+      a[r] = ld16a4(blk + 48 + 32 * h);
+      b[r] = ld16a4(blk + 64 + 32 * h);
+    }
+  }
+  template <int T, class X>
+  __device__ __forceinline__ void compute(const X& x, int u, float (&acc)[R][T]) const {
+    const int h = u & 3;
+    float dsc[R][2], dmn[R][2];
+#pragma unroll
+    for (int r = 0; r < R; r++) kquarter_scales(hdr[r], h, dsc[r], dmn[r]);
+    uint32_t lo[R][8], hi[R][8];
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+      const uint32_t q[8] = {a[r].x, a[r].y, a[r].z, a[r].w, b[r].x, b[r].y, b[r].z, b[r].w};
+      const uint32_t H[8] = {h0[r].x, h0[r].y, h0[r].z, h0[r].w, h1[r].x, h1[r].y, h1[r].z, h1[r].w};
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        lo[r][i] = (q[i] & 0x0F0F0F0Fu) | (((H[i] >> (2 * h)) & 0x01010101u) << 4);
+        hi[r][i] = ((q[i] >> 4) & 0x0F0F0F0Fu) | (((H[i] >> (2 * h + 1)) & 0x01010101u) << 4);
+      }
+    }
+    const int gA = 2 * u;
+#pragma unroll
+    for (int t = 0; t < T; t++) {
+      uint4 xa[3][2], xb[3][2];
+#pragma unroll
+      for (int j = 0; j < 3; j++)
+#pragma unroll
+        for (int hh = 0; hh < 2; hh++) {
+          xa[j][hh] = x.limb(t, j, hh, gA);
+          xb[j][hh] = x.limb(t, j, hh, gA + 1);
+        }
+      const XMeta ma = x.meta(t, gA), mb = x.meta(t, gA + 1);
+#pragma unroll
+      for (int r = 0; r < R; r++) {
+        int sa[3] = {0, 0, 0}, sbb[3] = {0, 0, 0};
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+#pragma unroll
+          for (int j = 0; j < 3; j++) {
+            sa[j] = dot4(lo[r][i], comp(xa[j][i >> 2], i & 3), sa[j]);
+            sbb[j] = dot4(hi[r][i], comp(xb[j][i >> 2], i & 3), sbb[j]);
+          }
+        const float va = limbs_to_float(sa[0], sa[1] * 256 + sa[2]);
+        const float vb = limbs_to_float(sbb[0], sbb[1] * 256 + sbb[2]);
+        float part = fmaf(dsc[r][0] * ma.scale, va, -dmn[r][0] * ma.xsum);
+        part = fmaf(dsc[r][1] * mb.scale, vb, part);
+        acc[r][t] += fmaf(-dmn[r][1], mb.xsum, part);
+      }
+    }
+  }
+};
+
 template <int KIND, int R>
 struct UnitOf;
 template <int R> struct UnitOf<MI_Q4_K, R> { using type = Q4KUnit<R>; };
 template <int R> struct UnitOf<MI_Q4_0, R> { using type = Q40Unit<R>; };
 template <int R> struct UnitOf<MI_Q8_0, R> { using type = Q80Unit<R>; };
 template <int R> struct UnitOf<MI_Q6_K, R> { using type = Q6KUnit<R>; };
+template <int R> struct UnitOf<MI_Q4_1, R> { using type = Q41Unit<R>; };
+template <int R> struct UnitOf<MI_Q5_0, R> { using type = Q5xUnit<R, false>; };
+template <int R> struct UnitOf<MI_Q5_1, R> { using type = Q5xUnit<R, true>; };
+template <int R> struct UnitOf<MI_Q5_K, R> { using type = Q5KUnit<R>; };
 
 // Activation accessor over the xq layout (mi_internal.h), in global memory
 // or in an LDS copy: the same byte layout either way.

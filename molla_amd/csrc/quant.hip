@@ -1,6 +1,7 @@
 // quant.hip -- bit-exact GGUF dequant and the activation quantizer.
 //
-// Dequant follows src/molla/nn/quant.mojo:184-409 operation for operation:
+// Dequant follows src/molla/nn/quant.mojo:184-409 operation for operation
+// (Q8_0, Q4_0, Q4_1, Q5_0, Q5_1, Q4_K, Q5_K, Q6_K):
 // every product is rounded on its own (no fused multiply-add), so the output
 // is bit-identical to the host decoder.  That is enforced with
 // `#pragma clang fp contract(off)` on the functions that compute values.
@@ -48,6 +49,48 @@ __global__ void dequant_kernel(int kind, const uint8_t* __restrict__ w, int64_t 
       v[l] = (float)((q & 0xF) - 8) * d;
       v[l + 16] = (float)((q >> 4) - 8) * d;
     }
+  } else if (kind == MI_Q4_1) {  // quant.mojo:247 _q4_1
+    const uint8_t* b = w + gi * 20;
+    float d = f16_at(b), m = f16_at(b + 2);
+#pragma unroll
+    for (int l = 0; l < 16; l++) {
+      int q = b[4 + l];
+      v[l] = (float)(q & 0xF) * d + m;
+      v[l + 16] = (float)(q >> 4) * d + m;
+    }
+  } else if (kind == MI_Q5_0 || kind == MI_Q5_1) {  // quant.mojo:272 _q5_0, :290 _q5_1
+    const bool one = kind == MI_Q5_1;
+    const uint8_t* b = w + gi * (one ? 24 : 22);
+    float d = f16_at(b), m = one ? f16_at(b + 2) : 0.0f;
+    const uint8_t* h = b + (one ? 4 : 2);
+    const uint32_t qh = (uint32_t)h[0] | ((uint32_t)h[1] << 8) | ((uint32_t)h[2] << 16) | ((uint32_t)h[3] << 24);
+    const uint8_t* qs = h + 4;
+#pragma unroll
+    for (int l = 0; l < 16; l++) {
+      int q = qs[l];
+      int lo = (q & 0xF) | (int)(((qh >> l) << 4) & 0x10);
+      int hi = (q >> 4) | (int)((qh >> (l + 12)) & 0x10);
+      if (one) {
+        v[l] = (float)lo * d + m;
+        v[l + 16] = (float)hi * d + m;
+      } else {
+        v[l] = (float)(lo - 16) * d;
+        v[l + 16] = (float)(hi - 16) * d;
+      }
+    }
+  } else if (kind == MI_Q5_K) {  // quant.mojo:331 _q5_k
+    const uint8_t* b = w + (gi >> 3) * 176;
+    int j = (int)(gi & 7), half = j >> 1;
+    float d = f16_at(b), dmin = f16_at(b + 2);
+    int sc, m;
+    k_scale(b + 4, j, sc, m);
+    float d1 = d * (float)sc;
+    float m1 = dmin * (float)m;
+    const uint8_t* qh = b + 16;
+    const uint8_t* q = b + 48 + half * 32;
+    int shift = (j & 1) * 4, bit = 2 * half + (j & 1);
+#pragma unroll
+    for (int l = 0; l < 32; l++) v[l] = d1 * (float)(((q[l] >> shift) & 0xF) + (((qh[l] >> bit) & 1) << 4)) - m1;
   } else if (kind == MI_Q4_K) {  // quant.mojo:310 _q4_k
     const uint8_t* b = w + (gi >> 3) * 144;
     int j = (int)(gi & 7), half = j >> 1;

@@ -28,8 +28,10 @@ int hip_check(hipError_t e, const char* what) {
 }
 
 static bool quant_kind(int kind) {
-  return kind == MI_Q4_0 || kind == MI_Q8_0 || kind == MI_Q4_K || kind == MI_Q6_K;
+  return kind == MI_Q4_0 || kind == MI_Q4_1 || kind == MI_Q5_0 || kind == MI_Q5_1 || kind == MI_Q8_0 ||
+         kind == MI_Q4_K || kind == MI_Q5_K || kind == MI_Q6_K;
 }
+static bool k_quant(int kind) { return kind == MI_Q4_K || kind == MI_Q5_K || kind == MI_Q6_K; }
 
 // The row geometry the kernels assume, checked once here.
 int check_weight(const char* name, int kind, const void* w, int64_t row_bytes, int32_t rows,
@@ -37,12 +39,11 @@ int check_weight(const char* name, int kind, const void* w, int64_t row_bytes, i
   if (!quant_kind(kind)) return fail(MI_ERR_KIND, "%s: ggml type %d has no device matvec", name, kind);
   if (!w) return fail(MI_ERR_ARG, "%s: null weight pointer", name);
   if (rows <= 0 || cols <= 0) return fail(MI_ERR_SHAPE, "%s: %d x %d is not a matrix", name, rows, cols);
-  const int unit = kind == MI_Q6_K ? 128 : (kind == MI_Q4_K ? 256 : 64);
+  // 64-value units; K quants also whole 256-value superblocks
+  const int unit = k_quant(kind) ? 256 : 64;
   if (cols % unit != 0)
     return fail(MI_ERR_SHAPE, "%s: %d columns is not a whole number of %d-value units for type %d", name,
                 cols, unit, kind);
-  if (kind == MI_Q6_K && cols % 256 != 0)
-    return fail(MI_ERR_SHAPE, "%s: %d columns is not a whole number of q6_k superblocks", name, cols);
   const int64_t want = (int64_t)cols / mi_block_elements(kind) * mi_block_bytes(kind);
   if (row_bytes != want)
     return fail(MI_ERR_SHAPE, "%s: row_bytes %lld, but %d columns of type %d take %lld", name,
@@ -69,8 +70,8 @@ int mi_sync(mi_stream stream) { return hip_check(hipStreamSynchronize((hipStream
 int mi_block_elements(int kind) {
   switch (kind) {
     case MI_F32: case MI_F16: return 1;
-    case MI_Q4_0: case MI_Q8_0: return 32;
-    case MI_Q4_K: case MI_Q6_K: return 256;
+    case MI_Q4_0: case MI_Q4_1: case MI_Q5_0: case MI_Q5_1: case MI_Q8_0: return 32;
+    case MI_Q4_K: case MI_Q5_K: case MI_Q6_K: return 256;
   }
   return 0;
 }
@@ -80,8 +81,12 @@ int mi_block_bytes(int kind) {
     case MI_F32: return 4;
     case MI_F16: return 2;
     case MI_Q4_0: return 18;
+    case MI_Q4_1: return 20;
+    case MI_Q5_0: return 22;
+    case MI_Q5_1: return 24;
     case MI_Q8_0: return 34;
     case MI_Q4_K: return 144;
+    case MI_Q5_K: return 176;
     case MI_Q6_K: return 210;
   }
   return 0;

@@ -10,6 +10,10 @@ configurations:
         in 0..63 packed as ggml's get_scale_min_k4 reads them, nibbles uniform.
   Q6_K: ql / qh bytes uniform, sixteen int8 scales uniform in [-64, 63],
         d = f16(|N(0,1)| * 0.005).
+  Q4_1, Q5_1: d = f16(|N(0,1)| * 0.01), m = f16(-|N(0,1)| * 0.08), the
+        nibbles and fifth bits uniform.
+  Q5_0: d = f16(|N(0,1)| * 0.01), nibbles and fifth bits uniform.
+  Q5_K: as Q4_K, with the fifth-bit plane uniform.
 Float16 fields are rounded to nearest even from float32.
 """
 
@@ -17,8 +21,9 @@ from __future__ import annotations
 
 import torch
 
-Q4_0, Q8_0, Q4_K, Q6_K = 2, 8, 12, 14
-BLOCK = {Q4_0: (32, 18), Q8_0: (32, 34), Q4_K: (256, 144), Q6_K: (256, 210)}
+Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q4_K, Q5_K, Q6_K = 2, 3, 6, 7, 8, 12, 13, 14
+BLOCK = {Q4_0: (32, 18), Q4_1: (32, 20), Q5_0: (32, 22), Q5_1: (32, 24), Q8_0: (32, 34), Q4_K: (256, 144),
+         Q5_K: (256, 176), Q6_K: (256, 210)}
 
 
 def _gen(seed: int, device) -> torch.Generator:
@@ -64,7 +69,12 @@ def quant_tensor(kind: int, rows: int, cols: int, seed: int, device="cpu") -> to
         b[:, 2:34] = q.to(torch.int8).view(torch.uint8)
     elif kind == Q4_0:
         b[:, 0:2] = _half_bytes(_abs_normal(n, 0.01, g, device))
-    elif kind == Q4_K:
+    elif kind in (Q4_1, Q5_1):
+        b[:, 0:2] = _half_bytes(_abs_normal(n, 0.01, g, device))
+        b[:, 2:4] = _half_bytes(-_abs_normal(n, 0.08, g, device))
+    elif kind == Q5_0:
+        b[:, 0:2] = _half_bytes(_abs_normal(n, 0.01, g, device))
+    elif kind in (Q4_K, Q5_K):
         b[:, 0:2] = _half_bytes(_abs_normal(n, 0.01, g, device))
         b[:, 2:4] = _half_bytes(_abs_normal(n, 0.01, g, device))
         sc = torch.randint(0, 64, (n, 8), generator=g, device=device, dtype=torch.int32)

@@ -15,7 +15,7 @@ bit shows up as a diff against committed data, and so that GPU tests can
 check dequant bits without the oracle.
 
 Contents (keys of the .npz):
-  deq_<kind>_blocks, deq_<kind>_out   64 blocks of each device kind and their
+  deq_<kind>_blocks, deq_<kind>_out   64 blocks of each of the eight kinds and their
                                       dequant as float32 (compared bitwise)
   mv_<kind>_w, mv_<kind>_x, mv_<kind>_y
                                       4 rows x 512 cols matvec (2 superblocks
@@ -41,7 +41,8 @@ sys.path.insert(0, ROOT)
 import oracle  # noqa: E402
 from molla_amd import synth  # noqa: E402
 
-KINDS = {"q8_0": oracle.Q8_0, "q4_0": oracle.Q4_0, "q4_k": oracle.Q4_K, "q6_k": oracle.Q6_K}
+KINDS = {"q8_0": oracle.Q8_0, "q4_0": oracle.Q4_0, "q4_k": oracle.Q4_K, "q6_k": oracle.Q6_K,
+         "q4_1": oracle.Q4_1, "q5_0": oracle.Q5_0, "q5_1": oracle.Q5_1, "q5_k": oracle.Q5_K}
 LAYER_SPEC = dict(width=256, hidden=512, heads=4, kv_heads=2, head_dim=64, rope_dim=64, neox=0, eps=1e-5,
                   rope_base=500000.0, attn_scale=float(np.float32(1 / math.sqrt(64))))
 LAYER_POS = 37

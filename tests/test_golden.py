@@ -16,7 +16,8 @@ import oracle
 from tests import npquant
 
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "golden.npz")
-KINDS = {"q8_0": oracle.Q8_0, "q4_0": oracle.Q4_0, "q4_k": oracle.Q4_K, "q6_k": oracle.Q6_K}
+KINDS = {"q8_0": oracle.Q8_0, "q4_0": oracle.Q4_0, "q4_k": oracle.Q4_K, "q6_k": oracle.Q6_K,
+         "q4_1": oracle.Q4_1, "q5_0": oracle.Q5_0, "q5_1": oracle.Q5_1, "q5_k": oracle.Q5_K}
 
 
 @pytest.fixture(scope="module")

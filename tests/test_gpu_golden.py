@@ -12,7 +12,7 @@ import torch
 pytestmark = pytest.mark.gpu
 
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "golden.npz")
-KINDS = {"q8_0": 8, "q4_0": 2, "q4_k": 12, "q6_k": 14}
+KINDS = {"q8_0": 8, "q4_0": 2, "q4_k": 12, "q6_k": 14, "q4_1": 3, "q5_0": 6, "q5_1": 7, "q5_k": 13}
 
 
 @pytest.fixture(scope="module")

@@ -22,7 +22,7 @@ from molla_amd import synth
 
 pytestmark = pytest.mark.gpu
 
-KINDS = [oracle.Q4_0, oracle.Q8_0, oracle.Q4_K, oracle.Q6_K]
+KINDS = [oracle.Q4_0, oracle.Q4_1, oracle.Q5_0, oracle.Q5_1, oracle.Q8_0, oracle.Q4_K, oracle.Q5_K, oracle.Q6_K]
 
 
 @pytest.fixture(scope="module")
@@ -40,14 +40,19 @@ def dequant_abs(kind, blob, rows, cols):
     return np.abs(oracle.dequant(kind, blob, rows * cols).reshape(rows, cols).astype(np.float64))
 
 
-def assert_matvec_close(got, want, wabs, x):
+def assert_matvec_close(got, want, wabs, x, peak_gate=True):
+    """The per-row gate always; the 1e-5-of-peak gate (kernel_oracle.mojo:59,
+    written for the benchmark shapes' realistic scales) unless peak_gate is
+    False: the reference tests' raw blocks carry scales up to 2^3 and mins,
+    so one row can be a near-cancellation of terms ~1000x its value."""
     got = np.asarray(got, np.float64).reshape(want.shape)
     want = np.asarray(want, np.float64)
     mag = np.abs(x.astype(np.float64).reshape(-1, wabs.shape[1])) @ wabs.T  # [tokens, rows]
     err = np.abs(got - want)
     assert (err <= 1e-4 * mag.reshape(want.shape) + 1e-6).all(), float((err / (mag.reshape(want.shape) + 1e-30)).max())
-    peak = np.abs(want).max()
-    assert err.max() <= 1e-5 * peak, (float(err.max()), float(peak))
+    if peak_gate:
+        peak = np.abs(want).max()
+        assert err.max() <= 1e-5 * peak, (float(err.max()), float(peak))
 
 
 # ---- dequant: bit-exact ------------------------------------------------------
@@ -90,7 +95,7 @@ def test_matvec_reference_blocks(ctx, kind, rows):
     w = upload(blob, kind, cols, rows)
     out = np.zeros(rows, np.float32)
     gpu.device_matvec(ctx, w, x, out)
-    assert_matvec_close(out, want, dequant_abs(kind, blob, rows, cols), x)
+    assert_matvec_close(out, want, dequant_abs(kind, blob, rows, cols), x, peak_gate=False)
 
 
 @pytest.mark.parametrize("kind", KINDS)
