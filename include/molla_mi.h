@@ -174,6 +174,9 @@ typedef struct {
   const float* ffn_norm;  /* device f32[width] */
   const float* rope_steps; /* device f32[rope_dim/2] from mi_rope_steps */
   mi_weight wq, wk, wv, wo, gate, up, down;
+  const float* rope_factors; /* device f32[rope_dim/2]: rope_freqs.weight of a
+                                Llama 3.1 file (each pair's angle is divided by
+                                its factor, rope.mojo:253), or NULL for none */
 } mi_layer_desc;
 
 /* One Llama layer for `tokens` independent sequences (batch decode, one token

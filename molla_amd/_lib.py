@@ -24,7 +24,8 @@ class MiLayerDesc(ctypes.Structure):
     _fields_ = [("width", I32), ("hidden", I32), ("heads", I32), ("kv_heads", I32), ("head_dim", I32),
                 ("rope_dim", I32), ("neox", I32), ("eps", F), ("attn_scale", F), ("attn_norm", P),
                 ("ffn_norm", P), ("rope_steps", P)] + \
-               [(n, MiWeight) for n in ("wq", "wk", "wv", "wo", "gate", "up", "down")]
+               [(n, MiWeight) for n in ("wq", "wk", "wv", "wo", "gate", "up", "down")] + \
+               [("rope_factors", P)]
 
 
 # Every symbol include/molla_mi.h declares, with its C signature.

@@ -51,12 +51,14 @@ class DeviceLayer:
     NAMES = ("wq", "wk", "wv", "wo", "gate", "up", "down")
 
     def __init__(self, spec: BlockSpec, attn_norm: torch.Tensor, ffn_norm: torch.Tensor, weights: dict,
-                 rope_steps: torch.Tensor):
+                 rope_steps: torch.Tensor, rope_factors: torch.Tensor | None = None):
         self.spec = spec
         self.attn_norm = attn_norm
         self.ffn_norm = ffn_norm
         self.weights = weights  # name -> gpu.Tensor
         self.rope_steps = rope_steps
+        # rope_freqs.weight of a Llama 3.1 file, one factor per pair, or None
+        self.rope_factors = rope_factors
         d = MiLayerDesc()
         d.width, d.hidden = spec.width, spec.hidden
         d.heads, d.kv_heads, d.head_dim = spec.heads, spec.kv_heads, spec.head_dim
@@ -65,6 +67,10 @@ class DeviceLayer:
         d.attn_norm, d.ffn_norm, d.rope_steps = attn_norm.data_ptr(), ffn_norm.data_ptr(), rope_steps.data_ptr()
         for n in self.NAMES:
             setattr(d, n, weights[n].weight())
+        if rope_factors is not None:
+            if rope_factors.dtype != torch.float32 or rope_factors.numel() < spec.rope_dim // 2:
+                raise ValueError(f"rope wants {spec.rope_dim // 2} f32 frequency factors")
+            d.rope_factors = rope_factors.data_ptr()
         self.desc = d
 
     def weight_bytes(self) -> int:

@@ -156,7 +156,7 @@ int mi_decoder_layer(mi_stream stream, const mi_layer_desc* d, float* resid, uin
     // the cache store in its epilogue: no separate rope launch
     float* trig = (float*)(base + c.trig);
     if ((rc = launch_rms_norm_trig(s, resid, d->attn_norm, d->width, d->eps, xq, pos, d->rope_steps,
-                                   d->rope_dim / 2, trig)))
+                                   d->rope_factors, d->rope_dim / 2, trig)))
       return rc;
     QkvRope rp{};
     rp.qw = qw;
@@ -201,7 +201,8 @@ int mi_decoder_layer(mi_stream stream, const mi_layer_desc* d, float* resid, uin
         return rc;
     }
     if ((rc = launch_rope_store(s, qkv, d->heads, d->kv_heads, d->head_dim, d->rope_dim, d->neox,
-                                d->rope_steps, pos, tokens, qkv_stride, k_cache, v_cache, cache_stride)))
+                                d->rope_steps, pos, tokens, qkv_stride, k_cache, v_cache, cache_stride,
+                                d->rope_factors)))
       return rc;
   }
   // count = pos + 1 per sequence: the attention kernels read pos and add one.

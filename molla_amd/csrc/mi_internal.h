@@ -102,14 +102,17 @@ int launch_matvec(hipStream_t s, int kind, const void* w, int64_t row_bytes, int
                   int32_t cols, const void* xq, int32_t tokens, float* y, int64_t ldy, int32_t epi,
                   const float* aux);
 // rms_norm_trig: also writes trig[p] = (cos, sin) of f32(pos[0]) * steps[p]
-// for p < pairs (float64 trig, as rope.mojo:253-285), for the fused q|k|v
-// epilogue of the same layer.
+// (divided by factors[p] when factors is given) for p < pairs (float64 trig,
+// as rope.mojo:253-285), for the fused q|k|v epilogue of the same layer.
 int launch_rms_norm_trig(hipStream_t s, const float* x, const float* gain, int32_t n, float eps, void* xq,
-                         const int32_t* pos, const float* steps, int32_t pairs, float* trig);
+                         const int32_t* pos, const float* steps, const float* factors, int32_t pairs,
+                         float* trig);
 int launch_rms_norm(hipStream_t s, const float* x, const float* gain, int32_t n, int32_t tokens,
                     float eps, float* out, void* xq);
+// factors: rope_freqs.weight (one per pair), or null for none.
 int launch_rope(hipStream_t s, float* x, int32_t heads, int32_t head_dim, int32_t dim, int32_t neox,
-                const float* steps, const int32_t* pos, int32_t tokens, int64_t row_stride);
+                const float* steps, const int32_t* pos, int32_t tokens, int64_t row_stride,
+                const float* factors = nullptr);
 int launch_store_kv(hipStream_t s, const float* k, const float* v, int32_t kv_width,
                     uint16_t* k_cache, uint16_t* v_cache, const int32_t* slot_dev, int32_t slot_host,
                     int32_t tokens, int64_t src_stride, int64_t cache_stride);
@@ -118,7 +121,7 @@ int launch_store_kv(hipStream_t s, const float* k, const float* v, int32_t kv_wi
 int launch_rope_store(hipStream_t s, float* qkv, int32_t heads, int32_t kv_heads, int32_t head_dim,
                       int32_t dim, int32_t neox, const float* steps, const int32_t* pos,
                       int32_t tokens, int64_t row_stride, uint16_t* k_cache, uint16_t* v_cache,
-                      int64_t cache_stride);
+                      int64_t cache_stride, const float* factors = nullptr);
 size_t attend_workspace(int32_t heads, int32_t head_dim, int32_t max_count, int32_t tokens);
 int launch_attend(hipStream_t s, const float* q, int64_t q_stride, const uint16_t* k_cache,
                   const uint16_t* v_cache, int64_t cache_stride, int32_t heads, int32_t kv_heads,

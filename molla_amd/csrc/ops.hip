@@ -25,22 +25,32 @@ namespace {
 // the slowest part.  All loads are issued before any arithmetic.
 constexpr int kNormThreads = 256;
 
-// With `trig`, the last block also writes (cos, sin) of f32(pos[0]) * steps[p]
-// for p < pairs, in float64 as rope.mojo:253-285, for the layer's fused q|k|v
-// rope; it has no other use for its spare threads' time.
+// rope.mojo:253 angle with scale 1 and no YaRN mix: f32(pos) * step / freq,
+// freq being the pair's rope_freqs.weight factor (none: 1, no division).
+__device__ __forceinline__ float rope_theta(int pos, const float* __restrict__ steps,
+                                            const float* __restrict__ factors, int pair) {
+#pragma clang fp contract(off)
+  const float theta = (float)pos * steps[pair];
+  return factors ? theta / factors[pair] : theta;
+}
+
+// With `trig`, the last block also writes (cos, sin) of the angle of pair p at
+// pos[0] for p < pairs, in float64 as rope.mojo:253-285, for the layer's fused
+// q|k|v rope; it has no other use for its spare threads' time.
 template <int PER>
 __global__ __launch_bounds__(kNormThreads) void rms_norm_kernel(const float* __restrict__ x,
                                                                 const float* __restrict__ gain, int n,
                                                                 float eps, float* __restrict__ out,
                                                                 uint8_t* __restrict__ xq,
                                                                 const int32_t* __restrict__ pos,
-                                                                const float* __restrict__ steps, int pairs,
+                                                                const float* __restrict__ steps,
+                                                                const float* __restrict__ factors, int pairs,
                                                                 float2* __restrict__ trig) {
 #pragma clang fp contract(off)
   const int t = blockIdx.y;
   if (trig && blockIdx.x == gridDim.x - 1) {
     for (int p = threadIdx.x; p < pairs; p += kNormThreads) {
-      const float theta = (float)pos[0] * steps[p];
+      const float theta = rope_theta(pos[0], steps, factors, p);
       trig[p] = make_float2((float)cos((double)theta), (float)sin((double)theta));
     }
   }
@@ -80,14 +90,15 @@ __global__ __launch_bounds__(kNormThreads) void rms_norm_kernel(const float* __r
 }
 
 // ---- RoPE ------------------------------------------------------------------
-// rope.mojo:253-338: theta = f32(pos) * step / freq (freq 1, scale 1),
+// rope.mojo:253-338: theta = f32(pos) * step / freq (scale 1),
 // c = f32(cos(f64(theta))), s likewise, (a, b) <- (a*c - b*s, a*s + b*c).
 // The trig is done in float64 on the device too, so the rotated values
 // match the host's to float32 rounding at any position.
 __device__ __forceinline__ void rotate_pair(float* __restrict__ row, int head_dim, int dim, int neox,
-                                            const float* __restrict__ steps, int pos, int head, int pair) {
+                                            const float* __restrict__ steps, const float* __restrict__ factors,
+                                            int pos, int head, int pair) {
 #pragma clang fp contract(off)
-  const float theta = (float)pos * steps[pair];
+  const float theta = rope_theta(pos, steps, factors, pair);
   const float c = (float)cos((double)theta);
   const float s = (float)sin((double)theta);
   const int pairs = dim >> 1;
@@ -100,13 +111,13 @@ __device__ __forceinline__ void rotate_pair(float* __restrict__ row, int head_di
 }
 
 __global__ void rope_kernel(float* __restrict__ x, int heads, int head_dim, int dim, int neox,
-                            const float* __restrict__ steps, const int32_t* __restrict__ pos,
-                            int64_t row_stride) {
+                            const float* __restrict__ steps, const float* __restrict__ factors,
+                            const int32_t* __restrict__ pos, int64_t row_stride) {
   const int t = blockIdx.x;
   const int pairs = dim >> 1;
   float* row = x + (int64_t)t * row_stride;
   for (int i = threadIdx.x; i < heads * pairs; i += blockDim.x)
-    rotate_pair(row, head_dim, dim, neox, steps, pos[t], i / pairs, i % pairs);
+    rotate_pair(row, head_dim, dim, neox, steps, factors, pos[t], i / pairs, i % pairs);
 }
 
 // Rotate q and k of a fused [q | k | v] row in place, then store k and v as
@@ -120,7 +131,8 @@ constexpr int kRopePer = 8;  // pairs per thread held in registers per pass
 
 __global__ __launch_bounds__(kRopeThreads) void rope_store_kernel(
     float* __restrict__ qkv, int heads, int kv_heads, int head_dim, int dim, int neox,
-    const float* __restrict__ steps, const int32_t* __restrict__ pos, int64_t row_stride,
+    const float* __restrict__ steps, const float* __restrict__ factors, const int32_t* __restrict__ pos,
+    int64_t row_stride,
     __half* __restrict__ kc, __half* __restrict__ vc, int64_t cache_stride) {
 #pragma clang fp contract(off)
   extern __shared__ float trig[];  // [pairs][2]
@@ -145,7 +157,7 @@ __global__ __launch_bounds__(kRopeThreads) void rope_store_kernel(
     }
     if (base == 0) {
       for (int q = threadIdx.x; q < pairs; q += kRopeThreads) {
-        const float theta = (float)p * steps[q];
+        const float theta = rope_theta(p, steps, factors, q);
         trig[2 * q] = (float)cos((double)theta);
         trig[2 * q + 1] = (float)sin((double)theta);
       }
@@ -484,12 +496,13 @@ __global__ void embed_kernel(const float* __restrict__ emb, int vocab, int width
 }  // namespace
 
 static int norm_launch(hipStream_t s, const float* x, const float* gain, int32_t n, int32_t tokens, float eps,
-                       float* out, void* xq, const int32_t* pos, const float* steps, int32_t pairs, float* trig) {
+                       float* out, void* xq, const int32_t* pos, const float* steps, const float* factors,
+                       int32_t pairs, float* trig) {
   const int per = (n + kNormThreads - 1) / kNormThreads;
   dim3 grid(per, tokens);
 #define MI_NORM(P)                                                                                      \
   hipLaunchKernelGGL(rms_norm_kernel<P>, grid, dim3(kNormThreads), 0, s, x, gain, n, eps, out, (uint8_t*)xq, \
-                     pos, steps, pairs, (float2*)trig)
+                     pos, steps, factors, pairs, (float2*)trig)
   if (per <= 4) MI_NORM(4);
   else if (per <= 8) MI_NORM(8);
   else if (per <= 16) MI_NORM(16);
@@ -502,17 +515,18 @@ static int norm_launch(hipStream_t s, const float* x, const float* gain, int32_t
 
 int launch_rms_norm(hipStream_t s, const float* x, const float* gain, int32_t n, int32_t tokens, float eps,
                     float* out, void* xq) {
-  return norm_launch(s, x, gain, n, tokens, eps, out, xq, nullptr, nullptr, 0, nullptr);
+  return norm_launch(s, x, gain, n, tokens, eps, out, xq, nullptr, nullptr, nullptr, 0, nullptr);
 }
 
 int launch_rms_norm_trig(hipStream_t s, const float* x, const float* gain, int32_t n, float eps, void* xq,
-                         const int32_t* pos, const float* steps, int32_t pairs, float* trig) {
-  return norm_launch(s, x, gain, n, 1, eps, nullptr, xq, pos, steps, pairs, trig);
+                         const int32_t* pos, const float* steps, const float* factors, int32_t pairs,
+                         float* trig) {
+  return norm_launch(s, x, gain, n, 1, eps, nullptr, xq, pos, steps, factors, pairs, trig);
 }
 
 int launch_rope(hipStream_t s, float* x, int32_t heads, int32_t head_dim, int32_t dim, int32_t neox,
-                const float* steps, const int32_t* pos, int32_t tokens, int64_t row_stride) {
-  hipLaunchKernelGGL(rope_kernel, dim3(tokens), dim3(256), 0, s, x, heads, head_dim, dim, neox, steps,
+                const float* steps, const int32_t* pos, int32_t tokens, int64_t row_stride, const float* factors) {
+  hipLaunchKernelGGL(rope_kernel, dim3(tokens), dim3(256), 0, s, x, heads, head_dim, dim, neox, steps, factors,
                      pos, row_stride);
   return hip_check(hipGetLastError(), "rope launch");
 }
@@ -520,9 +534,9 @@ int launch_rope(hipStream_t s, float* x, int32_t heads, int32_t head_dim, int32_
 int launch_rope_store(hipStream_t s, float* qkv, int32_t heads, int32_t kv_heads, int32_t head_dim,
                       int32_t dim, int32_t neox, const float* steps, const int32_t* pos,
                       int32_t tokens, int64_t row_stride, uint16_t* k_cache, uint16_t* v_cache,
-                      int64_t cache_stride) {
+                      int64_t cache_stride, const float* factors) {
   hipLaunchKernelGGL(rope_store_kernel, dim3(tokens), dim3(kRopeThreads), (size_t)dim * sizeof(float), s, qkv,
-                     heads, kv_heads, head_dim, dim, neox, steps, pos, row_stride, (__half*)k_cache,
+                     heads, kv_heads, head_dim, dim, neox, steps, factors, pos, row_stride, (__half*)k_cache,
                      (__half*)v_cache, cache_stride);
   return hip_check(hipGetLastError(), "rope_store launch");
 }

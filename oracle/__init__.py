@@ -62,7 +62,8 @@ class Layer(ctypes.Structure):
                 ("width", "hidden", "heads", "kv_heads", "head_dim", "rope_dim", "neox")] + \
                [(n, ctypes.c_float) for n in ("eps", "rope_base", "attn_scale")] + \
                [("attn_norm", ctypes.c_void_p), ("ffn_norm", ctypes.c_void_p)] + \
-               [(n, Weight) for n in ("wq", "wk", "wv", "wo", "gate", "up", "down")]
+               [(n, Weight) for n in ("wq", "wk", "wv", "wo", "gate", "up", "down")] + \
+               [("rope_factors", ctypes.c_void_p)]
 
 
 def _declare(l):
@@ -84,6 +85,7 @@ def _declare(l):
         "or_rope_steps": (None, [P, I32, F]),
         "or_rope_angle": (None, [I32, F, I32, I32, P, P]),
         "or_rotate_run": (None, [P, I32, I32, I32, F, I32, I32]),
+        "or_rotate_run_scaled": (None, [P, I32, I32, I32, F, I32, I32, P]),
         "or_attend": (None, [I32, I32, I32, F, P, P, P, I32, P, P]),
         "or_layer_step": (ctypes.c_int, [ctypes.POINTER(Layer), P, P, P, I32, I32, I32, I32]),
         "or_forward": (ctypes.c_int, [ctypes.POINTER(Layer), I32, P, I32, P, ctypes.POINTER(Weight),
@@ -200,9 +202,19 @@ def rope_angle(dim: int, base: float, pos: int, pair: int):
     return float(c[0]), float(s[0])
 
 
-def rotate(x: np.ndarray, heads: int, head_dim: int, dim: int, base: float, neox: bool, pos: int) -> np.ndarray:
+def rotate(x: np.ndarray, heads: int, head_dim: int, dim: int, base: float, neox: bool, pos: int,
+           factors=None) -> np.ndarray:
+    """rope.mojo:294 rotate_scaled; factors: one per pair (rope_freqs.weight) or None."""
     x = np.array(x, dtype=np.float32)
-    lib().or_rotate_run(_p(x), heads, head_dim, dim, base, int(neox), pos)
+    if factors is None:
+        lib().or_rotate_run(_p(x), heads, head_dim, dim, base, int(neox), pos)
+    else:
+        f = np.ascontiguousarray(factors, dtype=np.float32)
+        if f.size < dim // 2:
+            raise ValueError(f"rope wants {dim // 2} frequency factors but got {f.size}")
+        if (f == 0).any():
+            raise ValueError("a rope frequency factor of zero has no angle")
+        lib().or_rotate_run_scaled(_p(x), heads, head_dim, dim, base, int(neox), pos, _p(f))
     return x
 
 
@@ -218,7 +230,8 @@ def attend(heads, kv_heads, head_dim, scale, q, keys, values, count) -> np.ndarr
 
 def make_layer(spec: dict, weights: dict, keep: list) -> Layer:
     """spec: width, hidden, heads, kv_heads, head_dim, rope_dim, neox, eps, rope_base, attn_scale.
-    weights: attn_norm, ffn_norm (f32 arrays); wq..down as (kind, rows, cols, bytes)."""
+    weights: attn_norm, ffn_norm (f32 arrays); wq..down as (kind, rows, cols, bytes);
+    optionally rope_factors (f32, rope_dim / 2)."""
     L = Layer()
     for k in ("width", "hidden", "heads", "kv_heads", "head_dim", "rope_dim", "neox"):
         setattr(L, k, int(spec[k]))
@@ -233,6 +246,11 @@ def make_layer(spec: dict, weights: dict, keep: list) -> Layer:
         blob = np.ascontiguousarray(blob, dtype=np.uint8)
         keep.append(blob)
         setattr(L, k, Weight(blob.ctypes.data, kind, rows, cols, row_bytes(kind, cols)))
+    f = weights.get("rope_factors")  # rope_freqs.weight, one per pair, or absent
+    if f is not None:
+        f = np.ascontiguousarray(f, dtype=np.float32)
+        keep.append(f)
+        L.rope_factors = f.ctypes.data
     return L
 
 

@@ -524,25 +524,31 @@ void or_rope_steps(float* steps, int32_t dim, float base) {
     steps[pair] = powf_ref(base, -2.0f * (float)pair / (float)dim);
 }
 
-/* rope.mojo:253 angle, with scale 1, ext_factor 0, attn_factor 1, freq 1. */
-void or_rope_angle(int32_t dim, float base, int32_t pos, int32_t pair, float* c, float* s) {
+/* rope.mojo:253 angle, with scale 1, ext_factor 0, attn_factor 1; freq is
+ * the pair's rope_freqs.weight factor (1 when the model has none). */
+void or_rope_angle_scaled(int32_t dim, float base, int32_t pos, int32_t pair, float freq, float* c, float* s) {
   float step = powf_ref(base, -2.0f * (float)pair / (float)dim);
-  float extrap = (float)pos * step / 1.0f;
+  float extrap = (float)pos * step / freq;
   float interp = 1.0f * extrap;
   float theta = interp;
   *c = (float)cos((double)theta) * 1.0f;
   *s = (float)sin((double)theta) * 1.0f;
 }
 
-/* rope.mojo:294 rotate_scaled over every head (rope.mojo:374 rotate_run). */
-void or_rotate_run(float* x, int32_t heads, int32_t head_dim, int32_t dim,
-                   float base, int32_t neox, int32_t pos) {
+void or_rope_angle(int32_t dim, float base, int32_t pos, int32_t pair, float* c, float* s) {
+  or_rope_angle_scaled(dim, base, pos, pair, 1.0f, c, s);
+}
+
+/* rope.mojo:294 rotate_scaled over every head (rope.mojo:374 rotate_run);
+ * factors: one per pair (rope_freqs.weight), or NULL for none. */
+void or_rotate_run_scaled(float* x, int32_t heads, int32_t head_dim, int32_t dim,
+                          float base, int32_t neox, int32_t pos, const float* factors) {
   int32_t pairs = dim / 2;
   for (int32_t h = 0; h < heads; h++) {
     float* at = x + (int64_t)h * head_dim;
     for (int32_t pair = 0; pair < pairs; pair++) {
       float c, s;
-      or_rope_angle(dim, base, pos, pair, &c, &s);
+      or_rope_angle_scaled(dim, base, pos, pair, factors ? factors[pair] : 1.0f, &c, &s);
       int32_t lo, hi;
       if (neox) {
         lo = pair;
@@ -556,6 +562,11 @@ void or_rotate_run(float* x, int32_t heads, int32_t head_dim, int32_t dim,
       at[hi] = a * s + b * c;
     }
   }
+}
+
+void or_rotate_run(float* x, int32_t heads, int32_t head_dim, int32_t dim,
+                   float base, int32_t neox, int32_t pos) {
+  or_rotate_run_scaled(x, heads, head_dim, dim, base, neox, pos, NULL);
 }
 
 /* attention.mojo:144 attend over a contiguous run of positions 0..count-1. */
@@ -613,8 +624,9 @@ int or_layer_step(const or_layer* L, float* x, float* keys, float* values,
   float* vslot = values + (int64_t)slot * kvw;
   if ((rc = mv(&L->wk, norm, kslot, threads))) goto done;
   if ((rc = mv(&L->wv, norm, vslot, threads))) goto done;
-  or_rotate_run(q, L->heads, L->head_dim, L->rope_dim, L->rope_base, L->neox, pos);
-  or_rotate_run(kslot, L->kv_heads, L->head_dim, L->rope_dim, L->rope_base, L->neox, pos);
+  or_rotate_run_scaled(q, L->heads, L->head_dim, L->rope_dim, L->rope_base, L->neox, pos, L->rope_factors);
+  or_rotate_run_scaled(kslot, L->kv_heads, L->head_dim, L->rope_dim, L->rope_base, L->neox, pos,
+                       L->rope_factors);
   if (f16_store) {
     for (int32_t i = 0; i < kvw; i++) {
       kslot[i] = f16_round(kslot[i]);

@@ -55,6 +55,9 @@ void or_rope_steps(float* steps, int32_t dim, float base);
 void or_rope_angle(int32_t dim, float base, int32_t pos, int32_t pair, float* c, float* s);
 void or_rotate_run(float* x, int32_t heads, int32_t head_dim, int32_t dim,
                    float base, int32_t neox, int32_t pos);
+void or_rope_angle_scaled(int32_t dim, float base, int32_t pos, int32_t pair, float freq, float* c, float* s);
+void or_rotate_run_scaled(float* x, int32_t heads, int32_t head_dim, int32_t dim,
+                          float base, int32_t neox, int32_t pos, const float* factors);
 
 /* attention.mojo:144 attend, contiguous run of `count` positions, no window,
  * no sinks, no softcap.  scores: scratch of `count` floats. */
@@ -76,6 +79,7 @@ typedef struct {
   const float* attn_norm;
   const float* ffn_norm;
   or_weight wq, wk, wv, wo, gate, up, down;
+  const float* rope_factors; /* rope_dim/2 per-pair factors (rope_freqs.weight) or NULL */
 } or_layer;
 
 /* block.mojo:466 layer (attention_layer :319 + mlp_layer :429), in place on x.

@@ -35,6 +35,8 @@ def make_layer_weights(spec, seed):
 
 
 def device_layer_from(host, spec):
+    """(BlockSpec, DeviceLayer) holding the host dict's weights (and its
+    rope_factors, when present) on the device."""
     from molla_amd import block, gpu
     bs = block.BlockSpec(width=spec["width"], hidden=spec["hidden"], heads=spec["heads"],
                          kv_heads=spec["kv_heads"], head_dim=spec["head_dim"], rope_dim=spec["rope_dim"],
@@ -42,8 +44,10 @@ def device_layer_from(host, spec):
     weights = {n: gpu.Tensor.from_bytes(torch.from_numpy(host[n][3]), oracle.Q4_K, host[n][2], host[n][1])
                for n in block.DeviceLayer.NAMES}
     steps = torch.from_numpy(gpu.rope_steps(spec["rope_dim"], spec["rope_base"])).cuda()
+    factors = host.get("rope_factors")
+    factors = None if factors is None else torch.from_numpy(factors).cuda()
     return bs, block.DeviceLayer(bs, torch.from_numpy(host["attn_norm"]).cuda(),
-                                 torch.from_numpy(host["ffn_norm"]).cuda(), weights, steps)
+                                 torch.from_numpy(host["ffn_norm"]).cuda(), weights, steps, factors)
 
 
 def spec_of(width, hidden, heads, kv_heads, head_dim, base=500000.0):
@@ -51,17 +55,27 @@ def spec_of(width, hidden, heads, kv_heads, head_dim, base=500000.0):
                 neox=0, eps=1e-5, rope_base=base, attn_scale=float(np.float32(1 / math.sqrt(head_dim))))
 
 
-@pytest.mark.parametrize("dims,pos,tokens", [
-    ((256, 512, 4, 2, 64), 0, 1),
-    ((256, 512, 4, 2, 64), 37, 1),
-    ((512, 1024, 8, 2, 64), 300, 3),
-    ((4096, 14336, 32, 8, 128), 4096, 1),   # config 4
+def llama31_factors(pairs):
+    """Per-pair rope factors shaped like a Llama 3.1 file's rope_freqs.weight:
+    1 for the fast pairs, rising to 8 for the slow ones."""
+    return np.concatenate([np.ones(pairs - pairs // 2), np.linspace(1.5, 8.0, pairs // 2)]).astype(np.float32)
+
+
+@pytest.mark.parametrize("dims,pos,tokens,factors", [
+    ((256, 512, 4, 2, 64), 0, 1, False),
+    ((256, 512, 4, 2, 64), 37, 1, False),
+    ((256, 512, 4, 2, 64), 37, 1, True),
+    ((512, 1024, 8, 2, 64), 300, 3, False),
+    ((512, 1024, 8, 2, 64), 300, 3, True),
+    ((4096, 14336, 32, 8, 128), 4096, 1, False),   # config 4
 ])
-def test_layer_matches_oracle(dims, pos, tokens):
+def test_layer_matches_oracle(dims, pos, tokens, factors):
     from molla_amd import block, gpu
     ctx = gpu.DeviceContext(0)
     spec = spec_of(*dims)
     host = make_layer_weights(spec, 7)
+    if factors:
+        host["rope_factors"] = llama31_factors(spec["rope_dim"] // 2)
     bs, layer = device_layer_from(host, spec)
     kvw = bs.kv_width()
     count = pos + 1

@@ -311,6 +311,21 @@ def test_rope_plain_and_adjacent_pairs():
     assert (part[4:] == fresh[4:]).all() and part[0] != 1.0
 
 
+def test_rope_per_pair_factors():
+    # tests/test_rope.mojo:321-373: Llama 3.1's rope_freqs.weight divides each
+    # pair's angle by its own factor; factors of one are no scaling at all.
+    # RopeSpec(8, 10000.0) is half-split pairing (neox), the default there.
+    x = np.arange(1, 9, dtype=np.float32)
+    got = oracle.rotate(x, 1, 8, 8, 10000.0, True, 3, factors=[1.0, 2.0, 4.0, 8.0])
+    want = [-1.6955925, 1.0809134, 2.9474161, 3.9969997, -4.8088425, 6.2315027, 7.0223029, 8.0014994]
+    assert np.allclose(got, want, atol=1e-5)
+    for neox in (True, False):
+        ones = oracle.rotate(x, 1, 8, 8, 10000.0, neox, 3, factors=[1.0] * 4)
+        assert np.array_equal(ones, oracle.rotate(x, 1, 8, 8, 10000.0, neox, 3))
+    with pytest.raises(ValueError):
+        oracle.rotate(x, 1, 8, 8, 10000.0, True, 3, factors=[1.0])
+
+
 def test_rope_steps():
     # tests/test_rope.mojo:420-457: one step per pair, first is 1, falling.
     steps = oracle.rope_steps(64, 10000.0)
