@@ -144,6 +144,30 @@ int mi_attend(mi_stream stream, const float* q, const uint16_t* k_cache,
               int32_t head_dim, float scale, int32_t count, float* out,
               void* work, size_t work_bytes);
 
+/* KV cache forms (src/molla/nn/repack.mojo:174-218).  F16: a position is
+ * kv_width halves.  Q8: kv_width signed bytes (q8_0 quants), then kv_width/32
+ * float16 block factors, the row rounded up to a multiple of 8 halves; a
+ * value reads back as float(q) * float(factor).  Rows are counted in halves
+ * at either form: a cache of n positions is n * mi_cache_row(form, kv_width)
+ * halves. */
+enum { MI_CACHE_F16 = 0, MI_CACHE_Q8 = 1 };
+
+/* Halves one position occupies (repack.mojo:221 cache_row), or -1 for an
+ * unknown form or a q8_0 width that is not whole 32-value blocks. */
+int32_t mi_cache_row(int32_t form, int32_t kv_width);
+
+/* mi_store_kv into a cache of either form at position slot (a q8_0 row is
+ * encoded by gpu_ops.mojo:1531 store_kv_q8_kernel's rule: factor amax/127
+ * stored as a half, quants rounded half away from zero). */
+int mi_store_kv_form(mi_stream stream, int32_t form, const float* k, const float* v, int32_t kv_width,
+                     uint16_t* k_cache, uint16_t* v_cache, int32_t slot);
+
+/* mi_attend over a cache of either form (gpu_ops.mojo:678 attend_kernel's
+ * `form`); same workspace. */
+int mi_attend_form(mi_stream stream, int32_t form, const float* q, const uint16_t* k_cache,
+                   const uint16_t* v_cache, int32_t heads, int32_t kv_heads, int32_t head_dim, float scale,
+                   int32_t count, float* out, void* work, size_t work_bytes);
+
 /* Index of the maximum of x[t*n : (t+1)*n] for each t, ties to the lower
  * index (kernel.mojo:571 argmax, gpu_ops.mojo:408). out: device int32[tokens]. */
 int mi_argmax(mi_stream stream, const float* x, int32_t n, int32_t tokens, int32_t* out);
@@ -177,6 +201,8 @@ typedef struct {
   const float* rope_factors; /* device f32[rope_dim/2]: rope_freqs.weight of a
                                 Llama 3.1 file (each pair's angle is divided by
                                 its factor, rope.mojo:253), or NULL for none */
+  int32_t cache_form;        /* MI_CACHE_F16 (0, the default) or MI_CACHE_Q8; the
+                                caches' cache_stride counts halves either way */
 } mi_layer_desc;
 
 /* One Llama layer for `tokens` independent sequences (batch decode, one token

@@ -25,7 +25,7 @@ class MiLayerDesc(ctypes.Structure):
                 ("rope_dim", I32), ("neox", I32), ("eps", F), ("attn_scale", F), ("attn_norm", P),
                 ("ffn_norm", P), ("rope_steps", P)] + \
                [(n, MiWeight) for n in ("wq", "wk", "wv", "wo", "gate", "up", "down")] + \
-               [("rope_factors", P)]
+               [("rope_factors", P), ("cache_form", I32)]
 
 
 # Every symbol include/molla_mi.h declares, with its C signature.
@@ -47,6 +47,9 @@ SIGNATURES = {
     "mi_store_kv": (ctypes.c_int, [P, P, P, I32, P, P, I32]),
     "mi_attend_workspace": (SZ, [I32, I32, I32]),
     "mi_attend": (ctypes.c_int, [P, P, P, P, I32, I32, I32, F, I32, P, P, SZ]),
+    "mi_cache_row": (I32, [I32, I32]),
+    "mi_store_kv_form": (ctypes.c_int, [P, I32, P, P, I32, P, P, I32]),
+    "mi_attend_form": (ctypes.c_int, [P, I32, P, P, P, I32, I32, I32, F, I32, P, P, SZ]),
     "mi_argmax": (ctypes.c_int, [P, P, I32, I32, P]),
     "mi_embed": (ctypes.c_int, [P, P, I32, I32, P, I32, P]),
     "mi_layer_workspace": (SZ, [ctypes.POINTER(MiLayerDesc), I32, I32]),

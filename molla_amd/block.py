@@ -81,17 +81,26 @@ def layer_workspace(layer: DeviceLayer, max_count: int, tokens: int) -> int:
     return lib().mi_layer_workspace(ctypes.byref(layer.desc), max_count, tokens)
 
 
+def with_cache_form(desc: MiLayerDesc, form: int) -> MiLayerDesc:
+    """A copy of a layer descriptor reading and writing a cache of this form."""
+    d = MiLayerDesc.from_buffer_copy(desc)
+    d.cache_form = form
+    return d
+
+
 def device_layer(ctx: gpu.DeviceContext, layer: DeviceLayer, x: torch.Tensor, k_cache: torch.Tensor,
                  v_cache: torch.Tensor, cache_stride: int, pos: torch.Tensor, max_count: int, tokens: int = 1,
-                 work: torch.Tensor | None = None) -> None:
+                 work: torch.Tensor | None = None, form: int = gpu.CACHE_F16) -> None:
     """gpu_block.mojo:899 device_layer, in place on x ([tokens, width] f32).
 
     pos: device int32[tokens], the position (= cache slot) of each sequence's
-    token; max_count bounds pos + 1."""
+    token; max_count bounds pos + 1.  form: the caches' form (gpu.CACHE_F16 or
+    CACHE_Q8); cache_stride counts halves (sequences * cache_row apart)."""
     need = layer_workspace(layer, max_count, tokens)
     if work is None:
         work = ctx.workspace(need)
-    check(lib().mi_decoder_layer(ctx.handle, ctypes.byref(layer.desc), x.data_ptr(), k_cache.data_ptr(),
+    desc = layer.desc if form == gpu.CACHE_F16 else with_cache_form(layer.desc, form)
+    check(lib().mi_decoder_layer(ctx.handle, ctypes.byref(desc), x.data_ptr(), k_cache.data_ptr(),
                                  v_cache.data_ptr(), cache_stride, pos.data_ptr(), max_count, tokens,
                                  work.data_ptr(), work.numel()))
 
@@ -119,11 +128,15 @@ class DeviceSession:
     """KV caches and scratch for `batch` sequences decoding together
     (engine/device.mojo:194 DeviceKvCache + :809 DeviceSession)."""
 
-    def __init__(self, ctx: gpu.DeviceContext, model: DeviceModel, batch: int, context: int):
+    def __init__(self, ctx: gpu.DeviceContext, model: DeviceModel, batch: int, context: int,
+                 cache_form: int = gpu.CACHE_F16):
         self.ctx, self.model, self.batch, self.context = ctx, model, batch, context
         s = model.spec
         kvw = s.kv_width()
-        self.cache_stride = context * kvw
+        # f16 or q8_0 caches (repack.mojo:174-218), held as halves either way
+        self.cache_form = cache_form
+        self.cache_stride = context * gpu.cache_row(cache_form, kvw)
+        self.descs = [with_cache_form(l.desc, cache_form) for l in model.layers]
         dev = ctx.device
         self.k = [torch.empty(batch * self.cache_stride, dtype=torch.float16, device=dev) for _ in model.layers]
         self.v = [torch.empty(batch * self.cache_stride, dtype=torch.float16, device=dev) for _ in model.layers]
@@ -145,7 +158,7 @@ class DeviceSession:
         check(L.mi_embed(c.handle, m.embedding.data_ptr(), m.embedding.shape[0], s.width, self.ids.data_ptr(),
                          self.batch, self.x.data_ptr()))
         for i, layer in enumerate(m.layers):
-            check(L.mi_decoder_layer(c.handle, ctypes.byref(layer.desc), self.x.data_ptr(), self.k[i].data_ptr(),
+            check(L.mi_decoder_layer(c.handle, ctypes.byref(self.descs[i]), self.x.data_ptr(), self.k[i].data_ptr(),
                                      self.v[i].data_ptr(), self.cache_stride, self.pos.data_ptr(), self.context,
                                      self.batch, self.work.data_ptr(), self.work.numel()))
         xq = self.work.data_ptr()

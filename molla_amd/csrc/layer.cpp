@@ -74,6 +74,9 @@ int check_desc(const mi_layer_desc* d) {
     return fail(MI_ERR_SHAPE, "layer: %d query heads per key head is not 1, 2, 4 or 8", group);
   if (d->head_dim <= 0 || d->head_dim % 32 || d->head_dim > 512)
     return fail(MI_ERR_SHAPE, "layer: head_dim %d", d->head_dim);
+  if (cache_row(d->cache_form, d->kv_heads * d->head_dim) < 0)
+    return fail(MI_ERR_SHAPE, "layer: cache form %d has no row for %d key heads of %d", d->cache_form, d->kv_heads,
+                d->head_dim);
   if (d->rope_dim <= 0 || d->rope_dim % 2 || d->rope_dim > d->head_dim)
     return fail(MI_ERR_SHAPE, "layer: rope_dim %d in heads of %d", d->rope_dim, d->head_dim);
   if (!(d->eps > 0.0f)) return fail(MI_ERR_ARG, "layer: a norm epsilon has to be positive");
@@ -118,7 +121,8 @@ int mi_decoder_layer(mi_stream stream, const mi_layer_desc* d, float* resid, uin
   if (tokens < 1 || tokens > kMaxTokens) return fail(MI_ERR_ARG, "layer: tokens %d outside 1..8", tokens);
   if (max_count <= 0) return fail(MI_ERR_SHAPE, "layer: max_count must be positive");
   const int64_t kvw = (int64_t)d->kv_heads * d->head_dim;
-  if (tokens > 1 && cache_stride < (int64_t)max_count * kvw)
+  const int64_t crow = cache_row(d->cache_form, (int32_t)kvw);  // halves per position
+  if (tokens > 1 && cache_stride < (int64_t)max_count * crow)
     return fail(MI_ERR_SHAPE, "layer: cache stride %lld holds fewer than %d slots", (long long)cache_stride,
                 max_count);
   const Carve c = carve(d, max_count, tokens);
@@ -151,7 +155,8 @@ int mi_decoder_layer(mi_stream stream, const mi_layer_desc* d, float* resid, uin
     sg.end[2] = qw + 2 * (int32_t)kvw;
     sg.nseg = 3;
   }
-  if (fused_qkv && !d->neox && q4k_qkv_rope_fits(d->width, d->head_dim, d->rope_dim)) {
+  const bool q8 = d->cache_form == MI_CACHE_Q8;
+  if (fused_qkv && !d->neox && !q8 && q4k_qkv_rope_fits(d->width, d->head_dim, d->rope_dim)) {
     // norm (plus this position's rope table), then q|k|v with the rope and
     // the cache store in its epilogue: no separate rope launch
     float* trig = (float*)(base + c.trig);
@@ -200,14 +205,25 @@ int mi_decoder_layer(mi_stream stream, const mi_layer_desc* d, float* resid, uin
                               qkv + qw + kvw, qkv_stride, MI_EPI_NONE, nullptr)))
         return rc;
     }
-    if ((rc = launch_rope_store(s, qkv, d->heads, d->kv_heads, d->head_dim, d->rope_dim, d->neox,
-                                d->rope_steps, pos, tokens, qkv_stride, k_cache, v_cache, cache_stride,
-                                d->rope_factors)))
+    if (q8) {
+      // a q8_0 cache: q and k rotated in place (adjacent in the fused row),
+      // then k and v encoded a 32-value block per half-wave
+      if ((rc = launch_rope(s, qkv, d->heads + d->kv_heads, d->head_dim, d->rope_dim, d->neox, d->rope_steps,
+                            pos, tokens, qkv_stride, d->rope_factors)))
+        return rc;
+      if ((rc = launch_store_kv(s, qkv + qw, qkv + qw + kvw, (int32_t)kvw, k_cache, v_cache, pos, 0, tokens,
+                                qkv_stride, cache_stride, MI_CACHE_Q8)))
+        return rc;
+    } else if ((rc = launch_rope_store(s, qkv, d->heads, d->kv_heads, d->head_dim, d->rope_dim, d->neox,
+                                       d->rope_steps, pos, tokens, qkv_stride, k_cache, v_cache, cache_stride,
+                                       d->rope_factors))) {
       return rc;
+    }
   }
   // count = pos + 1 per sequence: the attention kernels read pos and add one.
   if ((rc = launch_attend(s, qkv, qkv_stride, k_cache, v_cache, cache_stride, d->heads, d->kv_heads,
-                          d->head_dim, d->attn_scale, pos, -1, max_count, tokens, nullptr, xq, attn)))
+                          d->head_dim, d->attn_scale, pos, -1, max_count, tokens, nullptr, xq, attn,
+                          d->cache_form)))
     return rc;
   if ((rc = launch_matvec(s, d->wo.kind, d->wo.data, d->wo.row_bytes, d->width, qw, xq, tokens, resid,
                           d->width, MI_EPI_ADD, nullptr)))

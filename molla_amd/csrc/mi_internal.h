@@ -113,9 +113,18 @@ int launch_rms_norm(hipStream_t s, const float* x, const float* gain, int32_t n,
 int launch_rope(hipStream_t s, float* x, int32_t heads, int32_t head_dim, int32_t dim, int32_t neox,
                 const float* steps, const int32_t* pos, int32_t tokens, int64_t row_stride,
                 const float* factors = nullptr);
+// Halves one cached position occupies at a cache form (repack.mojo:221
+// cache_row); -1 for an unknown form or a q8_0 width of partial blocks.
+__host__ __device__ inline int32_t cache_row(int32_t form, int32_t kv_width) {
+  if (kv_width <= 0) return -1;
+  if (form == MI_CACHE_F16) return kv_width;
+  if (form != MI_CACHE_Q8 || kv_width % 32) return -1;
+  return (kv_width / 2 + kv_width / 32 + 7) / 8 * 8;
+}
+// cache_stride: halves from one sequence's cache to the next; form: MI_CACHE_*.
 int launch_store_kv(hipStream_t s, const float* k, const float* v, int32_t kv_width,
                     uint16_t* k_cache, uint16_t* v_cache, const int32_t* slot_dev, int32_t slot_host,
-                    int32_t tokens, int64_t src_stride, int64_t cache_stride);
+                    int32_t tokens, int64_t src_stride, int64_t cache_stride, int32_t form = MI_CACHE_F16);
 // Rotate q and k heads of a fused qkv row and store k (rotated) and v into
 // the half caches at slot pos[t]; q is rotated in place.
 int launch_rope_store(hipStream_t s, float* qkv, int32_t heads, int32_t kv_heads, int32_t head_dim,
@@ -126,7 +135,8 @@ size_t attend_workspace(int32_t heads, int32_t head_dim, int32_t max_count, int3
 int launch_attend(hipStream_t s, const float* q, int64_t q_stride, const uint16_t* k_cache,
                   const uint16_t* v_cache, int64_t cache_stride, int32_t heads, int32_t kv_heads,
                   int32_t head_dim, float scale, const int32_t* pos_dev, int32_t count_host,
-                  int32_t max_count, int32_t tokens, float* out, void* xq_out, void* work);
+                  int32_t max_count, int32_t tokens, float* out, void* xq_out, void* work,
+                  int32_t form = MI_CACHE_F16);
 int launch_argmax(hipStream_t s, const float* x, int32_t n, int32_t tokens, int32_t* out);
 int launch_embed(hipStream_t s, const float* emb, int32_t vocab, int32_t width, const int32_t* ids,
                  int32_t tokens, float* out);

@@ -222,6 +222,11 @@ constexpr int kAttnThreads = 256;
 __host__ __device__ __forceinline__ int attn_slice(int head_dim) {
   return head_dim <= 128 ? 64 : (head_dim <= 256 ? 32 : 16);
 }
+__host__ __device__ __forceinline__ size_t attn_q8_lds_bytes(int head_dim, int group) {
+  const int kk = attn_slice(head_dim);
+  return (size_t)kk * (head_dim + 16) + (size_t)kk * head_dim + (size_t)2 * kk * (head_dim / 32) * 4 +
+         (size_t)group * head_dim * 4 + (size_t)group * kk * 4;
+}
 __host__ __device__ __forceinline__ size_t attn_lds_bytes(int head_dim, int group) {
   const int kk = attn_slice(head_dim);
   return (size_t)kk * (head_dim + 8) * 2 + (size_t)kk * head_dim * 2 + (size_t)group * head_dim * 4 +
@@ -350,6 +355,157 @@ __global__ __launch_bounds__(kAttnThreads) void attend_split_kernel(
     }
     *(float2*)(part_acc + (slot_base + (int64_t)g * max_chunks) * D + 2 * e) = make_float2(a0, a1);
   }
+}
+
+// The same slice over a q8_0 cache (repack.mojo:181 CACHE_Q8): a position's
+// row is kv_width signed bytes, then kv_width/32 float16 factors, `row`
+// halves in all.  Quants and factors are staged in LDS as they are (half the
+// bytes of the f16 form); a key or value element is read as float(q) *
+// float(factor), which is gpu.mojo:1168 cache_load, and then used exactly
+// as the f16 kernel uses a widened half.
+template <int GROUP>
+__global__ __launch_bounds__(kAttnThreads) void attend_split_q8_kernel(
+    const float* __restrict__ q, int64_t q_stride, const __half* __restrict__ kc,
+    const __half* __restrict__ vc, int64_t cache_stride, int row, int heads, int kv_heads, int head_dim,
+    float scale, const int32_t* __restrict__ pos_dev, int count_host, int max_chunks,
+    float* __restrict__ part_acc, float* __restrict__ part_ml) {
+#pragma clang fp contract(off)
+  const int c = blockIdx.x, kvh = blockIdx.y, t = blockIdx.z;
+  const int count = pos_dev ? pos_dev[t] + 1 : count_host;
+  const int kk = attn_slice(head_dim);
+  const int start = c * kk;
+  if (start >= count) return;
+  const int D = head_dim, KQ = head_dim + 16, NB = head_dim >> 5;  // LDS key rows padded by 16 bytes
+  const int nk = min(kk, count - start);
+  const int kvw = kv_heads * D;
+  extern __shared__ uint4 lds4[];
+  int8_t* Kq = (int8_t*)lds4;
+  int8_t* Vq = Kq + kk * KQ;
+  float* Ksc = (float*)(Vq + kk * D);
+  float* Vsc = Ksc + kk * NB;
+  float* Qs = Vsc + kk * NB;
+  float* Ps = Qs + GROUP * D;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+
+  const __half* kseq = kc + (int64_t)t * cache_stride;
+  const __half* vseq = vc + (int64_t)t * cache_stride;
+  // quants in 16-byte pieces, every load of the slice issued before any
+  // LDS store; keys past the end repeat the last live one (masked below)
+  const int pieces = D >> 4;
+  const int total = kk * pieces;
+  const float4* q4 = (const float4*)(q + (int64_t)t * q_stride + (int64_t)kvh * GROUP * D);
+  const int nq4 = GROUP * D / 4;
+  const float4 qv = q4[min(tid, nq4 - 1)];
+  for (int b0 = 0; b0 < total; b0 += kAttnThreads * 2) {
+    uint4 kv[2], vv[2];
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+      const int i = min(b0 + tid + j * kAttnThreads, total - 1);
+      const int key = min(i / pieces, nk - 1), pc = i % pieces;
+      const int64_t off = (int64_t)(start + key) * row * 2 + (int64_t)kvh * D + pc * 16;  // bytes
+      kv[j] = *(const uint4*)((const int8_t*)kseq + off);
+      vv[j] = *(const uint4*)((const int8_t*)vseq + off);
+    }
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+      const int i = b0 + tid + j * kAttnThreads;
+      const int key = i / pieces, pc = i % pieces;
+      if (i < total) {
+        *(uint4*)(Kq + key * KQ + pc * 16) = kv[j];
+        *(uint4*)(Vq + key * D + pc * 16) = vv[j];
+      }
+    }
+  }
+  for (int i = tid; i < kk * NB; i += kAttnThreads) {
+    const int key = min(i / NB, nk - 1), b = i % NB;
+    const int64_t at = (int64_t)(start + key) * row + (kvw >> 1) + (kvh * D >> 5) + b;  // halves
+    Ksc[i] = __half2float(kseq[at]);
+    Vsc[i] = __half2float(vseq[at]);
+  }
+  if (tid < nq4) ((float4*)Qs)[tid] = qv;
+  for (int i = tid + kAttnThreads; i < nq4; i += kAttnThreads) ((float4*)Qs)[i] = q4[i];
+  __syncthreads();
+
+  const int64_t slot_base = ((int64_t)t * heads + (int64_t)kvh * GROUP) * max_chunks + c;
+  for (int g = wave; g < GROUP; g += kAttnThreads / kWave) {
+    float sdot = 0.0f;
+    if (lane < kk) {
+      const int8_t* kr = Kq + lane * KQ;
+      const float* qg = Qs + g * D;
+      for (int d = 0; d < D; d += 16) {
+        const uint4 raw = *(const uint4*)(kr + d);
+        const int8_t* b = (const int8_t*)&raw;
+        const float f = Ksc[lane * NB + (d >> 5)];
+#pragma unroll
+        for (int i = 0; i < 16; i++) sdot = fmaf(qg[d + i], (float)b[i] * f, sdot);
+      }
+    }
+    const bool live = lane < nk;
+    const float sc = live ? sdot * scale : -INFINITY;
+    float m = sc;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    const float pr = live ? expf(sc - m) : 0.0f;
+    float l = pr;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) l += __shfl_xor(l, o);
+    if (lane < kk) Ps[g * kk + lane] = pr;
+    if (lane == 0) {
+      part_ml[(slot_base + (int64_t)g * max_chunks) * 2 + 0] = m;
+      part_ml[(slot_base + (int64_t)g * max_chunks) * 2 + 1] = l;
+    }
+  }
+  __syncthreads();
+  const int halfD = D >> 1;
+  for (int o = tid; o < GROUP * halfD; o += kAttnThreads) {
+    const int g = o / halfD, e = o - g * halfD;
+    const float* pg = Ps + g * kk;
+    const int b = (2 * e) >> 5;
+    float a0 = 0.0f, a1 = 0.0f;
+    for (int k = 0; k < nk; k += 4) {
+      const float4 p4 = *(const float4*)(pg + k);
+      const float pk[4] = {p4.x, p4.y, p4.z, p4.w};
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const char2 v = *(const char2*)(Vq + (k + j) * D + 2 * e);
+        const float f = Vsc[(k + j) * NB + b];
+        a0 = fmaf(pk[j], (float)v.x * f, a0);
+        a1 = fmaf(pk[j], (float)v.y * f, a1);
+      }
+    }
+    *(float2*)(part_acc + (slot_base + (int64_t)g * max_chunks) * D + 2 * e) = make_float2(a0, a1);
+  }
+}
+
+// f32 k / v rows -> q8_0 cache rows (gpu_ops.mojo:1531 store_kv_q8_kernel):
+// each 32-lane half-wave encodes one block: factor amax / 127 stored as a
+// half after the row's quants, quants round(v * 127 / amax) half away from
+// zero, clamped to [-127, 127].  Grid: (blocks of 8 per 256 threads, tokens, 2
+// for k then v).
+__global__ __launch_bounds__(256) void store_kv_q8_kernel(const float* __restrict__ k, const float* __restrict__ v,
+                                                          int kv_width, __half* __restrict__ kc,
+                                                          __half* __restrict__ vc, const int32_t* __restrict__ slot_dev,
+                                                          int slot_host, int64_t src_stride, int64_t cache_stride,
+                                                          int row) {
+#pragma clang fp contract(off)
+  const int t = blockIdx.y;
+  const bool isv = blockIdx.z == 1;
+  const int lane32 = threadIdx.x & 31;
+  const int b = (blockIdx.x * blockDim.x + threadIdx.x) >> 5;  // block of the row
+  const int nb = kv_width >> 5;
+  if (b >= nb) return;  // whole half-waves leave together
+  const int slot = slot_dev ? slot_dev[t] : slot_host;
+  const float x = (isv ? v : k)[(int64_t)t * src_stride + b * 32 + lane32];
+  float amax = fabsf(x);
+#pragma unroll
+  for (int m = 16; m >= 1; m >>= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 32));
+  const float inv = amax == 0.0f ? 0.0f : 127.0f / amax;
+  const float y = x * inv;
+  const float r = y >= 0.0f ? y + 0.5f : y - 0.5f;
+  const int qi = max(-127, min(127, (int)r));
+  __half* rowp = (isv ? vc : kc) + (int64_t)t * cache_stride + (int64_t)slot * row;
+  ((int8_t*)rowp)[b * 32 + lane32] = (int8_t)qi;
+  if (lane32 == 0) rowp[(kv_width >> 1) + b] = __float2half_rn(amax / 127.0f);
 }
 
 // One block per (query head, token); thread d owns output dimension d (the
@@ -543,7 +699,14 @@ int launch_rope_store(hipStream_t s, float* qkv, int32_t heads, int32_t kv_heads
 
 int launch_store_kv(hipStream_t s, const float* k, const float* v, int32_t kv_width,
                     uint16_t* k_cache, uint16_t* v_cache, const int32_t* slot_dev, int32_t slot_host,
-                    int32_t tokens, int64_t src_stride, int64_t cache_stride) {
+                    int32_t tokens, int64_t src_stride, int64_t cache_stride, int32_t form) {
+  if (form == MI_CACHE_Q8) {
+    dim3 grid((kv_width / 32 + 7) / 8, tokens, 2);
+    hipLaunchKernelGGL(store_kv_q8_kernel, grid, dim3(256), 0, s, k, v, kv_width, (__half*)k_cache,
+                       (__half*)v_cache, slot_dev, slot_host, src_stride, cache_stride,
+                       cache_row(MI_CACHE_Q8, kv_width));
+    return hip_check(hipGetLastError(), "store_kv_q8 launch");
+  }
   dim3 grid((kv_width + 255) / 256, tokens);
   hipLaunchKernelGGL(store_kv_kernel, grid, dim3(256), 0, s, k, v, kv_width, (__half*)k_cache,
                      (__half*)v_cache, slot_dev, slot_host, src_stride, cache_stride);
@@ -561,7 +724,7 @@ size_t attend_workspace(int32_t heads, int32_t head_dim, int32_t max_count, int3
 int launch_attend(hipStream_t s, const float* q, int64_t q_stride, const uint16_t* k_cache,
                   const uint16_t* v_cache, int64_t cache_stride, int32_t heads, int32_t kv_heads,
                   int32_t head_dim, float scale, const int32_t* pos_dev, int32_t count_host,
-                  int32_t max_count, int32_t tokens, float* out, void* xq_out, void* work) {
+                  int32_t max_count, int32_t tokens, float* out, void* xq_out, void* work, int32_t form) {
   const int kk = attn_slice(head_dim);
   const int chunks = (max_count + kk - 1) / kk;
   const int64_t slots = (int64_t)tokens * heads * chunks;
@@ -569,14 +732,21 @@ int launch_attend(hipStream_t s, const float* q, int64_t q_stride, const uint16_
   const size_t acc_bytes = ((size_t)slots * head_dim * sizeof(float) + 255) & ~(size_t)255;
   float* part_ml = (float*)((char*)work + acc_bytes);
   const int group = heads / kv_heads;
-  const size_t shmem = attn_lds_bytes(head_dim, group);
   dim3 grid(chunks, kv_heads, tokens);
   const __half* kc = (const __half*)k_cache;
   const __half* vc = (const __half*)v_cache;
-#define MI_ATTEND(G)                                                                                  \
-  hipLaunchKernelGGL(attend_split_kernel<G>, grid, dim3(kAttnThreads), shmem, s, q, q_stride, kc, vc,   \
-                     cache_stride, heads, kv_heads, head_dim, scale, pos_dev, count_host, chunks,     \
-                     part_acc, part_ml)
+  const bool q8 = form == MI_CACHE_Q8;
+  const int row = cache_row(form, kv_heads * head_dim);
+  const size_t shmem = q8 ? attn_q8_lds_bytes(head_dim, group) : attn_lds_bytes(head_dim, group);
+#define MI_ATTEND(G)                                                                                       \
+  if (q8)                                                                                                  \
+    hipLaunchKernelGGL(attend_split_q8_kernel<G>, grid, dim3(kAttnThreads), shmem, s, q, q_stride, kc, vc,  \
+                       cache_stride, row, heads, kv_heads, head_dim, scale, pos_dev, count_host, chunks,    \
+                       part_acc, part_ml);                                                                 \
+  else                                                                                                     \
+    hipLaunchKernelGGL(attend_split_kernel<G>, grid, dim3(kAttnThreads), shmem, s, q, q_stride, kc, vc,     \
+                       cache_stride, heads, kv_heads, head_dim, scale, pos_dev, count_host, chunks,         \
+                       part_acc, part_ml)
   switch (group) {
     case 1: MI_ATTEND(1); break;
     case 2: MI_ATTEND(2); break;

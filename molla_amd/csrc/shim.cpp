@@ -192,6 +192,19 @@ int mi_store_kv(mi_stream stream, const float* k, const float* v, int32_t kv_wid
   return launch_store_kv((hipStream_t)stream, k, v, kv_width, k_cache, v_cache, nullptr, slot, 1, kv_width, 0);
 }
 
+int32_t mi_cache_row(int32_t form, int32_t kv_width) { return cache_row(form, kv_width); }
+
+int mi_store_kv_form(mi_stream stream, int32_t form, const float* k, const float* v, int32_t kv_width,
+                     uint16_t* k_cache, uint16_t* v_cache, int32_t slot) {
+  if (!k || !v || !k_cache || !v_cache) return fail(MI_ERR_ARG, "store_kv: null pointer");
+  if (slot < 0 || cache_row(form, kv_width) < 0)
+    return fail(MI_ERR_SHAPE, "store_kv: cache form %d has no row of width %d (or slot %d)", form, kv_width, slot);
+  if (form == MI_CACHE_Q8 && (((uintptr_t)k_cache | (uintptr_t)v_cache) & 15))
+    return fail(MI_ERR_ALIGN, "store_kv: a q8_0 cache must be 16-byte aligned");
+  return launch_store_kv((hipStream_t)stream, k, v, kv_width, k_cache, v_cache, nullptr, slot, 1, kv_width, 0,
+                         form);
+}
+
 size_t mi_attend_workspace(int32_t heads, int32_t head_dim, int32_t count) {
   if (heads <= 0 || head_dim <= 0 || count <= 0) return 0;
   return attend_workspace(heads, head_dim, count, 1);
@@ -211,7 +224,15 @@ static int check_attn(const char* name, int32_t heads, int32_t kv_heads, int32_t
 int mi_attend(mi_stream stream, const float* q, const uint16_t* k_cache, const uint16_t* v_cache,
               int32_t heads, int32_t kv_heads, int32_t head_dim, float scale, int32_t count, float* out,
               void* work, size_t work_bytes) {
+  return mi_attend_form(stream, MI_CACHE_F16, q, k_cache, v_cache, heads, kv_heads, head_dim, scale, count, out,
+                        work, work_bytes);
+}
+
+int mi_attend_form(mi_stream stream, int32_t form, const float* q, const uint16_t* k_cache,
+                   const uint16_t* v_cache, int32_t heads, int32_t kv_heads, int32_t head_dim, float scale,
+                   int32_t count, float* out, void* work, size_t work_bytes) {
   if (!q || !k_cache || !v_cache || !out) return fail(MI_ERR_ARG, "attend: null pointer");
+  if (cache_row(form, kv_heads * head_dim) < 0) return fail(MI_ERR_SHAPE, "attend: unknown cache form %d", form);
   int rc = check_attn("attend", heads, kv_heads, head_dim);
   if (rc) return rc;
   if (count <= 0) return fail(MI_ERR_SHAPE, "attention needs at least one key to look at");
@@ -221,7 +242,7 @@ int mi_attend(mi_stream stream, const float* q, const uint16_t* k_cache, const u
     return fail(MI_ERR_WORKSPACE, "attend: workspace of %zu bytes, %zu needed", work_bytes,
                 mi_attend_workspace(heads, head_dim, count));
   return launch_attend((hipStream_t)stream, q, (int64_t)heads * head_dim, k_cache, v_cache, 0, heads,
-                       kv_heads, head_dim, scale, nullptr, count, count, 1, out, nullptr, work);
+                       kv_heads, head_dim, scale, nullptr, count, count, 1, out, nullptr, work, form);
 }
 
 int mi_argmax(mi_stream stream, const float* x, int32_t n, int32_t tokens, int32_t* out) {

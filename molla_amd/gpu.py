@@ -196,30 +196,43 @@ def device_rope(ctx: DeviceContext, x: torch.Tensor, heads: int, head_dim: int, 
                         pos.data_ptr(), tokens, stride))
 
 
+CACHE_F16, CACHE_Q8 = 0, 1  # repack.mojo:174-181
+
+
+def cache_row(form: int, kv_width: int) -> int:
+    """repack.mojo:221 cache_row: halves one cached position occupies."""
+    row = lib().mi_cache_row(form, kv_width)
+    if row < 0:
+        raise ValueError(f"cache form {form} has no row of width {kv_width}")
+    return row
+
+
 def device_store_kv(ctx: DeviceContext, k: torch.Tensor, v: torch.Tensor, k_cache: torch.Tensor,
-                    v_cache: torch.Tensor, slot: int) -> None:
-    """gpu_ops.mojo:1582 device_store_kv: f32 rows -> f16 cache at `slot`."""
+                    v_cache: torch.Tensor, slot: int, form: int = CACHE_F16) -> None:
+    """gpu_ops.mojo:1582 device_store_kv: f32 rows -> the cache at `slot`, f16
+    or q8_0 (the caches are torch halves either way, cache_row per slot)."""
     kvw = k.numel()
     if v.numel() != kvw:
         raise ValueError("store_kv wants k and v the same width")
-    if k_cache.numel() < (slot + 1) * kvw or v_cache.numel() < (slot + 1) * kvw:
+    row = cache_row(form, kvw)
+    if k_cache.numel() < (slot + 1) * row or v_cache.numel() < (slot + 1) * row:
         raise ValueError(f"the cache has no room for slot {slot}")
-    check(lib().mi_store_kv(ctx.handle, k.data_ptr(), v.data_ptr(), kvw, k_cache.data_ptr(), v_cache.data_ptr(),
-                            slot))
+    check(lib().mi_store_kv_form(ctx.handle, form, k.data_ptr(), v.data_ptr(), kvw, k_cache.data_ptr(),
+                                 v_cache.data_ptr(), slot))
 
 
 def device_attend(ctx: DeviceContext, q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
                   heads: int, kv_heads: int, head_dim: int, scale: float, count: int,
-                  out: torch.Tensor) -> None:
-    """attention.mojo:144 attend over `count` cached positions of f16 keys/values."""
+                  out: torch.Tensor, form: int = CACHE_F16) -> None:
+    """attention.mojo:144 attend over `count` cached positions (f16 or q8_0 cache)."""
     if count <= 0:
         raise ValueError("attention needs at least one key to look at")
-    if k_cache.numel() < count * kv_heads * head_dim:
+    if k_cache.numel() < count * cache_row(form, kv_heads * head_dim):
         raise ValueError("attention wants more keys than the cache holds")
     need = lib().mi_attend_workspace(heads, head_dim, count)
     work = ctx.workspace(need)
-    check(lib().mi_attend(ctx.handle, q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), heads, kv_heads,
-                          head_dim, scale, count, out.data_ptr(), work.data_ptr(), work.numel()))
+    check(lib().mi_attend_form(ctx.handle, form, q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), heads,
+                               kv_heads, head_dim, scale, count, out.data_ptr(), work.data_ptr(), work.numel()))
 
 
 def device_argmax(ctx: DeviceContext, x: torch.Tensor, n: int, tokens: int = 1) -> torch.Tensor:

@@ -86,6 +86,7 @@ def _declare(l):
         "or_rope_angle": (None, [I32, F, I32, I32, P, P]),
         "or_rotate_run": (None, [P, I32, I32, I32, F, I32, I32]),
         "or_rotate_run_scaled": (None, [P, I32, I32, I32, F, I32, I32, P]),
+        "or_q8_cache_round": (None, [P, I32]),
         "or_attend": (None, [I32, I32, I32, F, P, P, P, I32, P, P]),
         "or_layer_step": (ctypes.c_int, [ctypes.POINTER(Layer), P, P, P, I32, I32, I32, I32]),
         "or_forward": (ctypes.c_int, [ctypes.POINTER(Layer), I32, P, I32, P, ctypes.POINTER(Weight),
@@ -254,19 +255,33 @@ def make_layer(spec: dict, weights: dict, keep: list) -> Layer:
     return L
 
 
+def q8_cache_round(v: np.ndarray) -> np.ndarray:
+    """The values a q8_0 KV cache row holding v reads back (whole 32-blocks)."""
+    v = np.array(v, dtype=np.float32)
+    lib().or_q8_cache_round(_p(v), v.size)
+    return v
+
+
+def _store_form(f16_store, q8_store) -> int:
+    return 2 if q8_store else int(bool(f16_store))
+
+
 def layer_step(L: Layer, x: np.ndarray, keys: np.ndarray, values: np.ndarray, slot: int, pos: int,
-               f16_store: bool = False, threads: int = 1) -> None:
-    """In place on x, keys[slot], values[slot] (f32 caches)."""
+               f16_store: bool = False, threads: int = 1, q8_store: bool = False) -> None:
+    """In place on x, keys[slot], values[slot] (f32 caches).  f16_store /
+    q8_store: the new key and value go through what an f16 / q8_0 device cache
+    holds before they are attended over."""
     for a in (x, keys, values):
         assert a.dtype == np.float32 and a.flags["C_CONTIGUOUS"]
-    rc = lib().or_layer_step(ctypes.byref(L), _p(x), _p(keys), _p(values), slot, pos, int(f16_store), threads)
+    rc = lib().or_layer_step(ctypes.byref(L), _p(x), _p(keys), _p(values), slot, pos,
+                             _store_form(f16_store, q8_store), threads)
     if rc != 0:
         raise ValueError(f"layer refused (rc {rc})")
 
 
 def forward(layers: list, embedding: np.ndarray, output_norm: np.ndarray, output: tuple, token: int,
             pos: int, slot: int, keys: list, values: list, f16_store: bool = False,
-            threads: int = 1) -> np.ndarray:
+            threads: int = 1, q8_store: bool = False) -> np.ndarray:
     n = len(layers)
     arr = (Layer * n)(*layers)
     kind, rows, cols, blob = output
@@ -278,7 +293,8 @@ def forward(layers: list, embedding: np.ndarray, output_norm: np.ndarray, output
     emb = np.ascontiguousarray(embedding, dtype=np.float32)
     onorm = np.ascontiguousarray(output_norm, dtype=np.float32)
     rc = lib().or_forward(arr, n, _p(emb), emb.shape[0], _p(onorm), ctypes.byref(wout), token, pos, slot,
-                          ctypes.cast(kp, ctypes.c_void_p), ctypes.cast(vp, ctypes.c_void_p), int(f16_store),
+                          ctypes.cast(kp, ctypes.c_void_p), ctypes.cast(vp, ctypes.c_void_p),
+                          _store_form(f16_store, q8_store),
                           _p(logits), threads)
     if rc != 0:
         raise ValueError(f"forward refused (rc {rc})")

@@ -602,6 +602,31 @@ static int mv(const or_weight* w, const float* x, float* y, int32_t threads) {
 
 static float f16_round(float v) { return or_f16(or_f32_to_f16(v)); }
 
+/* What a q8_0 cache row holds for n values (gpu_ops.mojo:1531
+ * store_kv_q8_kernel; the host restatement is tests/test_gpu_ops.mojo
+ * _quantize_q8): per 32-value block a factor amax / 127 kept as float16, the
+ * values times 127 / amax rounded half away from zero and clamped to
+ * [-127, 127]; read back as float(q) * float(f16 factor).  In place. */
+void or_q8_cache_round(float* v, int32_t n) {
+  for (int32_t i = 0; i + 32 <= n; i += 32) {
+    float amax = 0.0f;
+    for (int k = 0; k < 32; k++) {
+      float a = v[i + k] < 0 ? -v[i + k] : v[i + k];
+      if (a > amax) amax = a;
+    }
+    float inv = amax == 0.0f ? 0.0f : 127.0f / amax;
+    float s = f16_round(amax / 127.0f);
+    for (int k = 0; k < 32; k++) {
+      float x = v[i + k] * inv;
+      float r = x >= 0 ? x + 0.5f : x - 0.5f;
+      int q = (int)r;
+      if (q > 127) q = 127;
+      if (q < -127) q = -127;
+      v[i + k] = (float)q * s;
+    }
+  }
+}
+
 /* block.mojo:466 layer = attention_layer (:319) then mlp_layer (:429). */
 int or_layer_step(const or_layer* L, float* x, float* keys, float* values,
                   int32_t slot, int32_t pos, int32_t f16_store, int32_t threads) {
@@ -627,7 +652,10 @@ int or_layer_step(const or_layer* L, float* x, float* keys, float* values,
   or_rotate_run_scaled(q, L->heads, L->head_dim, L->rope_dim, L->rope_base, L->neox, pos, L->rope_factors);
   or_rotate_run_scaled(kslot, L->kv_heads, L->head_dim, L->rope_dim, L->rope_base, L->neox, pos,
                        L->rope_factors);
-  if (f16_store) {
+  if (f16_store == 2) {  /* a q8_0 cache */
+    or_q8_cache_round(kslot, kvw);
+    or_q8_cache_round(vslot, kvw);
+  } else if (f16_store) {
     for (int32_t i = 0; i < kvw; i++) {
       kslot[i] = f16_round(kslot[i]);
       vslot[i] = f16_round(vslot[i]);

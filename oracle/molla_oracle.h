@@ -84,9 +84,13 @@ typedef struct {
 
 /* block.mojo:466 layer (attention_layer :319 + mlp_layer :429), in place on x.
  * keys/values: f32 cache, one row of kv_heads*head_dim per slot.  When
- * f16_store is set the freshly rotated key and the value are rounded through
+ * f16_store is 1 the freshly rotated key and the value are rounded through
  * float16 before attending, which is what a device cache of halves holds.
  * threads as for or_matvec.  Returns 0 or a negative error. */
+/* The values a q8_0 KV cache row reads back (float(q) * f16 factor per
+ * 32-value block), in place; or_layer_step does this to the new key and value
+ * when f16_store is 2. */
+void or_q8_cache_round(float* v, int32_t n);
 int or_layer_step(const or_layer* L, float* x, float* keys, float* values,
                   int32_t slot, int32_t pos, int32_t f16_store, int32_t threads);
 

@@ -32,13 +32,27 @@ def test_library_exports_every_declared_symbol():
 
 def test_geometry_matches_reference_table():
     lib = _lib.lib()
-    for kind in (2, 8, 12, 14):
+    for kind in (2, 3, 6, 7, 8, 12, 13, 14):
         assert lib.mi_block_elements(kind) == oracle.block_elements(kind)
         assert lib.mi_block_bytes(kind) == oracle.block_bytes(kind)
     assert lib.mi_row_bytes(12, 4096) == 2304
     assert lib.mi_row_bytes(14, 4096) == 3360
     assert lib.mi_row_bytes(8, 896) == 952
     assert lib.mi_row_bytes(12, 300) == -1
+
+
+def test_cache_rows():
+    # tests/test_repack.mojo:561-600: an f16 row is the width; a q8_0 row is a
+    # byte a value plus a half a 32-block, rounded up to 8 halves, under 5/8 of
+    # the f16 row; a width of partial blocks has no q8 row.
+    lib = _lib.lib()
+    assert lib.mi_cache_row(0, 1024) == 1024
+    assert lib.mi_cache_row(1, 1024) == 544
+    for heads in range(1, 17):
+        w = heads * 128
+        row = lib.mi_cache_row(1, w)
+        assert row % 8 == 0 and row * 8 < lib.mi_cache_row(0, w) * 5
+    assert lib.mi_cache_row(1, 48) == -1 and lib.mi_cache_row(2, 64) == -1 and lib.mi_cache_row(0, 0) == -1
 
 
 def test_rope_steps_match_oracle():

@@ -256,6 +256,69 @@ def test_attention(ctx, count):
     assert np.abs(got - want).max() <= 1e-5 * np.abs(want).max()
 
 
+def q8_rows(values, kvw):
+    """Host encoding of f32 rows into q8_0 cache rows (tests/test_gpu_ops.mojo
+    _quantize_q8 rule), as the uint16 halves the device cache holds."""
+    from molla_amd import gpu
+    row = gpu.cache_row(gpu.CACHE_Q8, kvw)
+    v = np.asarray(values, np.float32).reshape(-1, kvw)
+    out = np.zeros((v.shape[0], row * 2), np.uint8)
+    for r in range(v.shape[0]):
+        for b in range(kvw // 32):
+            blk = v[r, 32 * b:32 * b + 32]
+            amax = np.float32(np.abs(blk).max())
+            inv = np.float32(0) if amax == 0 else np.float32(127) / amax
+            y = blk * inv
+            q = np.clip(np.trunc(np.where(y >= 0, y + np.float32(0.5), y - np.float32(0.5))), -127, 127)
+            out[r, 32 * b:32 * b + 32] = q.astype(np.int8).view(np.uint8)
+            out[r, kvw + 2 * b:kvw + 2 * b + 2] = np.array([amax / np.float32(127)], np.float16).view(np.uint8)
+    return out.view(np.uint16).reshape(-1)
+
+
+def q8_decode(halves, kvw, count):
+    """f32 values of `count` q8_0 cache rows (float(q) * float(factor))."""
+    from molla_amd import gpu
+    row = gpu.cache_row(gpu.CACHE_Q8, kvw)
+    b = np.asarray(halves, np.uint16).reshape(-1)[:count * row].view(np.uint8).reshape(count, row * 2)
+    q = b[:, :kvw].view(np.int8).astype(np.float32)
+    f = b[:, kvw:kvw + kvw // 16].copy().view(np.float16).astype(np.float32)
+    return (q.reshape(count, kvw // 32, 32) * f[:, :, None]).reshape(count, kvw)
+
+
+@pytest.mark.parametrize("count", [1, 40, 129, 2049])
+def test_attention_q8_cache(ctx, count):
+    """tests/test_gpu_ops.mojo test_attend_q8: rows stored by the q8 store
+    kernel read back exactly as the host quantizer says, and attention over
+    them matches the oracle attending to those values."""
+    from molla_amd import gpu
+    heads, kv, hd = 8, 2, 32
+    kvw = kv * hd
+    i = np.arange(count * kvw)
+    raw_k = ((i * 31 % 173) / 173 - 0.5).astype(np.float32)
+    raw_v = ((i * 17 % 149) / 149 - 0.5).astype(np.float32)
+    row = gpu.cache_row(gpu.CACHE_Q8, kvw)
+    kc = torch.zeros(count * row, dtype=torch.float16, device="cuda")
+    vc = torch.zeros(count * row, dtype=torch.float16, device="cuda")
+    dk, dv = torch.from_numpy(raw_k).cuda(), torch.from_numpy(raw_v).cuda()
+    for slot in range(count):
+        gpu.device_store_kv(ctx, dk[slot * kvw:(slot + 1) * kvw], dv[slot * kvw:(slot + 1) * kvw], kc, vc, slot,
+                            gpu.CACHE_Q8)
+    ctx.synchronize()
+    kh = kc.cpu().numpy().view(np.uint16)
+    # the stored bytes are the host encoding, bit for bit
+    assert np.array_equal(kh, q8_rows(raw_k, kvw))
+    assert np.array_equal(vc.cpu().numpy().view(np.uint16), q8_rows(raw_v, kvw))
+    keys, values = oracle.q8_cache_round(raw_k), oracle.q8_cache_round(raw_v)
+    assert np.array_equal(q8_decode(kh, kvw, count).reshape(-1), keys)
+    q = synth.normal(heads * hd, 3).numpy()
+    scale = float(np.float32(1 / np.sqrt(hd)))
+    want = oracle.attend(heads, kv, hd, scale, q, keys, values, count)
+    out = torch.zeros(heads * hd, device="cuda")
+    gpu.device_attend(ctx, torch.from_numpy(q).cuda(), kc, vc, heads, kv, hd, scale, count, out, gpu.CACHE_Q8)
+    got = out.cpu().numpy()
+    assert np.abs(got - want).max() <= 1e-5 * np.abs(want).max()
+
+
 def test_attention_paper_case(ctx):
     """tests/test_attention.mojo:150: three keys by hand."""
     from molla_amd import gpu

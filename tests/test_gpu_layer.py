@@ -189,3 +189,57 @@ def test_graph_replay_matches_eager():
             # unrelated eager work between replays
             torch.randn(4096, device="cuda").sum().item()
         assert graphed.pos.cpu().tolist() == [steps, steps]
+
+
+@pytest.mark.parametrize("dims,pos,tokens", [
+    ((256, 512, 4, 2, 64), 37, 1),
+    ((512, 1024, 8, 2, 64), 300, 3),
+    ((4096, 14336, 32, 8, 128), 2048, 1),
+])
+def test_layer_q8_cache_matches_oracle(dims, pos, tokens):
+    """The layer over a q8_0 KV cache (repack.mojo:181 CACHE_Q8): the residual
+    within 1e-4 of its peak of the oracle attending over the values the cache
+    holds, earlier slots untouched, the new slot within one quant step of the
+    oracle's q8-rounded key and value."""
+    from molla_amd import block, gpu
+    from tests.test_gpu_kernels import q8_decode, q8_rows
+    ctx = gpu.DeviceContext(0)
+    spec = spec_of(*dims)
+    host = make_layer_weights(spec, 9)
+    bs, layer = device_layer_from(host, spec)
+    kvw = bs.kv_width()
+    row = gpu.cache_row(gpu.CACHE_Q8, kvw)
+    count = pos + 1
+    cache_stride = count * row
+    raw_k = synth.normal(tokens * count * kvw, 50).numpy()
+    raw_v = synth.normal(tokens * count * kvw, 51).numpy()
+    kh = np.concatenate([q8_rows(raw_k.reshape(tokens, -1)[t], kvw) for t in range(tokens)])
+    vh = np.concatenate([q8_rows(raw_v.reshape(tokens, -1)[t], kvw) for t in range(tokens)])
+    x = synth.normal(tokens * bs.width, 52).numpy()
+    kd = torch.from_numpy(kh.view(np.int16).copy()).view(torch.float16).cuda()
+    vd = torch.from_numpy(vh.view(np.int16).copy()).view(torch.float16).cuda()
+    xd = torch.from_numpy(x.copy()).cuda()
+    posd = torch.full((tokens,), pos, dtype=torch.int32, device="cuda")
+    block.device_layer(ctx, layer, xd, kd, vd, cache_stride, posd, count, tokens, form=gpu.CACHE_Q8)
+    ctx.synchronize()
+    got_x = xd.cpu().numpy().reshape(tokens, -1)
+    got_kh = kd.cpu().view(torch.int16).numpy().view(np.uint16).reshape(tokens, -1)
+    got_vh = vd.cpu().view(torch.int16).numpy().view(np.uint16).reshape(tokens, -1)
+    keep = []
+    L = oracle.make_layer(spec, host, keep)
+    for t in range(tokens):
+        kr = q8_decode(kh.reshape(tokens, -1)[t], kvw, count).reshape(-1).copy()
+        vr = q8_decode(vh.reshape(tokens, -1)[t], kvw, count).reshape(-1).copy()
+        xr = x.reshape(tokens, -1)[t].copy()
+        oracle.layer_step(L, xr, kr, vr, pos, pos, q8_store=True, threads=8)
+        err = np.abs(got_x[t].astype(np.float64) - xr)
+        assert err.max() <= 1e-4 * np.abs(xr).max(), (t, float(err.max()))
+        old = slice(0, pos * row)
+        assert np.array_equal(got_kh[t][old], kh.reshape(tokens, -1)[t][old])
+        assert np.array_equal(got_vh[t][old], vh.reshape(tokens, -1)[t][old])
+        gk = q8_decode(got_kh[t], kvw, count)[pos]
+        gv = q8_decode(got_vh[t], kvw, count)[pos]
+        wk, wv = kr.reshape(count, kvw)[pos], vr.reshape(count, kvw)[pos]
+        for got, want in ((gk, wk), (gv, wv)):
+            step = np.repeat(np.abs(want).reshape(-1, 32).max(axis=1) / 127, 32) * 1.01 + 1e-7
+            assert (np.abs(got - want) <= step).all()

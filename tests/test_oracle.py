@@ -326,6 +326,27 @@ def test_rope_per_pair_factors():
         oracle.rotate(x, 1, 8, 8, 10000.0, True, 3, factors=[1.0])
 
 
+def test_q8_cache_round():
+    # The q8_0 cache quantizer (tests/test_gpu_ops.mojo:925 _quantize_q8):
+    # per 32-value block, the largest magnitude maps to +-127 exactly; every
+    # value reads back within half a factor; a block of zeros stays zero;
+    # rounding is half away from zero.
+    rng = np.random.default_rng(3)
+    v = rng.standard_normal(256).astype(np.float32)
+    got = oracle.q8_cache_round(v)
+    for b in range(8):
+        blk, out = v[32 * b:32 * b + 32], got[32 * b:32 * b + 32]
+        amax = np.abs(blk).max()
+        s = np.float32(np.float16(amax / np.float32(127)))
+        q = out / s
+        assert np.allclose(q, np.rint(q), atol=1e-4) and np.abs(q).max() == 127.0
+        assert np.abs(out - blk).max() <= s * 0.5 + abs(amax - 127 * s) + 1e-6
+    assert not oracle.q8_cache_round(np.zeros(32, np.float32)).any()
+    half = np.zeros(32, np.float32)
+    half[0], half[1], half[2] = 127.0, 2.5, -2.5  # factor 1: 2.5 -> 3, -2.5 -> -3
+    assert list(oracle.q8_cache_round(half)[:3]) == [127.0, 3.0, -3.0]
+
+
 def test_rope_steps():
     # tests/test_rope.mojo:420-457: one step per pair, first is 1, falling.
     steps = oracle.rope_steps(64, 10000.0)
