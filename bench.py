@@ -17,7 +17,8 @@ same bytes, single thread, over a bounded number of repetitions.
 
 "decode" (skipped with --no-decode) is config 5: a synthetic 8B model (32 Q4_K
 layers, Q6_K head, f32 embedding, random weights), a 2048-token prompt fed one
-position per step, then greedy decode of 256 tokens at batch 1 and 4, each
+position per step, then greedy decode of 256 tokens at batch 1 and 4 (and at
+batch 1 over a q8_0 KV cache, `batch_1_q8_cache`), each
 step replayed from one captured HIP graph; tokens/s, ms per step, the eager
 (host-launched) ms per step and the weight-streaming fraction of 8 TB/s.
 """
@@ -49,6 +50,8 @@ def main():
     ap.add_argument("--no-decode", action="store_true", help="skip the synthetic 8B decode step")
     ap.add_argument("--decode-tokens", type=int, default=256)
     ap.add_argument("--decode-batch", type=int, nargs="+", default=[1, 4])
+    ap.add_argument("--decode-q8", type=int, nargs="*", default=[1],
+                    help="decode batch sizes also run over a q8_0 KV cache")
     ap.add_argument("--prompt", type=int, default=2048)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-batched", action="store_true", help="skip the batch-4/8 matrix-core tile lines")
@@ -305,10 +308,11 @@ def _decode(ctx, args):
     stream = torch.cuda.Stream()
     dctx = gpu.DeviceContext(0, stream=stream)
     eager_n = 16
-    for batch in args.decode_batch:
+    runs = [(b, gpu.CACHE_F16) for b in args.decode_batch] + [(b, gpu.CACHE_Q8) for b in args.decode_q8]
+    for batch, form in runs:
         ctxlen = args.prompt + args.decode_tokens + eager_n + 1
         with torch.cuda.stream(stream):
-            sess = block.DeviceSession(dctx, model, batch=batch, context=ctxlen)
+            sess = block.DeviceSession(dctx, model, batch=batch, context=ctxlen, cache_form=form)
             prompt = synth.tokens(args.prompt * batch, vocab, 5 + batch, device=dev).view(args.prompt, batch)
             sess.pos.zero_()
             t0 = time.perf_counter()
@@ -342,7 +346,7 @@ def _decode(ctx, args):
             stream.synchronize()
         ms_step = e0.elapsed_time(e1) / args.decode_tokens
         gbs = wb / (ms_step * 1e-3) / 1e9
-        out[f"batch_{batch}"] = {"tokens_per_s": round(1000 * batch / ms_step, 2), "ms_per_step": round(ms_step, 3),
+        out[f"batch_{batch}" + ("_q8_cache" if form == gpu.CACHE_Q8 else "")] = {"tokens_per_s": round(1000 * batch / ms_step, 2), "ms_per_step": round(ms_step, 3),
                                  "weight_stream_gbs": round(gbs, 1), "frac_of_weight_roofline": round(gbs / PEAK_GBS, 4),
                                  "eager_ms_per_step": round(eager_ms, 3), "prefill_s": round(prefill_s, 2)}
         del gp, gd

@@ -205,20 +205,12 @@ int mi_decoder_layer(mi_stream stream, const mi_layer_desc* d, float* resid, uin
                               qkv + qw + kvw, qkv_stride, MI_EPI_NONE, nullptr)))
         return rc;
     }
-    if (q8) {
-      // a q8_0 cache: q and k rotated in place (adjacent in the fused row),
-      // then k and v encoded a 32-value block per half-wave
-      if ((rc = launch_rope(s, qkv, d->heads + d->kv_heads, d->head_dim, d->rope_dim, d->neox, d->rope_steps,
-                            pos, tokens, qkv_stride, d->rope_factors)))
-        return rc;
-      if ((rc = launch_store_kv(s, qkv + qw, qkv + qw + kvw, (int32_t)kvw, k_cache, v_cache, pos, 0, tokens,
-                                qkv_stride, cache_stride, MI_CACHE_Q8)))
-        return rc;
-    } else if ((rc = launch_rope_store(s, qkv, d->heads, d->kv_heads, d->head_dim, d->rope_dim, d->neox,
-                                       d->rope_steps, pos, tokens, qkv_stride, k_cache, v_cache, cache_stride,
-                                       d->rope_factors))) {
+    // rotate q and k; k and v into the cache (f16, or q8_0 blocks encoded by
+    // the same launch once it holds every rotated key)
+    if ((rc = launch_rope_store(s, qkv, d->heads, d->kv_heads, d->head_dim, d->rope_dim, d->neox,
+                                d->rope_steps, pos, tokens, qkv_stride, k_cache, v_cache, cache_stride,
+                                d->rope_factors, d->cache_form)))
       return rc;
-    }
   }
   // count = pos + 1 per sequence: the attention kernels read pos and add one.
   if ((rc = launch_attend(s, qkv, qkv_stride, k_cache, v_cache, cache_stride, d->heads, d->kv_heads,

@@ -130,7 +130,7 @@ int launch_store_kv(hipStream_t s, const float* k, const float* v, int32_t kv_wi
 int launch_rope_store(hipStream_t s, float* qkv, int32_t heads, int32_t kv_heads, int32_t head_dim,
                       int32_t dim, int32_t neox, const float* steps, const int32_t* pos,
                       int32_t tokens, int64_t row_stride, uint16_t* k_cache, uint16_t* v_cache,
-                      int64_t cache_stride, const float* factors = nullptr);
+                      int64_t cache_stride, const float* factors = nullptr, int32_t form = MI_CACHE_F16);
 size_t attend_workspace(int32_t heads, int32_t head_dim, int32_t max_count, int32_t tokens);
 int launch_attend(hipStream_t s, const float* q, int64_t q_stride, const uint16_t* k_cache,
                   const uint16_t* v_cache, int64_t cache_stride, int32_t heads, int32_t kv_heads,

@@ -89,6 +89,22 @@ __global__ __launch_bounds__(kNormThreads) void rms_norm_kernel(const float* __r
   if (xq) quantize_group32(v, threadIdx.x & 31, mine >> 5, n >> 5, xq + (int64_t)t * xq_token_bytes(n), live);
 }
 
+// One q8_0 block of a cache row: the 32 lanes of a half-wave each bring one
+// value x of block b; rowp is the position's row (quants, then factors).
+__device__ __forceinline__ void q8_store_block(float x, __half* __restrict__ rowp, int b, int kv_width,
+                                               int lane32) {
+#pragma clang fp contract(off)
+  float amax = fabsf(x);
+#pragma unroll
+  for (int m = 16; m >= 1; m >>= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 32));
+  const float inv = amax == 0.0f ? 0.0f : 127.0f / amax;
+  const float y = x * inv;
+  const float r = y >= 0.0f ? y + 0.5f : y - 0.5f;
+  const int qi = max(-127, min(127, (int)r));
+  ((int8_t*)rowp)[b * 32 + lane32] = (int8_t)qi;
+  if (lane32 == 0) rowp[(kv_width >> 1) + b] = __float2half_rn(amax / 127.0f);
+}
+
 // ---- RoPE ------------------------------------------------------------------
 // rope.mojo:253-338: theta = f32(pos) * step / freq (scale 1),
 // c = f32(cos(f64(theta))), s likewise, (a, b) <- (a*c - b*s, a*s + b*c).
@@ -129,11 +145,15 @@ __global__ void rope_kernel(float* __restrict__ x, int heads, int head_dim, int 
 constexpr int kRopeThreads = 512;
 constexpr int kRopePer = 8;  // pairs per thread held in registers per pass
 
+// Q8: the cache is q8_0 (crow halves a position): the rotated keys go back
+// into the row like q, and once the block has them all, each half-wave
+// encodes 32-value blocks of k and v into the cache (no store launch).
+template <bool Q8>
 __global__ __launch_bounds__(kRopeThreads) void rope_store_kernel(
     float* __restrict__ qkv, int heads, int kv_heads, int head_dim, int dim, int neox,
     const float* __restrict__ steps, const float* __restrict__ factors, const int32_t* __restrict__ pos,
     int64_t row_stride,
-    __half* __restrict__ kc, __half* __restrict__ vc, int64_t cache_stride) {
+    __half* __restrict__ kc, __half* __restrict__ vc, int64_t cache_stride, int crow) {
 #pragma clang fp contract(off)
   extern __shared__ float trig[];  // [pairs][2]
   const int t = blockIdx.x;
@@ -141,8 +161,8 @@ __global__ __launch_bounds__(kRopeThreads) void rope_store_kernel(
   const int p = pos[t];
   float* row = qkv + (int64_t)t * row_stride;
   const int kvw = kv_heads * head_dim;
-  __half* kd = kc + (int64_t)t * cache_stride + (int64_t)p * kvw;
-  __half* vd = vc + (int64_t)t * cache_stride + (int64_t)p * kvw;
+  __half* kd = kc + (int64_t)t * cache_stride + (int64_t)p * crow;
+  __half* vd = vc + (int64_t)t * cache_stride + (int64_t)p * crow;
   const int total = (heads + kv_heads) * pairs;
   const int lo_step = neox ? 1 : 2, hi_off = neox ? pairs : 1;
   for (int base = 0; base < total; base += kRopeThreads * kRopePer) {
@@ -174,15 +194,26 @@ __global__ __launch_bounds__(kRopeThreads) void rope_store_kernel(
       const int64_t lo = (int64_t)h * head_dim + q * lo_step;
       row[lo] = ra;
       row[lo + hi_off] = rb;
-      if (h >= heads) {  // a key head: straight into the cache
+      if (!Q8 && h >= heads) {  // a key head: straight into the cache
         const int64_t kl = lo - (int64_t)heads * head_dim;
         kd[kl] = __float2half_rn(ra);
         kd[kl + hi_off] = __float2half_rn(rb);
       }
     }
   }
-  // values, and any key elements past the rotary dimension
   const float* v = row + (int64_t)(heads + kv_heads) * head_dim;
+  if constexpr (Q8) {
+    __syncthreads();  // every rotated key is in the row
+    const float* k = row + (int64_t)heads * head_dim;
+    const int nb = kvw >> 5, lane32 = threadIdx.x & 31;
+    for (int blk = threadIdx.x >> 5; blk < 2 * nb; blk += kRopeThreads >> 5) {
+      const bool isv = blk >= nb;
+      const int b = isv ? blk - nb : blk;
+      q8_store_block((isv ? v : k)[b * 32 + lane32], isv ? vd : kd, b, kvw, lane32);
+    }
+    return;
+  }
+  // values, and any key elements past the rotary dimension
   for (int i = threadIdx.x; i < kvw; i += kRopeThreads) vd[i] = __float2half_rn(v[i]);
   if (dim < head_dim) {
     const float* k = row + (int64_t)heads * head_dim;
@@ -487,25 +518,14 @@ __global__ __launch_bounds__(256) void store_kv_q8_kernel(const float* __restric
                                                           __half* __restrict__ vc, const int32_t* __restrict__ slot_dev,
                                                           int slot_host, int64_t src_stride, int64_t cache_stride,
                                                           int row) {
-#pragma clang fp contract(off)
   const int t = blockIdx.y;
   const bool isv = blockIdx.z == 1;
   const int lane32 = threadIdx.x & 31;
   const int b = (blockIdx.x * blockDim.x + threadIdx.x) >> 5;  // block of the row
-  const int nb = kv_width >> 5;
-  if (b >= nb) return;  // whole half-waves leave together
+  if (b >= (kv_width >> 5)) return;  // whole half-waves leave together
   const int slot = slot_dev ? slot_dev[t] : slot_host;
   const float x = (isv ? v : k)[(int64_t)t * src_stride + b * 32 + lane32];
-  float amax = fabsf(x);
-#pragma unroll
-  for (int m = 16; m >= 1; m >>= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 32));
-  const float inv = amax == 0.0f ? 0.0f : 127.0f / amax;
-  const float y = x * inv;
-  const float r = y >= 0.0f ? y + 0.5f : y - 0.5f;
-  const int qi = max(-127, min(127, (int)r));
-  __half* rowp = (isv ? vc : kc) + (int64_t)t * cache_stride + (int64_t)slot * row;
-  ((int8_t*)rowp)[b * 32 + lane32] = (int8_t)qi;
-  if (lane32 == 0) rowp[(kv_width >> 1) + b] = __float2half_rn(amax / 127.0f);
+  q8_store_block(x, (isv ? vc : kc) + (int64_t)t * cache_stride + (int64_t)slot * row, b, kv_width, lane32);
 }
 
 // One block per (query head, token); thread d owns output dimension d (the
@@ -690,10 +710,16 @@ int launch_rope(hipStream_t s, float* x, int32_t heads, int32_t head_dim, int32_
 int launch_rope_store(hipStream_t s, float* qkv, int32_t heads, int32_t kv_heads, int32_t head_dim,
                       int32_t dim, int32_t neox, const float* steps, const int32_t* pos,
                       int32_t tokens, int64_t row_stride, uint16_t* k_cache, uint16_t* v_cache,
-                      int64_t cache_stride, const float* factors) {
-  hipLaunchKernelGGL(rope_store_kernel, dim3(tokens), dim3(kRopeThreads), (size_t)dim * sizeof(float), s, qkv,
-                     heads, kv_heads, head_dim, dim, neox, steps, factors, pos, row_stride, (__half*)k_cache,
-                     (__half*)v_cache, cache_stride);
+                      int64_t cache_stride, const float* factors, int32_t form) {
+  const int crow = cache_row(form, kv_heads * head_dim);
+  if (form == MI_CACHE_Q8)
+    hipLaunchKernelGGL(rope_store_kernel<true>, dim3(tokens), dim3(kRopeThreads), (size_t)dim * sizeof(float), s,
+                       qkv, heads, kv_heads, head_dim, dim, neox, steps, factors, pos, row_stride, (__half*)k_cache,
+                       (__half*)v_cache, cache_stride, crow);
+  else
+    hipLaunchKernelGGL(rope_store_kernel<false>, dim3(tokens), dim3(kRopeThreads), (size_t)dim * sizeof(float), s,
+                       qkv, heads, kv_heads, head_dim, dim, neox, steps, factors, pos, row_stride, (__half*)k_cache,
+                       (__half*)v_cache, cache_stride, crow);
   return hip_check(hipGetLastError(), "rope_store launch");
 }
 
