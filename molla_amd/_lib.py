@@ -54,6 +54,8 @@ SIGNATURES = {
     "mi_embed": (ctypes.c_int, [P, P, I32, I32, P, I32, P]),
     "mi_layer_workspace": (SZ, [ctypes.POINTER(MiLayerDesc), I32, I32]),
     "mi_decoder_layer": (ctypes.c_int, [P, ctypes.POINTER(MiLayerDesc), P, P, P, I64, P, I32, I32, P, SZ]),
+    "mi_decoder_layer_paged": (ctypes.c_int, [P, ctypes.POINTER(MiLayerDesc), P, P, P, P, I64, P, I32, I32, P,
+                                              SZ]),
 }
 
 _lib = None

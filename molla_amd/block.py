@@ -105,6 +105,23 @@ def device_layer(ctx: gpu.DeviceContext, layer: DeviceLayer, x: torch.Tensor, k_
                                  work.data_ptr(), work.numel()))
 
 
+def device_layer_paged(ctx: gpu.DeviceContext, layer: DeviceLayer, x: torch.Tensor, k_pool: torch.Tensor,
+                       v_pool: torch.Tensor, kv_index: torch.Tensor, index_stride: int, pos: torch.Tensor,
+                       max_count: int, tokens: int = 1, work: torch.Tensor | None = None,
+                       form: int = gpu.CACHE_F16) -> None:
+    """device_layer over a paged pool (gpu.mojo:571 DevicePaging): kv_index is
+    a device int32 [tokens, index_stride] of pool cells, one per position of
+    each sequence (negative: not held), the new position's cell set before
+    the call."""
+    need = layer_workspace(layer, max_count, tokens)
+    if work is None:
+        work = ctx.workspace(need)
+    desc = layer.desc if form == gpu.CACHE_F16 else with_cache_form(layer.desc, form)
+    check(lib().mi_decoder_layer_paged(ctx.handle, ctypes.byref(desc), x.data_ptr(), k_pool.data_ptr(),
+                                       v_pool.data_ptr(), kv_index.data_ptr(), index_stride, pos.data_ptr(),
+                                       max_count, tokens, work.data_ptr(), work.numel()))
+
+
 class DeviceModel:
     """A Llama stack on the device: f32 embedding, layers, final norm, head."""
 

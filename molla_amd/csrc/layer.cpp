@@ -103,16 +103,9 @@ int check_desc(const mi_layer_desc* d) {
 
 }  // namespace
 
-extern "C" {
-
-size_t mi_layer_workspace(const mi_layer_desc* desc, int32_t max_count, int32_t tokens) {
-  if (!desc || max_count <= 0 || tokens <= 0) return 0;
-  return carve(desc, max_count, tokens).total;
-}
-
-int mi_decoder_layer(mi_stream stream, const mi_layer_desc* d, float* resid, uint16_t* k_cache,
-                     uint16_t* v_cache, int64_t cache_stride, const int32_t* pos, int32_t max_count,
-                     int32_t tokens, void* work, size_t work_bytes) {
+static int decoder_layer(mi_stream stream, const mi_layer_desc* d, float* resid, uint16_t* k_cache,
+                         uint16_t* v_cache, int64_t cache_stride, const int32_t* kv_index, int64_t index_stride,
+                         const int32_t* pos, int32_t max_count, int32_t tokens, void* work, size_t work_bytes) {
   int rc = check_desc(d);
   if (rc) return rc;
   if (!resid || !k_cache || !v_cache || !pos) return fail(MI_ERR_ARG, "layer: null pointer");
@@ -122,8 +115,11 @@ int mi_decoder_layer(mi_stream stream, const mi_layer_desc* d, float* resid, uin
   if (max_count <= 0) return fail(MI_ERR_SHAPE, "layer: max_count must be positive");
   const int64_t kvw = (int64_t)d->kv_heads * d->head_dim;
   const int64_t crow = cache_row(d->cache_form, (int32_t)kvw);  // halves per position
-  if (tokens > 1 && cache_stride < (int64_t)max_count * crow)
+  if (!kv_index && tokens > 1 && cache_stride < (int64_t)max_count * crow)
     return fail(MI_ERR_SHAPE, "layer: cache stride %lld holds fewer than %d slots", (long long)cache_stride,
+                max_count);
+  if (kv_index && tokens > 1 && index_stride < max_count)
+    return fail(MI_ERR_SHAPE, "layer: index stride %lld holds fewer than %d positions", (long long)index_stride,
                 max_count);
   const Carve c = carve(d, max_count, tokens);
   if (!work || ((uintptr_t)work & 255) || work_bytes < c.total)
@@ -172,6 +168,7 @@ int mi_decoder_layer(mi_stream stream, const mi_layer_desc* d, float* resid, uin
     rp.pos = pos;
     rp.k_cache = (__half*)k_cache;
     rp.v_cache = (__half*)v_cache;
+    rp.kv_index = kv_index;
     if ((rc = launch_q4k_qkv_rope(s, sg, d->width, xq, qkv, rp))) return rc;
   } else {
     if ((rc = launch_rms_norm(s, resid, d->attn_norm, d->width, tokens, d->eps, nullptr, xq))) return rc;
@@ -209,13 +206,13 @@ int mi_decoder_layer(mi_stream stream, const mi_layer_desc* d, float* resid, uin
     // the same launch once it holds every rotated key)
     if ((rc = launch_rope_store(s, qkv, d->heads, d->kv_heads, d->head_dim, d->rope_dim, d->neox,
                                 d->rope_steps, pos, tokens, qkv_stride, k_cache, v_cache, cache_stride,
-                                d->rope_factors, d->cache_form)))
+                                d->rope_factors, d->cache_form, kv_index, index_stride)))
       return rc;
   }
   // count = pos + 1 per sequence: the attention kernels read pos and add one.
   if ((rc = launch_attend(s, qkv, qkv_stride, k_cache, v_cache, cache_stride, d->heads, d->kv_heads,
                           d->head_dim, d->attn_scale, pos, -1, max_count, tokens, nullptr, xq, attn,
-                          d->cache_form)))
+                          d->cache_form, kv_index, index_stride)))
     return rc;
   if ((rc = launch_matvec(s, d->wo.kind, d->wo.data, d->wo.row_bytes, d->width, qw, xq, tokens, resid,
                           d->width, MI_EPI_ADD, nullptr)))
@@ -258,6 +255,30 @@ int mi_decoder_layer(mi_stream stream, const mi_layer_desc* d, float* resid, uin
   if ((rc = launch_quantize(s, gate, d->hidden, tokens, xq))) return rc;
   return launch_matvec(s, d->down.kind, d->down.data, d->down.row_bytes, d->width, d->hidden, xq, tokens,
                        resid, d->width, MI_EPI_ADD, nullptr);
+}
+
+extern "C" {
+
+size_t mi_layer_workspace(const mi_layer_desc* desc, int32_t max_count, int32_t tokens) {
+  if (!desc || max_count <= 0 || tokens <= 0) return 0;
+  return carve(desc, max_count, tokens).total;
+}
+
+// The layer over per-sequence caches (kv_index null) or a paged pool.
+
+int mi_decoder_layer(mi_stream stream, const mi_layer_desc* d, float* resid, uint16_t* k_cache,
+                     uint16_t* v_cache, int64_t cache_stride, const int32_t* pos, int32_t max_count,
+                     int32_t tokens, void* work, size_t work_bytes) {
+  return decoder_layer(stream, d, resid, k_cache, v_cache, cache_stride, nullptr, 0, pos, max_count, tokens, work,
+                       work_bytes);
+}
+
+int mi_decoder_layer_paged(mi_stream stream, const mi_layer_desc* d, float* resid, uint16_t* k_pool,
+                           uint16_t* v_pool, const int32_t* kv_index, int64_t index_stride, const int32_t* pos,
+                           int32_t max_count, int32_t tokens, void* work, size_t work_bytes) {
+  if (!kv_index) return fail(MI_ERR_ARG, "layer: a paged layer needs its index");
+  return decoder_layer(stream, d, resid, k_pool, v_pool, 0, kv_index, index_stride, pos, max_count, tokens, work,
+                       work_bytes);
 }
 
 }  // extern "C"

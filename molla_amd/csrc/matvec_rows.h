@@ -52,6 +52,7 @@ struct QkvRope {
   const int32_t* pos;
   __half* k_cache;
   __half* v_cache;
+  const int32_t* kv_index;  // paged: the cell of position pos[0] is kv_index[pos[0]]; null: slot pos[0]
 };
 
 namespace rows {
@@ -160,7 +161,7 @@ __global__ __launch_bounds__(GQ ? 32 / RPW * 64 : KS * 64) void rows_kernel(
           o = (e & 1) ? a * cs.y + b * cs.x : a * cs.x - b * cs.y;
         }
       }
-      const int64_t slot = (int64_t)rp.pos[0] * rp.kvw;
+      const int64_t slot = (int64_t)(rp.kv_index ? rp.kv_index[rp.pos[0]] : rp.pos[0]) * rp.kvw;
       if (is_q) y[row] = o;
       else if (is_k) rp.k_cache[slot + (row - rp.qw)] = __float2half_rn(o);
       else rp.v_cache[slot + (row - rp.qw - rp.kvw)] = __float2half_rn(o);

@@ -130,13 +130,18 @@ int launch_store_kv(hipStream_t s, const float* k, const float* v, int32_t kv_wi
 int launch_rope_store(hipStream_t s, float* qkv, int32_t heads, int32_t kv_heads, int32_t head_dim,
                       int32_t dim, int32_t neox, const float* steps, const int32_t* pos,
                       int32_t tokens, int64_t row_stride, uint16_t* k_cache, uint16_t* v_cache,
-                      int64_t cache_stride, const float* factors = nullptr, int32_t form = MI_CACHE_F16);
+                      int64_t cache_stride, const float* factors = nullptr, int32_t form = MI_CACHE_F16,
+                      const int32_t* kv_index = nullptr, int64_t index_stride = 0);
 size_t attend_workspace(int32_t heads, int32_t head_dim, int32_t max_count, int32_t tokens);
+// Attention and the cache stores take an optional paged index: kv_index[t *
+// index_stride + j] is the pool cell (one cache row) holding position j of
+// sequence t, negative for a position it does not hold; null for
+// per-sequence caches cache_stride halves apart.
 int launch_attend(hipStream_t s, const float* q, int64_t q_stride, const uint16_t* k_cache,
                   const uint16_t* v_cache, int64_t cache_stride, int32_t heads, int32_t kv_heads,
                   int32_t head_dim, float scale, const int32_t* pos_dev, int32_t count_host,
                   int32_t max_count, int32_t tokens, float* out, void* xq_out, void* work,
-                  int32_t form = MI_CACHE_F16);
+                  int32_t form = MI_CACHE_F16, const int32_t* kv_index = nullptr, int64_t index_stride = 0);
 int launch_argmax(hipStream_t s, const float* x, int32_t n, int32_t tokens, int32_t* out);
 int launch_embed(hipStream_t s, const float* emb, int32_t vocab, int32_t width, const int32_t* ids,
                  int32_t tokens, float* out);

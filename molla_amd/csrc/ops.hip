@@ -153,7 +153,8 @@ __global__ __launch_bounds__(kRopeThreads) void rope_store_kernel(
     float* __restrict__ qkv, int heads, int kv_heads, int head_dim, int dim, int neox,
     const float* __restrict__ steps, const float* __restrict__ factors, const int32_t* __restrict__ pos,
     int64_t row_stride,
-    __half* __restrict__ kc, __half* __restrict__ vc, int64_t cache_stride, int crow) {
+    __half* __restrict__ kc, __half* __restrict__ vc, int64_t cache_stride, int crow,
+    const int32_t* __restrict__ kv_index, int64_t index_stride) {
 #pragma clang fp contract(off)
   extern __shared__ float trig[];  // [pairs][2]
   const int t = blockIdx.x;
@@ -161,8 +162,10 @@ __global__ __launch_bounds__(kRopeThreads) void rope_store_kernel(
   const int p = pos[t];
   float* row = qkv + (int64_t)t * row_stride;
   const int kvw = kv_heads * head_dim;
-  __half* kd = kc + (int64_t)t * cache_stride + (int64_t)p * crow;
-  __half* vd = vc + (int64_t)t * cache_stride + (int64_t)p * crow;
+  const int64_t at = kv_index ? (int64_t)kv_index[t * index_stride + p] * crow
+                              : (int64_t)t * cache_stride + (int64_t)p * crow;
+  __half* kd = kc + at;
+  __half* vd = vc + at;
   const int total = (heads + kv_heads) * pairs;
   const int lo_step = neox ? 1 : 2, hi_off = neox ? pairs : 1;
   for (int base = 0; base < total; base += kRopeThreads * kRopePer) {
@@ -264,12 +267,22 @@ __host__ __device__ __forceinline__ size_t attn_lds_bytes(int head_dim, int grou
          (size_t)group * kk * 4;
 }
 
+// Paged caches (gpu_ops.mojo:660 _row_of): with kv_index, position j of
+// sequence t lives in cell kv_index[t * index_stride + j] of one shared pool
+// (cells of one cache row each, cache_stride unused), and a negative cell is
+// a position the sequence does not hold, masked like a key past the end;
+// without it, position j of sequence t is row j of that sequence's own cache.
+__device__ __forceinline__ int kv_cell(const int32_t* __restrict__ kv_index, int64_t index_stride, int t, int j) {
+  return kv_index ? kv_index[t * index_stride + j] : j;
+}
+
 template <int GROUP>
 __global__ __launch_bounds__(kAttnThreads) void attend_split_kernel(
     const float* __restrict__ q, int64_t q_stride, const __half* __restrict__ kc,
     const __half* __restrict__ vc, int64_t cache_stride, int heads, int kv_heads, int head_dim,
     float scale, const int32_t* __restrict__ pos_dev, int count_host, int max_chunks,
-    float* __restrict__ part_acc, float* __restrict__ part_ml) {
+    float* __restrict__ part_acc, float* __restrict__ part_ml, const int32_t* __restrict__ kv_index,
+    int64_t index_stride) {
   const int c = blockIdx.x, kvh = blockIdx.y, t = blockIdx.z;
   const int count = pos_dev ? pos_dev[t] + 1 : count_host;  // a position p attends over p + 1 slots
   const int kk = attn_slice(head_dim);
@@ -287,8 +300,9 @@ __global__ __launch_bounds__(kAttnThreads) void attend_split_kernel(
 
   // stage keys, values (16-byte pieces; keys past the end repeat the last
   // live one and are masked below) and the group's queries
-  const __half* kbase = kc + (int64_t)t * cache_stride + (int64_t)kvh * D;
-  const __half* vbase = vc + (int64_t)t * cache_stride + (int64_t)kvh * D;
+  const int64_t seq = kv_index ? 0 : (int64_t)t * cache_stride;
+  const __half* kbase = kc + seq + (int64_t)kvh * D;
+  const __half* vbase = vc + seq + (int64_t)kvh * D;
   // Every load of a batch is issued before any LDS store, with clamped
   // (always valid) addresses instead of guards: a guarded load becomes a
   // branch with its own wait, which serialised the staging.
@@ -304,7 +318,8 @@ __global__ __launch_bounds__(kAttnThreads) void attend_split_kernel(
     for (int j = 0; j < kBatch; j++) {
       const int i = min(b0 + tid + j * kAttnThreads, total - 1);
       const int key = min(i / pieces, nk - 1), pc = i % pieces;
-      const int64_t off = (int64_t)(start + key) * kvw + pc * 8;
+      const int cell = max(kv_cell(kv_index, index_stride, t, start + key), 0);
+      const int64_t off = (int64_t)cell * kvw + pc * 8;
       kv[j] = *(const uint4*)(kbase + off);
       vv[j] = *(const uint4*)(vbase + off);
     }
@@ -345,7 +360,7 @@ __global__ __launch_bounds__(kAttnThreads) void attend_split_kernel(
         sdot = fmaf(qb.w, k3.y, sdot);
       }
     }
-    const bool live = lane < nk;
+    const bool live = lane < nk && (!kv_index || kv_cell(kv_index, index_stride, t, start + lane) >= 0);
     const float sc = live ? sdot * scale : -INFINITY;
     float m = sc;
 #pragma unroll
@@ -399,7 +414,8 @@ __global__ __launch_bounds__(kAttnThreads) void attend_split_q8_kernel(
     const float* __restrict__ q, int64_t q_stride, const __half* __restrict__ kc,
     const __half* __restrict__ vc, int64_t cache_stride, int row, int heads, int kv_heads, int head_dim,
     float scale, const int32_t* __restrict__ pos_dev, int count_host, int max_chunks,
-    float* __restrict__ part_acc, float* __restrict__ part_ml) {
+    float* __restrict__ part_acc, float* __restrict__ part_ml, const int32_t* __restrict__ kv_index,
+    int64_t index_stride) {
 #pragma clang fp contract(off)
   const int c = blockIdx.x, kvh = blockIdx.y, t = blockIdx.z;
   const int count = pos_dev ? pos_dev[t] + 1 : count_host;
@@ -418,8 +434,9 @@ __global__ __launch_bounds__(kAttnThreads) void attend_split_q8_kernel(
   float* Ps = Qs + GROUP * D;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
 
-  const __half* kseq = kc + (int64_t)t * cache_stride;
-  const __half* vseq = vc + (int64_t)t * cache_stride;
+  const int64_t seq = kv_index ? 0 : (int64_t)t * cache_stride;
+  const __half* kseq = kc + seq;
+  const __half* vseq = vc + seq;
   // quants in 16-byte pieces, every load of the slice issued before any
   // LDS store; keys past the end repeat the last live one (masked below)
   const int pieces = D >> 4;
@@ -433,7 +450,8 @@ __global__ __launch_bounds__(kAttnThreads) void attend_split_q8_kernel(
     for (int j = 0; j < 2; j++) {
       const int i = min(b0 + tid + j * kAttnThreads, total - 1);
       const int key = min(i / pieces, nk - 1), pc = i % pieces;
-      const int64_t off = (int64_t)(start + key) * row * 2 + (int64_t)kvh * D + pc * 16;  // bytes
+      const int cell = max(kv_cell(kv_index, index_stride, t, start + key), 0);
+      const int64_t off = (int64_t)cell * row * 2 + (int64_t)kvh * D + pc * 16;  // bytes
       kv[j] = *(const uint4*)((const int8_t*)kseq + off);
       vv[j] = *(const uint4*)((const int8_t*)vseq + off);
     }
@@ -449,7 +467,8 @@ __global__ __launch_bounds__(kAttnThreads) void attend_split_q8_kernel(
   }
   for (int i = tid; i < kk * NB; i += kAttnThreads) {
     const int key = min(i / NB, nk - 1), b = i % NB;
-    const int64_t at = (int64_t)(start + key) * row + (kvw >> 1) + (kvh * D >> 5) + b;  // halves
+    const int cell = max(kv_cell(kv_index, index_stride, t, start + key), 0);
+    const int64_t at = (int64_t)cell * row + (kvw >> 1) + (kvh * D >> 5) + b;  // halves
     Ksc[i] = __half2float(kseq[at]);
     Vsc[i] = __half2float(vseq[at]);
   }
@@ -471,7 +490,7 @@ __global__ __launch_bounds__(kAttnThreads) void attend_split_q8_kernel(
         for (int i = 0; i < 16; i++) sdot = fmaf(qg[d + i], (float)b[i] * f, sdot);
       }
     }
-    const bool live = lane < nk;
+    const bool live = lane < nk && (!kv_index || kv_cell(kv_index, index_stride, t, start + lane) >= 0);
     const float sc = live ? sdot * scale : -INFINITY;
     float m = sc;
 #pragma unroll
@@ -710,16 +729,17 @@ int launch_rope(hipStream_t s, float* x, int32_t heads, int32_t head_dim, int32_
 int launch_rope_store(hipStream_t s, float* qkv, int32_t heads, int32_t kv_heads, int32_t head_dim,
                       int32_t dim, int32_t neox, const float* steps, const int32_t* pos,
                       int32_t tokens, int64_t row_stride, uint16_t* k_cache, uint16_t* v_cache,
-                      int64_t cache_stride, const float* factors, int32_t form) {
+                      int64_t cache_stride, const float* factors, int32_t form, const int32_t* kv_index,
+                      int64_t index_stride) {
   const int crow = cache_row(form, kv_heads * head_dim);
   if (form == MI_CACHE_Q8)
     hipLaunchKernelGGL(rope_store_kernel<true>, dim3(tokens), dim3(kRopeThreads), (size_t)dim * sizeof(float), s,
                        qkv, heads, kv_heads, head_dim, dim, neox, steps, factors, pos, row_stride, (__half*)k_cache,
-                       (__half*)v_cache, cache_stride, crow);
+                       (__half*)v_cache, cache_stride, crow, kv_index, index_stride);
   else
     hipLaunchKernelGGL(rope_store_kernel<false>, dim3(tokens), dim3(kRopeThreads), (size_t)dim * sizeof(float), s,
                        qkv, heads, kv_heads, head_dim, dim, neox, steps, factors, pos, row_stride, (__half*)k_cache,
-                       (__half*)v_cache, cache_stride, crow);
+                       (__half*)v_cache, cache_stride, crow, kv_index, index_stride);
   return hip_check(hipGetLastError(), "rope_store launch");
 }
 
@@ -750,7 +770,8 @@ size_t attend_workspace(int32_t heads, int32_t head_dim, int32_t max_count, int3
 int launch_attend(hipStream_t s, const float* q, int64_t q_stride, const uint16_t* k_cache,
                   const uint16_t* v_cache, int64_t cache_stride, int32_t heads, int32_t kv_heads,
                   int32_t head_dim, float scale, const int32_t* pos_dev, int32_t count_host,
-                  int32_t max_count, int32_t tokens, float* out, void* xq_out, void* work, int32_t form) {
+                  int32_t max_count, int32_t tokens, float* out, void* xq_out, void* work, int32_t form,
+                  const int32_t* kv_index, int64_t index_stride) {
   const int kk = attn_slice(head_dim);
   const int chunks = (max_count + kk - 1) / kk;
   const int64_t slots = (int64_t)tokens * heads * chunks;
@@ -768,11 +789,11 @@ int launch_attend(hipStream_t s, const float* q, int64_t q_stride, const uint16_
   if (q8)                                                                                                  \
     hipLaunchKernelGGL(attend_split_q8_kernel<G>, grid, dim3(kAttnThreads), shmem, s, q, q_stride, kc, vc,  \
                        cache_stride, row, heads, kv_heads, head_dim, scale, pos_dev, count_host, chunks,    \
-                       part_acc, part_ml);                                                                 \
+                       part_acc, part_ml, kv_index, index_stride);                                         \
   else                                                                                                     \
     hipLaunchKernelGGL(attend_split_kernel<G>, grid, dim3(kAttnThreads), shmem, s, q, q_stride, kc, vc,     \
                        cache_stride, heads, kv_heads, head_dim, scale, pos_dev, count_host, chunks,         \
-                       part_acc, part_ml)
+                       part_acc, part_ml, kv_index, index_stride)
   switch (group) {
     case 1: MI_ATTEND(1); break;
     case 2: MI_ATTEND(2); break;

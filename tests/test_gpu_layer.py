@@ -243,3 +243,109 @@ def test_layer_q8_cache_matches_oracle(dims, pos, tokens):
         for got, want in ((gk, wk), (gv, wv)):
             step = np.repeat(np.abs(want).reshape(-1, 32).max(axis=1) / 127, 32) * 1.01 + 1e-7
             assert (np.abs(got - want) <= step).all()
+
+
+def paged_from_contiguous(caches, count, row, tokens, extra, seed):
+    """A pool holding the rows of per-sequence caches (uint16 [tokens, count *
+    row]) in shuffled cells, and the index [tokens, count] of each position's
+    cell."""
+    rng = np.random.default_rng(seed)
+    cells = rng.permutation(tokens * count + extra)[: tokens * count].reshape(tokens, count).astype(np.int32)
+    pool = np.zeros(((tokens * count + extra) * row,), np.uint16)
+    for t in range(tokens):
+        for j in range(count):
+            pool[cells[t, j] * row:(cells[t, j] + 1) * row] = caches[t, j * row:(j + 1) * row]
+    return pool, cells
+
+
+@pytest.mark.parametrize("form", ["f16", "q8"])
+@pytest.mark.parametrize("dims,pos,tokens", [((256, 512, 4, 2, 64), 77, 1), ((512, 1024, 8, 2, 64), 300, 3)])
+def test_layer_paged_matches_contiguous(form, dims, pos, tokens):
+    """The paged layer (cells scattered over a shared pool, gpu.mojo:571
+    DevicePaging) gives the contiguous layer's residual and new cache rows
+    bit for bit: only the addressing differs."""
+    from molla_amd import block, gpu
+    from tests.test_gpu_kernels import q8_rows
+    ctx = gpu.DeviceContext(0)
+    f = gpu.CACHE_Q8 if form == "q8" else gpu.CACHE_F16
+    spec = spec_of(*dims)
+    bs, layer = device_layer_from(make_layer_weights(spec, 11), spec)
+    kvw = bs.kv_width()
+    row = gpu.cache_row(f, kvw)
+    count = pos + 1
+    raw = [synth.normal(tokens * count * kvw, 60 + i).numpy() for i in (0, 1)]
+    if f == gpu.CACHE_Q8:
+        caches = [np.stack([q8_rows(r.reshape(tokens, -1)[t], kvw) for t in range(tokens)]) for r in raw]
+    else:
+        caches = [r.astype(np.float16).view(np.uint16).reshape(tokens, -1) for r in raw]
+    x = synth.normal(tokens * bs.width, 62).numpy()
+    posd = torch.full((tokens,), pos, dtype=torch.int32, device="cuda")
+
+    def dev(a):
+        return torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).view(torch.float16).cuda()
+
+    kd, vd, xd = dev(caches[0]), dev(caches[1]), torch.from_numpy(x.copy()).cuda()
+    block.device_layer(ctx, layer, xd, kd, vd, count * row, posd, count, tokens, form=f)
+    extra = 5
+    kp, cells = paged_from_contiguous(caches[0], count, row, tokens, extra, 7)
+    vp, _ = paged_from_contiguous(caches[1], count, row, tokens, extra, 7)
+    kpd, vpd, xpd = dev(kp), dev(vp), torch.from_numpy(x.copy()).cuda()
+    idx = torch.from_numpy(cells).cuda()
+    block.device_layer_paged(ctx, layer, xpd, kpd, vpd, idx, count, posd, count, tokens, form=f)
+    ctx.synchronize()
+    assert torch.equal(xd, xpd)
+    kc = kd.cpu().view(torch.int16).numpy().reshape(tokens, -1)
+    kpool = kpd.cpu().view(torch.int16).numpy()
+    vc = vd.cpu().view(torch.int16).numpy().reshape(tokens, -1)
+    vpool = vpd.cpu().view(torch.int16).numpy()
+    for t in range(tokens):
+        for j in (0, pos // 2, pos):
+            c = cells[t, j]
+            assert np.array_equal(kc[t, j * row:(j + 1) * row], kpool[c * row:(c + 1) * row])
+            assert np.array_equal(vc[t, j * row:(j + 1) * row], vpool[c * row:(c + 1) * row])
+
+
+def test_layer_paged_skips_positions_it_does_not_hold():
+    """A negative cell is a position the sequence does not hold
+    (gpu_ops.mojo:660 _row_of): attention leaves it out.  The oracle attends
+    over the held positions only (slot = how many it holds, rope at pos)."""
+    from molla_amd import block, gpu
+    ctx = gpu.DeviceContext(0)
+    spec = spec_of(256, 512, 4, 2, 64)
+    host = make_layer_weights(spec, 13)
+    bs, layer = device_layer_from(host, spec)
+    kvw = bs.kv_width()
+    pos = 90
+    count = pos + 1
+    held = np.ones(count, bool)
+    held[[3, 10, 11, 12, 64, 65, 89]] = False  # windows trimmed out
+    raw_k = synth.normal(count * kvw, 70).half().numpy().reshape(count, kvw)
+    raw_v = synth.normal(count * kvw, 71).half().numpy().reshape(count, kvw)
+    cells = np.full(count, -1, np.int32)
+    order = np.random.default_rng(9).permutation(count + 4)
+    pool_k = np.zeros(((count + 4), kvw), np.float16)
+    pool_v = np.zeros(((count + 4), kvw), np.float16)
+    for j in range(count):
+        if held[j] or j == pos:
+            cells[j] = order[j]
+            pool_k[order[j]] = raw_k[j]
+            pool_v[order[j]] = raw_v[j]
+    x = synth.normal(bs.width, 72).numpy()
+    xd = torch.from_numpy(x.copy()).cuda()
+    kpd = torch.from_numpy(pool_k.reshape(-1)).cuda()
+    vpd = torch.from_numpy(pool_v.reshape(-1)).cuda()
+    posd = torch.tensor([pos], dtype=torch.int32, device="cuda")
+    block.device_layer_paged(ctx, layer, xd, kpd, vpd, torch.from_numpy(cells).cuda(), count, posd, count, 1)
+    ctx.synchronize()
+    keep = []
+    L = oracle.make_layer(spec, host, keep)
+    kept = [j for j in range(pos) if held[j]]
+    slot = len(kept)
+    kr = np.zeros(((slot + 1), kvw), np.float32)
+    vr = np.zeros(((slot + 1), kvw), np.float32)
+    kr[:slot], vr[:slot] = raw_k[kept].astype(np.float32), raw_v[kept].astype(np.float32)
+    xr = x.copy()
+    kr, vr = kr.reshape(-1).copy(), vr.reshape(-1).copy()
+    oracle.layer_step(L, xr, kr, vr, slot, pos, f16_store=True, threads=8)
+    got = xd.cpu().numpy()
+    assert np.abs(got - xr).max() <= 1e-4 * np.abs(xr).max()
