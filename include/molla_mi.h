@@ -221,13 +221,17 @@ int mi_decoder_layer(mi_stream stream, const mi_layer_desc* desc, float* resid,
                      const int32_t* pos, int32_t max_count, int32_t tokens,
                      void* work, size_t work_bytes);
 
-/* The same layer over a paged pool (gpu_ops.mojo:660 _row_of, gpu.mojo:571
+/* The same layer over a paged pool (gpu_ops.mojo:662 _row_of, gpu.mojo:571
  * DevicePaging): k_pool / v_pool hold cells of mi_cache_row(form, kv_width)
  * halves each, shared by every sequence; kv_index[t * index_stride + j] is
  * the cell holding position j of sequence t, or negative for a position the
  * sequence does not hold (masked out of attention).  The caller sets the
  * cell of the new position, kv_index[t * index_stride + pos[t]], before the
- * call; the rotated key and the value are written there. */
+ * call; the rotated key and the value are written there.  index_stride 0
+ * makes the tokens one sequence's chunk (the reference's `bases` all zero):
+ * they share one list, sit at distinct positions pos[t], and each attends
+ * over the positions up to its own, the chunk's earlier tokens included.
+ * cache_stride 0 does the same for mi_decoder_layer. */
 int mi_decoder_layer_paged(mi_stream stream, const mi_layer_desc* desc, float* resid, uint16_t* k_pool,
                            uint16_t* v_pool, const int32_t* kv_index, int64_t index_stride, const int32_t* pos,
                            int32_t max_count, int32_t tokens, void* work, size_t work_bytes);

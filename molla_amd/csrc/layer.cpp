@@ -115,10 +115,13 @@ static int decoder_layer(mi_stream stream, const mi_layer_desc* d, float* resid,
   if (max_count <= 0) return fail(MI_ERR_SHAPE, "layer: max_count must be positive");
   const int64_t kvw = (int64_t)d->kv_heads * d->head_dim;
   const int64_t crow = cache_row(d->cache_form, (int32_t)kvw);  // halves per position
-  if (!kv_index && tokens > 1 && cache_stride < (int64_t)max_count * crow)
+  // A stride of 0 makes the tokens one sequence's chunk at distinct positions
+  // (every token reads and writes the same cache or index list).
+  if (cache_stride < 0 || index_stride < 0) return fail(MI_ERR_SHAPE, "layer: negative stride");
+  if (!kv_index && tokens > 1 && cache_stride != 0 && cache_stride < (int64_t)max_count * crow)
     return fail(MI_ERR_SHAPE, "layer: cache stride %lld holds fewer than %d slots", (long long)cache_stride,
                 max_count);
-  if (kv_index && tokens > 1 && index_stride < max_count)
+  if (kv_index && tokens > 1 && index_stride != 0 && index_stride < max_count)
     return fail(MI_ERR_SHAPE, "layer: index stride %lld holds fewer than %d positions", (long long)index_stride,
                 max_count);
   const Carve c = carve(d, max_count, tokens);

@@ -349,3 +349,61 @@ def test_layer_paged_skips_positions_it_does_not_hold():
     oracle.layer_step(L, xr, kr, vr, slot, pos, f16_store=True, threads=8)
     got = xd.cpu().numpy()
     assert np.abs(got - xr).max() <= 1e-4 * np.abs(xr).max()
+
+
+@pytest.mark.parametrize("paged", [False, True])
+def test_layer_chunk_of_one_sequence(paged):
+    """Stride 0: the tokens are one sequence's chunk at consecutive positions
+    (gpu.mojo:617 `bases` all zero).  Each token attends over the positions up
+    to its own, the chunk's earlier tokens included; the oracle runs them one
+    at a time over the same cache (fed the rows the device stored for the
+    chunk's earlier tokens)."""
+    from molla_amd import block, gpu
+    ctx = gpu.DeviceContext(0)
+    spec = spec_of(512, 1024, 8, 2, 64)
+    host = make_layer_weights(spec, 17)
+    host["rope_factors"] = llama31_factors(spec["rope_dim"] // 2)
+    bs, layer = device_layer_from(host, spec)
+    kvw = bs.kv_width()
+    tokens, first = 4, 200
+    count = first + tokens
+    keys16 = synth.normal(count * kvw, 80).half().numpy().reshape(count, kvw)
+    vals16 = synth.normal(count * kvw, 81).half().numpy().reshape(count, kvw)
+    keys16[first:] = 0
+    vals16[first:] = 0
+    x = synth.normal(tokens * bs.width, 82).numpy()
+    xd = torch.from_numpy(x.copy()).cuda()
+    posd = torch.arange(first, count, dtype=torch.int32, device="cuda")
+    if paged:
+        order = np.random.default_rng(3).permutation(count + 7).astype(np.int32)[:count]
+        pk = np.zeros((count + 7, kvw), np.float16)
+        pv = np.zeros((count + 7, kvw), np.float16)
+        pk[order], pv[order] = keys16, vals16
+        kd, vd = torch.from_numpy(pk.reshape(-1)).cuda(), torch.from_numpy(pv.reshape(-1)).cuda()
+        block.device_layer_paged(ctx, layer, xd, kd, vd, torch.from_numpy(order).cuda(), 0, posd, count, tokens)
+        ctx.synchronize()
+        got_k = kd.cpu().numpy().reshape(-1, kvw)[order].astype(np.float32)
+        got_v = vd.cpu().numpy().reshape(-1, kvw)[order].astype(np.float32)
+    else:
+        kd, vd = torch.from_numpy(keys16.reshape(-1).copy()).cuda(), torch.from_numpy(vals16.reshape(-1).copy()).cuda()
+        block.device_layer(ctx, layer, xd, kd, vd, 0, posd, count, tokens)
+        ctx.synchronize()
+        got_k = kd.cpu().float().numpy().reshape(count, kvw)
+        got_v = vd.cpu().float().numpy().reshape(count, kvw)
+    got_x = xd.cpu().numpy().reshape(tokens, -1)
+    assert (got_k[:first] == keys16[:first].astype(np.float32)).all()
+    keep = []
+    L = oracle.make_layer(spec, host, keep)
+    for i in range(tokens):
+        p = first + i
+        kr = keys16.astype(np.float32).copy()
+        vr = vals16.astype(np.float32).copy()
+        kr[first:p], vr[first:p] = got_k[first:p], got_v[first:p]
+        kr, vr = kr.reshape(-1), vr.reshape(-1)
+        xr = x.reshape(tokens, -1)[i].copy()
+        oracle.layer_step(L, xr, kr, vr, p, p, f16_store=True, threads=8)
+        err = np.abs(got_x[i].astype(np.float64) - xr)
+        assert err.max() <= 1e-4 * np.abs(xr).max(), (i, err.max())
+        kr, vr = kr.reshape(count, kvw), vr.reshape(count, kvw)
+        assert np.allclose(got_k[p], kr[p], rtol=2e-3, atol=1e-3)
+        assert np.allclose(got_v[p], vr[p], rtol=2e-3, atol=1e-3)
