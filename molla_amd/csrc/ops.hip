@@ -267,7 +267,7 @@ __host__ __device__ __forceinline__ size_t attn_lds_bytes(int head_dim, int grou
          (size_t)group * kk * 4;
 }
 
-// Paged caches (gpu_ops.mojo:660 _row_of): with kv_index, position j of
+// Paged caches (gpu_ops.mojo:662 _row_of): with kv_index, position j of
 // sequence t lives in cell kv_index[t * index_stride + j] of one shared pool
 // (cells of one cache row each, cache_stride unused), and a negative cell is
 // a position the sequence does not hold, masked like a key past the end;

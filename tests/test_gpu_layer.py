@@ -307,7 +307,7 @@ def test_layer_paged_matches_contiguous(form, dims, pos, tokens):
 
 def test_layer_paged_skips_positions_it_does_not_hold():
     """A negative cell is a position the sequence does not hold
-    (gpu_ops.mojo:660 _row_of): attention leaves it out.  The oracle attends
+    (gpu_ops.mojo:662 _row_of): attention leaves it out.  The oracle attends
     over the held positions only (slot = how many it holds, rope at pos)."""
     from molla_amd import block, gpu
     ctx = gpu.DeviceContext(0)
