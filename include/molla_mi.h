@@ -94,8 +94,17 @@ int mi_dequant(mi_stream stream, int kind, const void* w, int64_t count, float* 
  * head of the configs).  Activations are carried as 23-bit block fixed point
  * per 32 values (three int8 limbs), so every product is an exact integer dot;
  * the result agrees with the fp32 host path to ~1e-7 relative.
- * Workspace: mi_matvec_workspace(cols, tokens) bytes, 256-byte aligned. */
+ * Workspace: mi_matvec_workspace(cols, tokens) bytes, 256-byte aligned.
+ *
+ * tokens 9..65536 is the prefill matmul (device_matmul_into at a prompt
+ * chunk, gpu.mojo:1695 PREFILL_CHUNK; the tile of gpu.mojo:2665): matrix
+ * cores on half-precision operands, the activations split into two halves
+ * (22 bits) and the weights as the exact integer codes of their blocks, so
+ * the result stays within ~1e-6 relative of the fp32 host dot.  It needs
+ * mi_matvec_workspace(cols, tokens) bytes; given mi_matmul_workspace(rows,
+ * cols, tokens) it may also split long reductions across more blocks. */
 size_t mi_matvec_workspace(int32_t cols, int32_t tokens);
+size_t mi_matmul_workspace(int32_t rows, int32_t cols, int32_t tokens);
 int mi_matvec(mi_stream stream, int kind, const void* w, int64_t row_bytes,
               int32_t rows, int32_t cols, const float* x, int32_t tokens,
               float* y, int32_t epi, const float* aux, void* work, size_t work_bytes);

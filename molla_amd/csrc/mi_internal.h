@@ -96,6 +96,19 @@ int launch_q6k_tile(hipStream_t s, const void* w, int64_t row_bytes, int32_t row
 bool b32_tile_fits(int kind, int32_t cols, int64_t row_bytes, int32_t tokens);
 int launch_b32_tile(hipStream_t s, int kind, const void* w, int64_t row_bytes, int32_t rows, int32_t cols,
                     const void* xq, int32_t tokens, float* y, int64_t ldy, int32_t epi, const float* aux);
+// prefill.hip -- tokens above the decode batch (up to kMaxPrefill) on the
+// f16 matrix cores, from float activations; prefill_fits says whether the
+// kind, width and alignment take the tile (else mi_matvec runs the decode
+// kernels eight tokens at a time).  The workspace is prefill_prep_bytes for
+// the activation halves, plus room for split-K partial sums up to
+// prefill_workspace; with less, K is not split.
+constexpr int kMaxPrefill = 65536;
+bool prefill_fits(int kind, int32_t cols, int64_t row_bytes, const void* w);
+size_t prefill_prep_bytes(int32_t cols, int32_t tokens);
+size_t prefill_workspace(int32_t rows, int32_t cols, int32_t tokens);
+int launch_prefill(hipStream_t s, int kind, const void* w, int64_t row_bytes, int32_t rows, int32_t cols,
+                   const float* x, int32_t tokens, float* y, int64_t ldy, int32_t epi, const float* aux, void* work,
+                   size_t work_bytes);
 // Every kind and batch: routes to the kernels above or the general
 // matvec_kernel.h.
 int launch_matvec(hipStream_t s, int kind, const void* w, int64_t row_bytes, int32_t rows,

@@ -1,0 +1,673 @@
+// prefill.hip -- the many-token matmul (prefill chunks, tokens > 8) on the
+// matrix cores: v_mfma_f32_32x32x16_f16, gfx950.
+//
+// y[t * ldy + r] = epilogue(sum_k W[r][k] * x[t][k]) for every kind of the
+// decode path, at roughly float32 accuracy although the multiplier takes
+// half precision operands:
+//
+//  * Activations.  Token t is scaled by a power of two 2^-e_t so its largest
+//    |x| lies in [2^13, 2^14), then each value is split into two halves,
+//    x' = hi + lo with hi = f16(x') and lo = f16(x' - hi): 22 significant bits
+//    (prefill_x_kernel).  The scale comes back once, on the finished sum.
+//  * Weights enter as the integer codes of the format, which half precision
+//    holds exactly: sc * q for Q4_K and Q5_K (at most 63 * 31), the signed
+//    code for the 32-value kinds (q - 8, q - 16, the int8 of Q8_0, or q), and
+//    sc * (q - 32) for Q6_K split into its even part and its low bit (up to
+//    4096 in magnitude, one bit more than half precision carries).  Every
+//    product code * hi, code * lo is then exact in the float32 accumulator.
+//  * The scale of a weight block multiplies the accumulator once per block
+//    (per 256 values for the K-quants, per 32 for the others), and the
+//    min terms (dmin * m of the K-quants, m of Q4_1 / Q5_1) are one more MFMA
+//    per 256 values against the per-32 means of x (hi and lo in the 16
+//    K-slots; a sum of 32 scaled values would overflow a half).
+//
+// Against the float32 host dot this differs by float32 rounding of the sums.
+// The reference's own tensor-core tile (src/molla/nn/gpu.mojo:2665
+// planar_nvmma_kernel) rounds the activations and weights to half precision
+// and is held to 2e-3 of the peak; this form keeps the 1e-5 gate of its float
+// tiles (tests/test_gpu.mojo:255-300).
+//
+// Work decomposition.  One MFMA is 32 tokens (M) x 32 rows (N) x 16 values
+// (K): lane l holds token / row l % 32 and values 8 (l / 32) .. +8 of the
+// step, and accumulator element j belongs to token 8 (j / 4) + 4 (l / 32) +
+// j % 4, row l % 32.  A wave owns 2 row tiles x 2 token tiles (64 rows x 64
+// tokens); a block of W waves shares the 64 tokens, whose activation halves
+// are staged through LDS 64 values at a time (double-buffered), while each
+// wave decodes its own rows' weight codes straight from global memory, one
+// stage ahead.  Long reductions over few output tiles split K across
+// blockIdx.z, with partial sums in the workspace and a second kernel adding
+// them in split order (deterministic) before the epilogue.
+//
+// Replaces device_matmul_into's batched kernels (src/molla/nn/gpu.mojo:1809
+// planar_matmul_kernel, :2665 planar_nvmma_kernel; dispatch :3015) for
+// tokens above the decode batch; output layout and epilogues as
+// gpu.mojo:1005 and :2955-2961.
+#include "matvec_units.h"
+
+namespace mi {
+namespace {
+
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+constexpr int kTileTok = 32;     // tokens of one MFMA tile
+constexpr int kStage = 64;       // values of K per LDS stage (4 MFMA steps)
+constexpr int kChunk = 256;      // values per min-term MFMA / K-quant superblock
+constexpr int kWaveTok = 2;      // token tiles per wave (and per block)
+constexpr int kWaveRows = 2;     // row tiles per wave
+constexpr int kStageBytes = kWaveTok * 4 * 2 * 1024;  // one LDS buffer
+
+__device__ __forceinline__ v16f mfma(v8h a, v8h b, v16f c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ v8h as_v8h(uint4 u) {
+  union {
+    uint4 u;
+    v8h h;
+  } c;
+  c.u = u;
+  return c.h;
+}
+
+// 8 bytes from a 2-byte aligned address, as two dwords (the 34/18/22-byte
+// blocks sit 2 bytes off alignment every other block).
+__device__ __forceinline__ uint2 ld8(const uint8_t* p) {
+  const uintptr_t a = (uintptr_t)p;
+  const uint32_t* q = (const uint32_t*)(a & ~(uintptr_t)3);
+  const uint32_t sh = (uint32_t)(a & 3);
+  const uint32_t d0 = q[0], d1 = q[1];
+  if (sh == 0) return make_uint2(d0, d1);
+  const uint32_t d2 = q[2];
+  return make_uint2(__builtin_amdgcn_alignbyte(d1, d0, sh), __builtin_amdgcn_alignbyte(d2, d1, sh));
+}
+__device__ __forceinline__ uint32_t ld4u(const uint8_t* p) {
+  const uintptr_t a = (uintptr_t)p;
+  const uint32_t* q = (const uint32_t*)(a & ~(uintptr_t)3);
+  const uint32_t sh = (uint32_t)(a & 3);
+  return sh ? __builtin_amdgcn_alignbyte(q[1], q[0], sh) : q[0];
+}
+__device__ __forceinline__ uint32_t ld2(const uint8_t* p) { return *(const uint16_t*)p; }
+__device__ __forceinline__ float f16f(uint32_t bits) { return half_bits_to_float(bits & 0xFFFF); }
+__device__ __forceinline__ uint32_t byte_of(uint2 v, int i) { return ((i < 4 ? v.x : v.y) >> (8 * (i & 3))) & 0xFF; }
+
+// (sc, m) of group j of a K-quant superblock from scales[0..11] in y, z, w
+// (quant.mojo:161 _k_scale).
+__device__ __forceinline__ void kscale(uint32_t y, uint32_t z, uint32_t w, int j, uint32_t& sc, uint32_t& m) {
+  const uint32_t s = 8u * (uint32_t)(j & 3);
+  const uint32_t hi = (uint32_t)(j >> 2);
+  sc = __builtin_amdgcn_ubfe(hi ? w : y, s, 4) | (__builtin_amdgcn_ubfe(y, s + 4 + 2 * hi, 2) << 4);
+  m = __builtin_amdgcn_ubfe(hi ? w : z, s + 4 * hi, 4) | (__builtin_amdgcn_ubfe(z, s + 4 + 2 * hi, 2) << 4);
+}
+
+__device__ __forceinline__ v8h codes8(const int (&c)[8]) {
+  v8h b;
+#pragma unroll
+  for (int i = 0; i < 8; i++) b[i] = (_Float16)(short)c[i];
+  return b;
+}
+
+// ---- per-kind weight access ------------------------------------------------
+// Raw: what one lane reads of one row for one stage (64 values of K);
+// load(raw, row, stage, kh); codes(raw, stage, s4, kh, b0, b1) for MFMA step
+// s4 (0..3) of the stage, b1 only when LIMBS == 2.
+// GROUP: values per block scale.  MIN: 0 none, 1 K-quant dmin * m (scaled per
+// superblock), 2 m per 32-value block (Q4_1, Q5_1).
+
+struct KQ4K {
+  static constexpr int GROUP = 256, LIMBS = 1, MIN = 1, BLOCK = 144;
+  struct Raw {
+    uint4 hdr;
+    uint2 q[2];
+  };
+  static __device__ __forceinline__ void load(Raw& r, const uint8_t* row, int st, int kh) {
+    const uint8_t* b = row + (int64_t)(st >> 2) * BLOCK;
+    r.hdr = *(const uint4*)b;
+    const uint8_t* q = b + 16 + 32 * (st & 3) + 8 * kh;
+    r.q[0] = *(const uint2*)q;
+    r.q[1] = *(const uint2*)(q + 16);
+  }
+  static __device__ __forceinline__ void codes(const Raw& r, int st, int s4, int kh, v8h& b0, v8h&) {
+    const int j = 2 * (st & 3) + (s4 >> 1);
+    uint32_t sc, m;
+    kscale(r.hdr.y, r.hdr.z, r.hdr.w, j, sc, m);
+    const uint2 q = r.q[s4 & 1];
+    const int sh = 4 * (s4 >> 1);
+    int c[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) c[i] = (int)(((byte_of(q, i) >> sh) & 0xF) * sc);
+    b0 = codes8(c);
+  }
+  static __device__ __forceinline__ float d(const Raw& r) { return f16f(r.hdr.x); }
+  static __device__ __forceinline__ float dmin(const Raw& r) { return f16f(r.hdr.x >> 16); }
+  static __device__ __forceinline__ v8h mins(const Raw& r) {
+    int c[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      uint32_t sc, m;
+      kscale(r.hdr.y, r.hdr.z, r.hdr.w, j, sc, m);
+      c[j] = (int)m;
+    }
+    return codes8(c);
+  }
+};
+
+struct KQ5K {
+  static constexpr int GROUP = 256, LIMBS = 1, MIN = 1, BLOCK = 176;
+  struct Raw {
+    uint4 hdr;
+    uint2 qh[2], q[2];
+  };
+  static __device__ __forceinline__ void load(Raw& r, const uint8_t* row, int st, int kh) {
+    const uint8_t* b = row + (int64_t)(st >> 2) * BLOCK;
+    r.hdr = *(const uint4*)b;
+    r.qh[0] = *(const uint2*)(b + 16 + 8 * kh);
+    r.qh[1] = *(const uint2*)(b + 32 + 8 * kh);
+    const uint8_t* q = b + 48 + 32 * (st & 3) + 8 * kh;
+    r.q[0] = *(const uint2*)q;
+    r.q[1] = *(const uint2*)(q + 16);
+  }
+  static __device__ __forceinline__ void codes(const Raw& r, int st, int s4, int kh, v8h& b0, v8h&) {
+    const int j = 2 * (st & 3) + (s4 >> 1);
+    uint32_t sc, m;
+    kscale(r.hdr.y, r.hdr.z, r.hdr.w, j, sc, m);
+    const uint2 q = r.q[s4 & 1], h = r.qh[s4 & 1];
+    const int sh = 4 * (s4 >> 1);
+    int c[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+      c[i] = (int)((((byte_of(q, i) >> sh) & 0xF) | (((byte_of(h, i) >> j) & 1) << 4)) * sc);
+    b0 = codes8(c);
+  }
+  static __device__ __forceinline__ float d(const Raw& r) { return f16f(r.hdr.x); }
+  static __device__ __forceinline__ float dmin(const Raw& r) { return f16f(r.hdr.x >> 16); }
+  static __device__ __forceinline__ v8h mins(const Raw& r) { return KQ4K::mins(*(const KQ4K::Raw*)&r); }
+};
+
+// Q6_K (quant.mojo:371): stage st' = st % 4 of a superblock covers half
+// n = st' / 2 and quarters 2 (st' % 2) + {0, 1}; step s4 is quarter
+// 2 (st' % 2) + s4 / 2, values 16 (s4 % 2) + 8 kh .. +8 of it, whose scale is
+// sc[8n + 4 (st' % 2) + s4].
+struct KQ6K {
+  static constexpr int GROUP = 256, LIMBS = 2, MIN = 0, BLOCK = 210;
+  struct Raw {
+    uint2 ql[2][2], qh[2];
+    uint32_t sc, dbits;
+  };
+  static __device__ __forceinline__ void load(Raw& r, const uint8_t* row, int st, int kh) {
+    const uint8_t* b = row + (int64_t)(st >> 2) * BLOCK;
+    const int sp = st & 3, n = sp >> 1;
+#pragma unroll
+    for (int a = 0; a < 2; a++)
+#pragma unroll
+      for (int c = 0; c < 2; c++) r.ql[a][c] = ld8(b + 64 * n + 32 * a + 16 * c + 8 * kh);
+#pragma unroll
+    for (int c = 0; c < 2; c++) r.qh[c] = ld8(b + 128 + 32 * n + 16 * c + 8 * kh);
+    r.sc = ld4u(b + 192 + 8 * n + 4 * (sp & 1));
+    r.dbits = ld2(b + 208);
+  }
+  static __device__ __forceinline__ void codes(const Raw& r, int st, int s4, int, v8h& b0, v8h& b1) {
+    const int sp = st & 3, a = s4 >> 1, c = s4 & 1;
+    const int kq = 2 * (sp & 1) + a;
+    const int nib = 4 * (sp & 1);
+    const int sc = (int)(int8_t)(r.sc >> (8 * s4));
+    const uint2 ql = r.ql[a][c], qh = r.qh[c];
+    int e[8], o[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const int q = (int)(((byte_of(ql, i) >> nib) & 0xF) | (((byte_of(qh, i) >> (2 * kq)) & 3) << 4)) - 32;
+      const int w = sc * q;
+      e[i] = w & ~1;
+      o[i] = w & 1;
+    }
+    b0 = codes8(e);
+    b1 = codes8(o);
+  }
+  static __device__ __forceinline__ float d(const Raw& r) { return f16f(r.dbits); }
+  static __device__ __forceinline__ float dmin(const Raw&) { return 0.0f; }
+  static __device__ __forceinline__ v8h mins(const Raw&) { return v8h{}; }
+};
+
+// The 32-value kinds: a stage is two blocks; step s4 is block s4 / 2, values
+// 16 (s4 % 2) + 8 kh .. +8 of it.
+template <int KIND>
+struct KB32 {
+  static constexpr int GROUP = 32, LIMBS = 1;
+  static constexpr int MIN = (KIND == MI_Q4_1 || KIND == MI_Q5_1) ? 2 : 0;
+  static constexpr int BLOCK = KIND == MI_Q8_0 ? 34 : KIND == MI_Q4_0 ? 18 : KIND == MI_Q4_1 ? 20
+                               : KIND == MI_Q5_0 ? 22 : 24;
+  struct Raw {
+    uint32_t dm[2];    // d | m << 16
+    uint32_t qh[2];    // Q5_0 / Q5_1 fifth bits
+    uint2 q[2][2];     // [block][Q8_0: half of the block; else [0] = the 8 nibble bytes]
+  };
+  static __device__ __forceinline__ void load(Raw& r, const uint8_t* row, int st, int kh) {
+#pragma unroll
+    for (int bb = 0; bb < 2; bb++) {
+      const uint8_t* b = row + (int64_t)(2 * st + bb) * BLOCK;
+      if (KIND == MI_Q8_0) {
+        r.dm[bb] = ld2(b);
+        r.q[bb][0] = ld8(b + 2 + 8 * kh);
+        r.q[bb][1] = ld8(b + 18 + 8 * kh);
+      } else if (KIND == MI_Q4_0) {
+        r.dm[bb] = ld2(b);
+        r.q[bb][0] = ld8(b + 2 + 8 * kh);
+      } else if (KIND == MI_Q4_1) {
+        r.dm[bb] = *(const uint32_t*)b;
+        r.q[bb][0] = *(const uint2*)(b + 4 + 8 * kh);
+      } else if (KIND == MI_Q5_0) {
+        r.dm[bb] = ld2(b);
+        r.qh[bb] = ld4u(b + 2);
+        r.q[bb][0] = ld8(b + 6 + 8 * kh);
+      } else {
+        r.dm[bb] = *(const uint32_t*)b;
+        r.qh[bb] = *(const uint32_t*)(b + 4);
+        r.q[bb][0] = *(const uint2*)(b + 8 + 8 * kh);
+      }
+    }
+  }
+  static __device__ __forceinline__ void codes(const Raw& r, int, int s4, int kh, v8h& b0, v8h&) {
+    const int bb = s4 >> 1, hf = s4 & 1;
+    int c[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      if (KIND == MI_Q8_0) {
+        c[i] = (int)(int8_t)byte_of(r.q[bb][hf], i);
+      } else {
+        const uint32_t nb = (byte_of(r.q[bb][0], i) >> (4 * hf)) & 0xF;
+        if (KIND == MI_Q4_0) c[i] = (int)nb - 8;
+        else if (KIND == MI_Q4_1) c[i] = (int)nb;
+        else {
+          const int l = 16 * hf + 8 * kh + i;
+          const int q = (int)(nb | (((r.qh[bb] >> l) & 1) << 4));
+          c[i] = KIND == MI_Q5_0 ? q - 16 : q;
+        }
+      }
+    }
+    b0 = codes8(c);
+  }
+  static __device__ __forceinline__ float d(const Raw& r, int bb) { return f16f(r.dm[bb]); }
+  static __device__ __forceinline__ uint32_t mbits(const Raw& r, int bb) { return r.dm[bb] >> 16; }
+};
+
+template <int KIND> struct KindOf;
+template <> struct KindOf<MI_Q4_K> { using T = KQ4K; };
+template <> struct KindOf<MI_Q5_K> { using T = KQ5K; };
+template <> struct KindOf<MI_Q6_K> { using T = KQ6K; };
+template <> struct KindOf<MI_Q8_0> { using T = KB32<MI_Q8_0>; };
+template <> struct KindOf<MI_Q4_0> { using T = KB32<MI_Q4_0>; };
+template <> struct KindOf<MI_Q4_1> { using T = KB32<MI_Q4_1>; };
+template <> struct KindOf<MI_Q5_0> { using T = KB32<MI_Q5_0>; };
+template <> struct KindOf<MI_Q5_1> { using T = KB32<MI_Q5_1>; };
+
+// ---- activations -----------------------------------------------------------
+// Layout (ttp token tiles of 32, ks = cols / 16 steps, nch = ceil(cols/256)):
+//   xp: [tile][step][limb][lane][8 halves]: lane (kh, m) holds token
+//       32 tile + m, values 16 step + 8 kh .. +8; limb 0 = hi, 1 = lo.
+//   xm: [tile][chunk][lane][8 halves]: lane (0, m) holds hi of the means of
+//       the chunk's eight 32-value blocks for token 32 tile + m, lane (1, m)
+//       their lo (zero past cols).
+//   xs: [32 ttp] the power of two each token's sums are multiplied by.
+struct Prep {
+  int ttp, ks, nch;
+  size_t xp, xm, xs, total;
+};
+
+__host__ __device__ inline Prep prep_layout(int cols, int tokens) {
+  Prep p;
+  const int tt = (tokens + kTileTok - 1) / kTileTok;
+  p.ttp = (tt + kWaveTok - 1) / kWaveTok * kWaveTok;
+  p.ks = cols / 16;
+  p.nch = (cols + kChunk - 1) / kChunk;
+  p.xp = 0;
+  p.xm = p.xp + (size_t)p.ttp * p.ks * 2048;
+  p.xs = p.xm + (size_t)p.ttp * p.nch * 1024;
+  p.total = (p.xs + (size_t)p.ttp * kTileTok * 4 + 255) & ~(size_t)255;
+  return p;
+}
+
+__device__ __forceinline__ void split_half(float v, _Float16& hi, _Float16& lo) {
+  hi = (_Float16)v;
+  lo = (_Float16)(v - (float)hi);
+}
+
+// One block per token (padding tokens write zeros).
+__global__ __launch_bounds__(256) void prefill_x_kernel(const float* __restrict__ x, int cols, int tokens,
+                                                        uint8_t* __restrict__ work) {
+  const Prep P = prep_layout(cols, tokens);
+  const int t = blockIdx.x;
+  const bool live = t < tokens;
+  const float* row = x + (int64_t)(live ? t : 0) * cols;
+  const int nc = cols >> 3;  // 8-value chunks
+  __shared__ float red[4];
+  float mx = 0.0f;
+  for (int c = threadIdx.x; c < nc; c += blockDim.x) {
+    if (!live) break;
+    const float4 a = *(const float4*)(row + 8 * c), b = *(const float4*)(row + 8 * c + 4);
+    mx = fmaxf(mx, fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))));
+    mx = fmaxf(mx, fmaxf(fmaxf(fabsf(b.x), fabsf(b.y)), fmaxf(fabsf(b.z), fabsf(b.w))));
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  // largest |x| * 2^-e in [2^13, 2^14); the exponent is clamped so the scale
+  // stays a normal float
+  int e = 0;
+  if (mx > 0.0f) e = min(max(ilogbf(mx) - 13, -100), 100);
+  if (threadIdx.x == 0) ((float*)(work + P.xs))[t] = ldexpf(1.0f, e);
+  const int tile = t >> 5, m = t & 31;
+  for (int c = threadIdx.x; c < nc; c += blockDim.x) {
+    float v[8];
+    if (live) {
+      const float4 a = *(const float4*)(row + 8 * c), b = *(const float4*)(row + 8 * c + 4);
+      v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w, v[4] = b.x, v[5] = b.y, v[6] = b.z, v[7] = b.w;
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; i++) v[i] = 0.0f;
+    }
+    v8h hi, lo;
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const float u = ldexpf(v[i], -e);
+      _Float16 h, l;
+      split_half(u, h, l);
+      hi[i] = h;
+      lo[i] = l;
+      s += u;
+    }
+    const int step = c >> 1, kh = c & 1;
+    uint8_t* dst = work + P.xp + ((size_t)(tile * P.ks + step) * 2) * 1024 + (kh * 32 + m) * 16;
+    *(v8h*)dst = hi;
+    *(v8h*)(dst + 1024) = lo;
+    // the 32-value block's sum: four consecutive lanes hold its four chunks
+    s += __shfl_xor(s, 1);
+    s += __shfl_xor(s, 2);
+    if ((c & 3) == 0) {
+      const int blk = c >> 2, ch = blk >> 3, j = blk & 7;
+      _Float16 h, l;
+      split_half(s * (1.0f / 32.0f), h, l);  // a mean: 32 values of up to 2^14 overflow a half
+      _Float16* mdst = (_Float16*)(work + P.xm + (size_t)(tile * P.nch + ch) * 1024);
+      mdst[m * 8 + j] = h;
+      mdst[(32 + m) * 8 + j] = l;
+    }
+  }
+  // the last chunk's slots past cols
+  const int nb = cols >> 5;
+  for (int blk = nb + threadIdx.x; blk < P.nch * 8; blk += blockDim.x) {
+    _Float16* mdst = (_Float16*)(work + P.xm + (size_t)(tile * P.nch + (blk >> 3)) * 1024);
+    mdst[m * 8 + (blk & 7)] = (_Float16)0.0f;
+    mdst[(32 + m) * 8 + (blk & 7)] = (_Float16)0.0f;
+  }
+}
+
+// ---- the matmul ------------------------------------------------------------
+template <int KIND, int W>
+__global__ __launch_bounds__(W * 64) void prefill_kernel(const uint8_t* __restrict__ w, int64_t rb, int rows,
+                                                         int cols, int tokens, const uint8_t* __restrict__ work,
+                                                         int stages_per_split, float* __restrict__ y, int64_t ldy,
+                                                         int epi, const float* __restrict__ aux,
+                                                         float* __restrict__ part) {
+  using K = typename KindOf<KIND>::T;
+  __shared__ __attribute__((aligned(16))) uint8_t xl[2][kStageBytes];
+  const Prep P = prep_layout(cols, tokens);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int n = lane & 31, kh = lane >> 5;
+  const int tile0 = blockIdx.y * kWaveTok;
+  const int nst = cols / kStage;
+  const int st0 = blockIdx.z * stages_per_split;
+  const int st1 = min(st0 + stages_per_split, nst);
+  const int row_base = (blockIdx.x * W + wave) * (kWaveRows * 32);
+  const uint8_t* wrow[kWaveRows];
+#pragma unroll
+  for (int rt = 0; rt < kWaveRows; rt++) wrow[rt] = w + (int64_t)min(row_base + rt * 32 + n, rows - 1) * rb;
+
+  // activation stage copy: 16 KB, four 16-byte pieces a thread
+  const uint8_t* xp = work + P.xp;
+  uint4 xr[kStageBytes / 16 / (W * 64) > 0 ? kStageBytes / 16 / (W * 64) : 1];
+  constexpr int kPieces = kStageBytes / 16 / (W * 64);
+  auto load_x = [&](int st) {
+#pragma unroll
+    for (int q = 0; q < kPieces; q++) {
+      const int idx = threadIdx.x + q * W * 64;
+      const int tt = idx >> 9, within = idx & 511;
+      xr[q] = *(const uint4*)(xp + ((size_t)((tile0 + tt) * P.ks + st * 4) * 2) * 1024 + within * 16);
+    }
+  };
+  auto store_x = [&](int buf) {
+#pragma unroll
+    for (int q = 0; q < kPieces; q++) *(uint4*)(&xl[buf][(threadIdx.x + q * W * 64) * 16]) = xr[q];
+  };
+
+  typename K::Raw raw[2][kWaveRows];
+  v16f tot[kWaveRows][kWaveTok], acc[kWaveRows][kWaveTok];
+  const v16f zero = {};
+#pragma unroll
+  for (int rt = 0; rt < kWaveRows; rt++)
+#pragma unroll
+    for (int tt = 0; tt < kWaveTok; tt++) tot[rt][tt] = acc[rt][tt] = zero;
+  uint4 am[kWaveTok];  // min-term A fragments of the current chunk
+  uint32_t mrec[kWaveRows][4];
+#pragma unroll
+  for (int rt = 0; rt < kWaveRows; rt++)
+#pragma unroll
+    for (int q = 0; q < 4; q++) mrec[rt][q] = 0;
+
+  load_x(st0);
+#pragma unroll
+  for (int rt = 0; rt < kWaveRows; rt++) K::load(raw[0][rt], wrow[rt], st0, kh);
+  store_x(0);
+  __syncthreads();
+
+  for (int st = st0; st < st1; st++) {
+    const int cur = (st - st0) & 1;
+    const bool more = st + 1 < st1;
+    if (more) {
+      load_x(st + 1);
+#pragma unroll
+      for (int rt = 0; rt < kWaveRows; rt++) K::load(raw[cur ^ 1][rt], wrow[rt], st + 1, kh);
+    }
+    if (K::MIN && (st & 3) == 0) {
+#pragma unroll
+      for (int tt = 0; tt < kWaveTok; tt++)
+        am[tt] = *(const uint4*)(work + P.xm + (size_t)((tile0 + tt) * P.nch + (st >> 2)) * 1024 + lane * 16);
+    }
+#pragma unroll
+    for (int s4 = 0; s4 < 4; s4++) {
+      v8h b0[kWaveRows], b1[kWaveRows];
+#pragma unroll
+      for (int rt = 0; rt < kWaveRows; rt++) K::codes(raw[cur][rt], st, s4, kh, b0[rt], b1[rt]);
+#pragma unroll
+      for (int tt = 0; tt < kWaveTok; tt++) {
+        const uint8_t* base = &xl[cur][((tt * 4 + s4) * 2) * 1024 + lane * 16];
+        const v8h ahi = as_v8h(*(const uint4*)base), alo = as_v8h(*(const uint4*)(base + 1024));
+#pragma unroll
+        for (int rt = 0; rt < kWaveRows; rt++) {
+          acc[rt][tt] = mfma(ahi, b0[rt], acc[rt][tt]);
+          acc[rt][tt] = mfma(alo, b0[rt], acc[rt][tt]);
+          if (K::LIMBS == 2) acc[rt][tt] = mfma(ahi, b1[rt], acc[rt][tt]);
+        }
+      }
+      if constexpr (K::GROUP == 32) {
+       if (s4 & 1) {  // a 32-value block ends
+        const int bb = s4 >> 1;
+#pragma unroll
+        for (int rt = 0; rt < kWaveRows; rt++) {
+          const float dv = K::d(raw[cur][rt], bb);
+#pragma unroll
+          for (int tt = 0; tt < kWaveTok; tt++) {
+            tot[rt][tt] += dv * acc[rt][tt];
+            acc[rt][tt] = zero;
+          }
+          if constexpr (K::MIN == 2) {
+            const int slot = 2 * (st & 3) + bb;  // block of the chunk
+            const uint32_t mb = K::mbits(raw[cur][rt], bb);
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+              if (q == (slot >> 1)) mrec[rt][q] = (slot & 1) ? (mrec[rt][q] | (mb << 16)) : mb;
+          }
+        }
+       }
+      }
+    }
+    if constexpr (K::GROUP == 256) {
+     if ((st & 3) == 3) {  // a superblock ends
+#pragma unroll
+      for (int rt = 0; rt < kWaveRows; rt++) {
+        const float dv = K::d(raw[cur][rt]);
+        const float dm = K::dmin(raw[cur][rt]);
+        const v8h bm = K::mins(raw[cur][rt]);
+#pragma unroll
+        for (int tt = 0; tt < kWaveTok; tt++) {
+          tot[rt][tt] += dv * acc[rt][tt];
+          acc[rt][tt] = zero;
+          if constexpr (K::MIN == 1) {
+            const v16f mn = mfma(as_v8h(am[tt]), bm, zero);
+            tot[rt][tt] -= (32.0f * dm) * mn;
+          }
+        }
+      }
+     }
+    }
+    if constexpr (K::MIN == 2) {
+     if ((st & 3) == 3 || st + 1 == st1) {  // a chunk of eight blocks ends
+#pragma unroll
+      for (int rt = 0; rt < kWaveRows; rt++) {
+        const v8h bm = as_v8h(make_uint4(mrec[rt][0], mrec[rt][1], mrec[rt][2], mrec[rt][3]));
+#pragma unroll
+        for (int tt = 0; tt < kWaveTok; tt++) tot[rt][tt] += 32.0f * mfma(as_v8h(am[tt]), bm, zero);
+#pragma unroll
+        for (int q = 0; q < 4; q++) mrec[rt][q] = 0;
+      }
+     }
+    }
+    if (more) store_x(cur ^ 1);
+    __syncthreads();
+  }
+
+  // results: element j of tile (rt, tt) is token 32 (tile0 + tt) + 8 (j / 4) +
+  // 4 kh + j % 4, row row_base + 32 rt + n
+  const float* xs = (const float*)(work + P.xs);
+#pragma unroll
+  for (int tt = 0; tt < kWaveTok; tt++) {
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+      const int t = (tile0 + tt) * 32 + 8 * (j >> 2) + 4 * kh + (j & 3);
+      if (t >= tokens) continue;
+      const float sc = xs[t];
+#pragma unroll
+      for (int rt = 0; rt < kWaveRows; rt++) {
+        const int r = row_base + rt * 32 + n;
+        if (r >= rows) continue;
+        const float v = tot[rt][tt][j] * sc;
+        if (part) part[((size_t)blockIdx.z * tokens + t) * rows + r] = v;
+        else mv::epilogue(y, aux, epi, (int64_t)t * ldy + r, r, v);
+      }
+    }
+  }
+}
+
+// Adds the splits' partial sums in split order and applies the epilogue.
+__global__ __launch_bounds__(256) void prefill_reduce_kernel(const float* __restrict__ part, int splits, int rows,
+                                                             int tokens, float* __restrict__ y, int64_t ldy, int epi,
+                                                             const float* __restrict__ aux) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t n = (int64_t)rows * tokens;
+  if (i >= n) return;
+  float v = part[i];
+  for (int z = 1; z < splits; z++) v += part[z * n + i];
+  const int t = (int)(i / rows), r = (int)(i - (int64_t)t * rows);
+  mv::epilogue(y, aux, epi, (int64_t)t * ldy + r, r, v);
+}
+
+constexpr int kWaves = 4;
+constexpr int kBlockRows = kWaves * kWaveRows * 32;
+
+template <int KIND>
+int launch_kind(hipStream_t s, const void* w, int64_t rb, int rows, int cols, int tokens, const void* work,
+                int splits, int sps, float* y, int64_t ldy, int epi, const float* aux, float* part) {
+  const Prep P = prep_layout(cols, tokens);
+  dim3 grid((rows + kBlockRows - 1) / kBlockRows, P.ttp / kWaveTok, splits);
+  hipLaunchKernelGGL((prefill_kernel<KIND, kWaves>), grid, dim3(kWaves * 64), 0, s, (const uint8_t*)w, rb, rows,
+                     cols, tokens, (const uint8_t*)work, sps, y, ldy, epi, aux, splits > 1 ? part : nullptr);
+  return hip_check(hipGetLastError(), "prefill launch");
+}
+
+// Splits of K (in whole 256-value chunks) for a matmul: enough blocks to put
+// about two waves on every SIMD, each split at least 1024 values long.
+int choose_splits(int rows, int cols, int tokens) {
+  const Prep P = prep_layout(cols, tokens);
+  const int64_t blocks = (int64_t)((rows + kBlockRows - 1) / kBlockRows) * (P.ttp / kWaveTok);
+  const int chunks = (cols + kChunk - 1) / kChunk;
+  int s = 1;
+  while (blocks * s * kWaves < 2048 && (chunks / (2 * s)) >= 4) s *= 2;
+  return s;
+}
+
+}  // namespace
+
+bool prefill_fits(int kind, int32_t cols, int64_t row_bytes, const void* w) {
+  if (cols % kStage) return false;
+  switch (kind) {
+    case MI_Q4_K:
+    case MI_Q5_K:
+      return cols % 256 == 0 && ((uintptr_t)w & 15) == 0 && row_bytes % 16 == 0;
+    case MI_Q6_K:
+      return cols % 256 == 0 && ((uintptr_t)w & 1) == 0 && row_bytes % 2 == 0;
+    case MI_Q4_1:
+      return ((uintptr_t)w & 3) == 0 && row_bytes % 4 == 0;
+    case MI_Q5_1:
+      return ((uintptr_t)w & 7) == 0 && row_bytes % 8 == 0;
+    case MI_Q8_0:
+    case MI_Q4_0:
+    case MI_Q5_0:
+      return ((uintptr_t)w & 1) == 0 && row_bytes % 2 == 0;
+  }
+  return false;
+}
+
+size_t prefill_workspace(int32_t rows, int32_t cols, int32_t tokens) {
+  const Prep P = prep_layout(cols, tokens);
+  const int splits = rows > 0 ? choose_splits(rows, cols, tokens) : 1;
+  size_t part = splits > 1 ? (size_t)splits * tokens * rows * 4 : 0;
+  return P.total + ((part + 255) & ~(size_t)255);
+}
+
+size_t prefill_prep_bytes(int32_t cols, int32_t tokens) { return prep_layout(cols, tokens).total; }
+
+int launch_prefill(hipStream_t s, int kind, const void* w, int64_t row_bytes, int32_t rows, int32_t cols,
+                   const float* x, int32_t tokens, float* y, int64_t ldy, int32_t epi, const float* aux, void* work,
+                   size_t work_bytes) {
+  const Prep P = prep_layout(cols, tokens);
+  hipLaunchKernelGGL(prefill_x_kernel, dim3(P.ttp * kTileTok), dim3(256), 0, s, x, cols, tokens, (uint8_t*)work);
+  int rc = hip_check(hipGetLastError(), "prefill activation launch");
+  if (rc) return rc;
+  int splits = choose_splits(rows, cols, tokens);
+  const size_t need = (size_t)splits * tokens * rows * 4;
+  if (splits > 1 && work_bytes < P.total + need) splits = 1;  // no room for partial sums
+  const int nst = cols / kStage;
+  int sps = (nst + splits - 1) / splits;
+  sps = (sps + 3) & ~3;  // whole 256-value chunks
+  splits = (nst + sps - 1) / sps;
+  float* part = (float*)((uint8_t*)work + P.total);
+  switch (kind) {
+    case MI_Q4_K: rc = launch_kind<MI_Q4_K>(s, w, row_bytes, rows, cols, tokens, work, splits, sps, y, ldy, epi, aux, part); break;
+    case MI_Q5_K: rc = launch_kind<MI_Q5_K>(s, w, row_bytes, rows, cols, tokens, work, splits, sps, y, ldy, epi, aux, part); break;
+    case MI_Q6_K: rc = launch_kind<MI_Q6_K>(s, w, row_bytes, rows, cols, tokens, work, splits, sps, y, ldy, epi, aux, part); break;
+    case MI_Q8_0: rc = launch_kind<MI_Q8_0>(s, w, row_bytes, rows, cols, tokens, work, splits, sps, y, ldy, epi, aux, part); break;
+    case MI_Q4_0: rc = launch_kind<MI_Q4_0>(s, w, row_bytes, rows, cols, tokens, work, splits, sps, y, ldy, epi, aux, part); break;
+    case MI_Q4_1: rc = launch_kind<MI_Q4_1>(s, w, row_bytes, rows, cols, tokens, work, splits, sps, y, ldy, epi, aux, part); break;
+    case MI_Q5_0: rc = launch_kind<MI_Q5_0>(s, w, row_bytes, rows, cols, tokens, work, splits, sps, y, ldy, epi, aux, part); break;
+    case MI_Q5_1: rc = launch_kind<MI_Q5_1>(s, w, row_bytes, rows, cols, tokens, work, splits, sps, y, ldy, epi, aux, part); break;
+    default: return fail(MI_ERR_KIND, "prefill: ggml type %d has no tile", kind);
+  }
+  if (rc || splits == 1) return rc;
+  const int64_t n = (int64_t)rows * tokens;
+  hipLaunchKernelGGL(prefill_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, part, splits, rows,
+                     tokens, y, ldy, epi, aux);
+  return hip_check(hipGetLastError(), "prefill reduce launch");
+}
+
+}  // namespace mi

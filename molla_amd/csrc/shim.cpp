@@ -110,8 +110,15 @@ int mi_dequant(mi_stream stream, int kind, const void* w, int64_t count, float* 
 }
 
 size_t mi_matvec_workspace(int32_t cols, int32_t tokens) {
-  if (cols <= 0 || tokens <= 0) return 0;
+  if (cols <= 0 || tokens <= 0 || tokens > kMaxPrefill) return 0;
+  if (tokens > kMaxTokens) return prefill_prep_bytes(cols, tokens);
   return (size_t)xq_token_bytes(cols) * (size_t)tokens;
+}
+
+size_t mi_matmul_workspace(int32_t rows, int32_t cols, int32_t tokens) {
+  if (rows <= 0 || cols <= 0 || tokens <= 0 || tokens > kMaxPrefill) return 0;
+  if (tokens > kMaxTokens) return prefill_workspace(rows, cols, tokens);
+  return mi_matvec_workspace(cols, tokens);
 }
 
 static int check_xq(const char* name, const void* xq, int32_t cols, int32_t tokens) {
@@ -142,12 +149,47 @@ int mi_matvec_xq(mi_stream stream, int kind, const void* w, int64_t row_bytes, i
   return launch_matvec((hipStream_t)stream, kind, w, row_bytes, rows, cols, xq, tokens, y, rows, epi, aux);
 }
 
+// Tokens above the decode batch: the prefill tile where it fits, else the
+// decode kernels over runs of eight tokens (the GLU aux and the output move
+// with the run; a bias does not).
+static int matmul_many(mi_stream stream, int kind, const void* w, int64_t row_bytes, int32_t rows, int32_t cols,
+                       const float* x, int32_t tokens, float* y, int32_t epi, const float* aux, void* work,
+                       size_t work_bytes) {
+  if (!work || ((uintptr_t)work & 255)) return fail(MI_ERR_ALIGN, "matvec: workspace must be 256-byte aligned");
+  if (cols % 32) return fail(MI_ERR_SHAPE, "matvec: %d values is not a whole number of 32", cols);
+  if (work_bytes < mi_matvec_workspace(cols, tokens))
+    return fail(MI_ERR_WORKSPACE, "matvec: workspace of %zu bytes, %zu needed", work_bytes,
+                mi_matvec_workspace(cols, tokens));
+  hipStream_t s = (hipStream_t)stream;
+  if (prefill_fits(kind, cols, row_bytes, w))
+    return launch_prefill(s, kind, w, row_bytes, rows, cols, x, tokens, y, rows, epi, aux, work, work_bytes);
+  for (int32_t t0 = 0; t0 < tokens; t0 += kMaxTokens) {
+    const int32_t n = tokens - t0 < kMaxTokens ? tokens - t0 : kMaxTokens;
+    int rc = launch_quantize(s, x + (int64_t)t0 * cols, cols, n, work);
+    if (!rc) {
+      const float* a = (epi & MI_EPI_GLU) ? aux + (int64_t)t0 * rows : aux;
+      rc = launch_matvec(s, kind, w, row_bytes, rows, cols, work, n, y + (int64_t)t0 * rows, rows, epi, a);
+    }
+    if (rc) return rc;
+  }
+  return MI_OK;
+}
+
 int mi_matvec(mi_stream stream, int kind, const void* w, int64_t row_bytes, int32_t rows, int32_t cols,
               const float* x, int32_t tokens, float* y, int32_t epi, const float* aux, void* work,
               size_t work_bytes) {
   int rc = check_weight("matvec", kind, w, row_bytes, rows, cols);
   if (rc) return rc;
   if (!x) return fail(MI_ERR_ARG, "matvec: null input");
+  if (tokens > kMaxTokens) {
+    if (tokens > kMaxPrefill) return fail(MI_ERR_ARG, "matvec: tokens %d above %d", tokens, kMaxPrefill);
+    if (!y) return fail(MI_ERR_ARG, "matvec: null output");
+    if (epi & ~(MI_EPI_BIAS | MI_EPI_ADD | MI_EPI_GLU | MI_ACT_GELU))
+      return fail(MI_ERR_ARG, "matvec: unknown epilogue bits 0x%x", epi);
+    if ((epi & MI_EPI_BIAS) && (epi & MI_EPI_GLU)) return fail(MI_ERR_ARG, "matvec: BIAS and GLU together");
+    if ((epi & (MI_EPI_BIAS | MI_EPI_GLU)) && !aux) return fail(MI_ERR_ARG, "matvec: epilogue needs aux");
+    return matmul_many(stream, kind, w, row_bytes, rows, cols, x, tokens, y, epi, aux, work, work_bytes);
+  }
   if ((rc = check_xq("matvec", work, cols, tokens))) return rc;
   if (work_bytes < mi_matvec_workspace(cols, tokens))
     return fail(MI_ERR_WORKSPACE, "matvec: workspace of %zu bytes, %zu needed", work_bytes,

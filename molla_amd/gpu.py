@@ -141,7 +141,8 @@ def device_matmul_into(ctx: DeviceContext, w: Tensor, x: torch.Tensor, out: torc
     check_matvec_shapes(w, x.numel(), out.numel() - at, tokens)
     if aux is not None:
         _f32(aux, "aux")
-    need = lib().mi_matvec_workspace(w.cols, tokens)
+    # with room for split-K partial sums when the chunk is a prefill one
+    need = lib().mi_matmul_workspace(w.rows, w.cols, tokens)
     work = ctx.workspace(need)
     y = out.data_ptr() + 4 * at
     # aux defaults to the output when the epilogue does not read it (gpu.mojo:2217)
