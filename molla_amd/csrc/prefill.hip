@@ -42,6 +42,8 @@
 // planar_matmul_kernel, :2665 planar_nvmma_kernel; dispatch :3015) for
 // tokens above the decode batch; output layout and epilogues as
 // gpu.mojo:1005 and :2955-2961.
+#include <type_traits>
+
 #include "matvec_units.h"
 
 namespace mi {
@@ -49,13 +51,15 @@ namespace {
 
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef float v16f __attribute__((ext_vector_type(16)));
+typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 
 constexpr int kTileTok = 32;     // tokens of one MFMA tile
 constexpr int kStage = 64;       // values of K per LDS stage (4 MFMA steps)
 constexpr int kChunk = 256;      // values per min-term MFMA / K-quant superblock
 constexpr int kWaveTok = 2;      // token tiles per wave (and per block)
-constexpr int kWaveRows = 2;     // row tiles per wave
+constexpr int kWaveRows = 2;     // row tiles per wave (the pipeline below writes out two)
 constexpr int kStageBytes = kWaveTok * 4 * 2 * 1024;  // one LDS buffer
+constexpr int kRing = 4;         // register slots: stages in flight + 1
 
 __device__ __forceinline__ v16f mfma(v8h a, v8h b, v16f c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
@@ -100,19 +104,35 @@ __device__ __forceinline__ void kscale(uint32_t y, uint32_t z, uint32_t w, int j
   m = __builtin_amdgcn_ubfe(hi ? w : z, s + 4 * hi, 4) | (__builtin_amdgcn_ubfe(z, s + 4 + 2 * hi, 2) << 4);
 }
 
-__device__ __forceinline__ v8h codes8(const int (&c)[8]) {
-  v8h b;
-#pragma unroll
-  for (int i = 0; i < 8; i++) b[i] = (_Float16)(short)c[i];
-  return b;
+typedef _Float16 v2h __attribute__((ext_vector_type(2)));
+
+// Eight byte codes u (0..255, bytes of t0 then t1) as the halves 1024 + u:
+// 0x64 above each byte is the exponent of 1024, the byte the mantissa.
+__device__ __forceinline__ v8h magic8(uint32_t t0, uint32_t t1) {
+  return as_v8h(make_uint4(__builtin_amdgcn_perm(0x64646464u, t0, 0x04010400u),
+                           __builtin_amdgcn_perm(0x64646464u, t0, 0x04030402u),
+                           __builtin_amdgcn_perm(0x64646464u, t1, 0x04010400u),
+                           __builtin_amdgcn_perm(0x64646464u, t1, 0x04030402u)));
+}
+__device__ __forceinline__ v8h splat8(_Float16 v) { return v8h{v, v, v, v, v, v, v, v}; }
+// (1024 + u) * a + b, once rounded: exact when the result is a small integer.
+__device__ __forceinline__ v8h fma8(v8h v, _Float16 a, _Float16 b) {
+  return __builtin_elementwise_fma(v, splat8(a), splat8(b));
 }
 
 // ---- per-kind weight access ------------------------------------------------
 // Raw: what one lane reads of one row for one stage (64 values of K);
 // load(raw, row, stage, kh); codes(raw, stage, s4, kh, b0, b1) for MFMA step
-// s4 (0..3) of the stage, b1 only when LIMBS == 2.
+// s4 (0..3) of the stage, b1 only when LIMBS == 2.  Codes are made in half
+// precision from "magic" halves 1024 + u (magic8), so each pair of values
+// costs a byte permute and one packed multiply-add.
 // GROUP: values per block scale.  MIN: 0 none, 1 K-quant dmin * m (scaled per
 // superblock), 2 m per 32-value block (Q4_1, Q5_1).
+
+__device__ __forceinline__ v8h kquant_codes(uint32_t t0, uint32_t t1, uint32_t sc) {
+  // sc * u = (1024 + u) * sc - 1024 * sc; both terms exact halves (sc < 64)
+  return fma8(magic8(t0, t1), (_Float16)(float)sc, (_Float16)(-1024.0f * (float)sc));
+}
 
 struct KQ4K {
   static constexpr int GROUP = 256, LIMBS = 1, MIN = 1, BLOCK = 144;
@@ -127,28 +147,25 @@ struct KQ4K {
     r.q[0] = *(const uint2*)q;
     r.q[1] = *(const uint2*)(q + 16);
   }
-  static __device__ __forceinline__ void codes(const Raw& r, int st, int s4, int kh, v8h& b0, v8h&) {
+  static __device__ __forceinline__ void codes(const Raw& r, int st, int s4, int, v8h& b0, v8h&) {
     const int j = 2 * (st & 3) + (s4 >> 1);
     uint32_t sc, m;
     kscale(r.hdr.y, r.hdr.z, r.hdr.w, j, sc, m);
     const uint2 q = r.q[s4 & 1];
     const int sh = 4 * (s4 >> 1);
-    int c[8];
-#pragma unroll
-    for (int i = 0; i < 8; i++) c[i] = (int)(((byte_of(q, i) >> sh) & 0xF) * sc);
-    b0 = codes8(c);
+    b0 = kquant_codes((q.x >> sh) & 0x0F0F0F0Fu, (q.y >> sh) & 0x0F0F0F0Fu, sc);
   }
   static __device__ __forceinline__ float d(const Raw& r) { return f16f(r.hdr.x); }
   static __device__ __forceinline__ float dmin(const Raw& r) { return f16f(r.hdr.x >> 16); }
   static __device__ __forceinline__ v8h mins(const Raw& r) {
-    int c[8];
+    v8h c;
 #pragma unroll
     for (int j = 0; j < 8; j++) {
       uint32_t sc, m;
       kscale(r.hdr.y, r.hdr.z, r.hdr.w, j, sc, m);
-      c[j] = (int)m;
+      c[j] = (_Float16)(float)m;
     }
-    return codes8(c);
+    return c;
   }
 };
 
@@ -167,17 +184,16 @@ struct KQ5K {
     r.q[0] = *(const uint2*)q;
     r.q[1] = *(const uint2*)(q + 16);
   }
-  static __device__ __forceinline__ void codes(const Raw& r, int st, int s4, int kh, v8h& b0, v8h&) {
+  static __device__ __forceinline__ void codes(const Raw& r, int st, int s4, int, v8h& b0, v8h&) {
     const int j = 2 * (st & 3) + (s4 >> 1);
     uint32_t sc, m;
     kscale(r.hdr.y, r.hdr.z, r.hdr.w, j, sc, m);
     const uint2 q = r.q[s4 & 1], h = r.qh[s4 & 1];
     const int sh = 4 * (s4 >> 1);
-    int c[8];
-#pragma unroll
-    for (int i = 0; i < 8; i++)
-      c[i] = (int)((((byte_of(q, i) >> sh) & 0xF) | (((byte_of(h, i) >> j) & 1) << 4)) * sc);
-    b0 = codes8(c);
+    // the fifth bit of value i is bit j of qh byte i
+    const uint32_t t0 = ((q.x >> sh) & 0x0F0F0F0Fu) | (((h.x >> j) & 0x01010101u) << 4);
+    const uint32_t t1 = ((q.y >> sh) & 0x0F0F0F0Fu) | (((h.y >> j) & 0x01010101u) << 4);
+    b0 = kquant_codes(t0, t1, sc);
   }
   static __device__ __forceinline__ float d(const Raw& r) { return f16f(r.hdr.x); }
   static __device__ __forceinline__ float dmin(const Raw& r) { return f16f(r.hdr.x >> 16); }
@@ -187,7 +203,8 @@ struct KQ5K {
 // Q6_K (quant.mojo:371): stage st' = st % 4 of a superblock covers half
 // n = st' / 2 and quarters 2 (st' % 2) + {0, 1}; step s4 is quarter
 // 2 (st' % 2) + s4 / 2, values 16 (s4 % 2) + 8 kh .. +8 of it, whose scale is
-// sc[8n + 4 (st' % 2) + s4].
+// sc[8n + 4 (st' % 2) + s4].  sc * (q - 32) reaches 4096 in magnitude: b0 is
+// its nearest half, b1 the remainder (-1, 0 or 1), both exact.
 struct KQ6K {
   static constexpr int GROUP = 256, LIMBS = 2, MIN = 0, BLOCK = 210;
   struct Raw {
@@ -210,18 +227,13 @@ struct KQ6K {
     const int sp = st & 3, a = s4 >> 1, c = s4 & 1;
     const int kq = 2 * (sp & 1) + a;
     const int nib = 4 * (sp & 1);
-    const int sc = (int)(int8_t)(r.sc >> (8 * s4));
+    const _Float16 sc = (_Float16)(float)(int8_t)(r.sc >> (8 * s4));
     const uint2 ql = r.ql[a][c], qh = r.qh[c];
-    int e[8], o[8];
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-      const int q = (int)(((byte_of(ql, i) >> nib) & 0xF) | (((byte_of(qh, i) >> (2 * kq)) & 3) << 4)) - 32;
-      const int w = sc * q;
-      e[i] = w & ~1;
-      o[i] = w & 1;
-    }
-    b0 = codes8(e);
-    b1 = codes8(o);
+    const uint32_t t0 = ((ql.x >> nib) & 0x0F0F0F0Fu) | (((qh.x >> (2 * kq)) & 0x03030303u) << 4);
+    const uint32_t t1 = ((ql.y >> nib) & 0x0F0F0F0Fu) | (((qh.y >> (2 * kq)) & 0x03030303u) << 4);
+    const v8h q = magic8(t0, t1) - splat8((_Float16)1056.0f);  // q - 32, exact
+    b0 = q * splat8(sc);
+    b1 = __builtin_elementwise_fma(q, splat8(sc), -b0);
   }
   static __device__ __forceinline__ float d(const Raw& r) { return f16f(r.dbits); }
   static __device__ __forceinline__ float dmin(const Raw&) { return 0.0f; }
@@ -236,6 +248,8 @@ struct KB32 {
   static constexpr int MIN = (KIND == MI_Q4_1 || KIND == MI_Q5_1) ? 2 : 0;
   static constexpr int BLOCK = KIND == MI_Q8_0 ? 34 : KIND == MI_Q4_0 ? 18 : KIND == MI_Q4_1 ? 20
                                : KIND == MI_Q5_0 ? 22 : 24;
+  // u of the magic halves is the unsigned code; the signed one is u - BIAS
+  static constexpr float BIAS = KIND == MI_Q8_0 ? 128.0f : KIND == MI_Q4_0 ? 8.0f : KIND == MI_Q5_0 ? 16.0f : 0.0f;
   struct Raw {
     uint32_t dm[2];    // d | m << 16
     uint32_t qh[2];    // Q5_0 / Q5_1 fifth bits
@@ -268,23 +282,20 @@ struct KB32 {
   }
   static __device__ __forceinline__ void codes(const Raw& r, int, int s4, int kh, v8h& b0, v8h&) {
     const int bb = s4 >> 1, hf = s4 & 1;
-    int c[8];
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-      if (KIND == MI_Q8_0) {
-        c[i] = (int)(int8_t)byte_of(r.q[bb][hf], i);
-      } else {
-        const uint32_t nb = (byte_of(r.q[bb][0], i) >> (4 * hf)) & 0xF;
-        if (KIND == MI_Q4_0) c[i] = (int)nb - 8;
-        else if (KIND == MI_Q4_1) c[i] = (int)nb;
-        else {
-          const int l = 16 * hf + 8 * kh + i;
-          const int q = (int)(nb | (((r.qh[bb] >> l) & 1) << 4));
-          c[i] = KIND == MI_Q5_0 ? q - 16 : q;
-        }
+    uint32_t t0, t1;
+    if (KIND == MI_Q8_0) {
+      t0 = r.q[bb][hf].x ^ 0x80808080u;  // int8 + 128
+      t1 = r.q[bb][hf].y ^ 0x80808080u;
+    } else {
+      t0 = (r.q[bb][0].x >> (4 * hf)) & 0x0F0F0F0Fu;
+      t1 = (r.q[bb][0].y >> (4 * hf)) & 0x0F0F0F0Fu;
+      if (KIND == MI_Q5_0 || KIND == MI_Q5_1) {  // bit l of qh is value l's fifth
+        const uint32_t bits = (r.qh[bb] >> (16 * hf + 8 * kh)) & 0xFFu;
+        t0 |= mv::spread4(bits & 0xFu) << 4;
+        t1 |= mv::spread4(bits >> 4) << 4;
       }
     }
-    b0 = codes8(c);
+    b0 = magic8(t0, t1) - splat8((_Float16)(1024.0f + BIAS));
   }
   static __device__ __forceinline__ float d(const Raw& r, int bb) { return f16f(r.dm[bb]); }
   static __device__ __forceinline__ uint32_t mbits(const Raw& r, int bb) { return r.dm[bb] >> 16; }
@@ -331,76 +342,88 @@ __device__ __forceinline__ void split_half(float v, _Float16& hi, _Float16& lo) 
   lo = (_Float16)(v - (float)hi);
 }
 
-// One block per token (padding tokens write zeros).
-__global__ __launch_bounds__(256) void prefill_x_kernel(const float* __restrict__ x, int cols, int tokens,
-                                                        uint8_t* __restrict__ work) {
+// Each token's scale: the power of two 2^e with its largest |x| * 2^-e in
+// [2^13, 2^14) (e clamped so the scale stays a normal float; 1 for a zero or
+// padding token).  One block per token, xs[t] = 2^e.
+__global__ __launch_bounds__(256) void prefill_scale_kernel(const float* __restrict__ x, int cols, int tokens,
+                                                            uint8_t* __restrict__ work) {
   const Prep P = prep_layout(cols, tokens);
   const int t = blockIdx.x;
-  const bool live = t < tokens;
-  const float* row = x + (int64_t)(live ? t : 0) * cols;
-  const int nc = cols >> 3;  // 8-value chunks
   __shared__ float red[4];
   float mx = 0.0f;
-  for (int c = threadIdx.x; c < nc; c += blockDim.x) {
-    if (!live) break;
-    const float4 a = *(const float4*)(row + 8 * c), b = *(const float4*)(row + 8 * c + 4);
-    mx = fmaxf(mx, fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))));
-    mx = fmaxf(mx, fmaxf(fmaxf(fabsf(b.x), fabsf(b.y)), fmaxf(fabsf(b.z), fabsf(b.w))));
+  if (t < tokens) {
+    const float4* row = (const float4*)(x + (int64_t)t * cols);
+    for (int c = threadIdx.x; c < (cols >> 2); c += blockDim.x) {
+      const float4 a = row[c];
+      mx = fmaxf(mx, fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))));
+    }
   }
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
   __syncthreads();
-  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  // largest |x| * 2^-e in [2^13, 2^14); the exponent is clamped so the scale
-  // stays a normal float
-  int e = 0;
-  if (mx > 0.0f) e = min(max(ilogbf(mx) - 13, -100), 100);
-  if (threadIdx.x == 0) ((float*)(work + P.xs))[t] = ldexpf(1.0f, e);
-  const int tile = t >> 5, m = t & 31;
-  for (int c = threadIdx.x; c < nc; c += blockDim.x) {
+  if (threadIdx.x == 0) {
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    const int e = mx > 0.0f ? min(max(ilogbf(mx) - 13, -100), 100) : 0;
+    ((float*)(work + P.xs))[t] = ldexpf(1.0f, e);
+  }
+}
+
+// The halves and block means of one 256-value chunk of one 32-token tile
+// (grid: chunks x tiles).  Thread f of 1024 fragments per chunk holds step
+// f / 64, lane f % 64; consecutive threads write consecutive 16 bytes.
+__global__ __launch_bounds__(256) void prefill_x_kernel(const float* __restrict__ x, int cols, int tokens,
+                                                        uint8_t* __restrict__ work) {
+  const Prep P = prep_layout(cols, tokens);
+  const int ch = blockIdx.x, tile = blockIdx.y;
+  const int steps = min(16, (cols >> 4) - ch * 16);  // the last chunk may be short
+  const float* xs = (const float*)(work + P.xs);
+  __shared__ float part[16][2][32];  // [step][kh][token] sums of 8 values
+#pragma unroll
+  for (int q = 0; q < 4; q++) {
+    const int f = threadIdx.x + 256 * q;
+    const int s = f >> 6, L = f & 63, m = L & 31, kh = L >> 5;
+    if (s >= steps) continue;
+    const int t = tile * 32 + m;
     float v[8];
-    if (live) {
-      const float4 a = *(const float4*)(row + 8 * c), b = *(const float4*)(row + 8 * c + 4);
-      v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w, v[4] = b.x, v[5] = b.y, v[6] = b.z, v[7] = b.w;
+    if (t < tokens) {
+      const float* src = x + (int64_t)t * cols + ch * 256 + 16 * s + 8 * kh;
+      const float4 a = *(const float4*)src, b = *(const float4*)(src + 4);
+      const int e = ilogbf(xs[t]);
+      v[0] = ldexpf(a.x, -e), v[1] = ldexpf(a.y, -e), v[2] = ldexpf(a.z, -e), v[3] = ldexpf(a.w, -e);
+      v[4] = ldexpf(b.x, -e), v[5] = ldexpf(b.y, -e), v[6] = ldexpf(b.z, -e), v[7] = ldexpf(b.w, -e);
     } else {
 #pragma unroll
       for (int i = 0; i < 8; i++) v[i] = 0.0f;
     }
     v8h hi, lo;
-    float s = 0.0f;
+    float sum = 0.0f;
 #pragma unroll
     for (int i = 0; i < 8; i++) {
-      const float u = ldexpf(v[i], -e);
       _Float16 h, l;
-      split_half(u, h, l);
+      split_half(v[i], h, l);
       hi[i] = h;
       lo[i] = l;
-      s += u;
+      sum += v[i];
     }
-    const int step = c >> 1, kh = c & 1;
-    uint8_t* dst = work + P.xp + ((size_t)(tile * P.ks + step) * 2) * 1024 + (kh * 32 + m) * 16;
+    uint8_t* dst = work + P.xp + ((size_t)(tile * P.ks + ch * 16 + s) * 2) * 1024 + L * 16;
     *(v8h*)dst = hi;
     *(v8h*)(dst + 1024) = lo;
-    // the 32-value block's sum: four consecutive lanes hold its four chunks
-    s += __shfl_xor(s, 1);
-    s += __shfl_xor(s, 2);
-    if ((c & 3) == 0) {
-      const int blk = c >> 2, ch = blk >> 3, j = blk & 7;
-      _Float16 h, l;
-      split_half(s * (1.0f / 32.0f), h, l);  // a mean: 32 values of up to 2^14 overflow a half
-      _Float16* mdst = (_Float16*)(work + P.xm + (size_t)(tile * P.nch + ch) * 1024);
-      mdst[m * 8 + j] = h;
-      mdst[(32 + m) * 8 + j] = l;
-    }
+    part[s][kh][m] = sum;
   }
-  // the last chunk's slots past cols
-  const int nb = cols >> 5;
-  for (int blk = nb + threadIdx.x; blk < P.nch * 8; blk += blockDim.x) {
-    _Float16* mdst = (_Float16*)(work + P.xm + (size_t)(tile * P.nch + (blk >> 3)) * 1024);
-    mdst[m * 8 + (blk & 7)] = (_Float16)0.0f;
-    mdst[(32 + m) * 8 + (blk & 7)] = (_Float16)0.0f;
-  }
+  __syncthreads();
+  // thread (g, m): the mean of 32-value block g of the chunk for token m (a
+  // mean, since 32 values of up to 2^14 overflow a half); zero past cols
+  const int g = threadIdx.x >> 5, m = threadIdx.x & 31;
+  float mean = 0.0f;
+  if (2 * g + 1 < steps)
+    mean = ((part[2 * g][0][m] + part[2 * g][1][m]) + (part[2 * g + 1][0][m] + part[2 * g + 1][1][m])) *
+           (1.0f / 32.0f);
+  _Float16 h, l;
+  split_half(mean, h, l);
+  _Float16* mdst = (_Float16*)(work + P.xm + (size_t)(tile * P.nch + ch) * 1024);
+  mdst[m * 8 + g] = h;
+  mdst[(32 + m) * 8 + g] = l;
 }
 
 // ---- the matmul ------------------------------------------------------------
@@ -426,22 +449,39 @@ __global__ __launch_bounds__(W * 64) void prefill_kernel(const uint8_t* __restri
 
   // activation stage copy: 16 KB, four 16-byte pieces a thread
   const uint8_t* xp = work + P.xp;
-  uint4 xr[kStageBytes / 16 / (W * 64) > 0 ? kStageBytes / 16 / (W * 64) : 1];
   constexpr int kPieces = kStageBytes / 16 / (W * 64);
-  auto load_x = [&](int st) {
+  static_assert(kPieces * 16 * W * 64 == kStageBytes, "stage copy");
+  // the register ring (a native vector type: HIP's uint4 struct is copied through memory)
+  v4u xr0[kPieces], xr1[kPieces], xr2[kPieces], xr3[kPieces];
+  // piece q of a stage's activation copy: 16 bytes of tile tt, offset within
+  const size_t x_tile = (size_t)P.ks * 2048;
+  const uint8_t* xsrc[kPieces];
+  int xdst[kPieces];
 #pragma unroll
-    for (int q = 0; q < kPieces; q++) {
-      const int idx = threadIdx.x + q * W * 64;
-      const int tt = idx >> 9, within = idx & 511;
-      xr[q] = *(const uint4*)(xp + ((size_t)((tile0 + tt) * P.ks + st * 4) * 2) * 1024 + within * 16);
-    }
-  };
-  auto store_x = [&](int buf) {
-#pragma unroll
-    for (int q = 0; q < kPieces; q++) *(uint4*)(&xl[buf][(threadIdx.x + q * W * 64) * 16]) = xr[q];
-  };
+  for (int q = 0; q < kPieces; q++) {
+    const int idx = threadIdx.x + q * W * 64;
+    const int tt = idx >> 9, within = idx & 511;
+    xsrc[q] = xp + (tile0 + tt) * x_tile + within * 16;
+    xdst[q] = idx * 16;
+  }
+  static_assert(kPieces == 4, "the copy below is written out for four pieces");
+#define PF_LOAD_X(ST, DST)                                         \
+  {                                                                \
+    const size_t o_ = (size_t)(ST) * 8192;                         \
+    DST[0] = *(const v4u*)(xsrc[0] + o_);                        \
+    DST[1] = *(const v4u*)(xsrc[1] + o_);                        \
+    DST[2] = *(const v4u*)(xsrc[2] + o_);                        \
+    DST[3] = *(const v4u*)(xsrc[3] + o_);                        \
+  }
+#define PF_STORE_X(SRC, BUF)                      \
+  {                                               \
+    *(v4u*)(&xl[BUF][xdst[0]]) = SRC[0];        \
+    *(v4u*)(&xl[BUF][xdst[1]]) = SRC[1];        \
+    *(v4u*)(&xl[BUF][xdst[2]]) = SRC[2];        \
+    *(v4u*)(&xl[BUF][xdst[3]]) = SRC[3];        \
+  }
 
-  typename K::Raw raw[2][kWaveRows];
+  typename K::Raw raw[kRing][kWaveRows];
   v16f tot[kWaveRows][kWaveTok], acc[kWaveRows][kWaveTok];
   const v16f zero = {};
 #pragma unroll
@@ -455,21 +495,13 @@ __global__ __launch_bounds__(W * 64) void prefill_kernel(const uint8_t* __restri
 #pragma unroll
     for (int q = 0; q < 4; q++) mrec[rt][q] = 0;
 
-  load_x(st0);
-#pragma unroll
-  for (int rt = 0; rt < kWaveRows; rt++) K::load(raw[0][rt], wrow[rt], st0, kh);
-  store_x(0);
-  __syncthreads();
-
-  for (int st = st0; st < st1; st++) {
-    const int cur = (st - st0) & 1;
-    const bool more = st + 1 < st1;
-    if (more) {
-      load_x(st + 1);
-#pragma unroll
-      for (int rt = 0; rt < kWaveRows; rt++) K::load(raw[cur ^ 1][rt], wrow[rt], st + 1, kh);
-    }
-    if (K::MIN && (st & 3) == 0) {
+  // One stage of the reduction, stage C (static) of its 256-value chunk: x
+  // from LDS buffer C % 2, weights from rw.  Stages past st1 (the tail of a
+  // short last chunk) run on clamped loads and count with factor zero.
+  auto stage = [&](auto cc, int st, const typename K::Raw (&rw)[kWaveRows]) __attribute__((always_inline)) {
+    constexpr int C = decltype(cc)::value;
+    const bool live = st < st1;
+    if constexpr (K::MIN != 0 && C == 0) {
 #pragma unroll
       for (int tt = 0; tt < kWaveTok; tt++)
         am[tt] = *(const uint4*)(work + P.xm + (size_t)((tile0 + tt) * P.nch + (st >> 2)) * 1024 + lane * 16);
@@ -478,16 +510,16 @@ __global__ __launch_bounds__(W * 64) void prefill_kernel(const uint8_t* __restri
     for (int s4 = 0; s4 < 4; s4++) {
       v8h b0[kWaveRows], b1[kWaveRows];
 #pragma unroll
-      for (int rt = 0; rt < kWaveRows; rt++) K::codes(raw[cur][rt], st, s4, kh, b0[rt], b1[rt]);
+      for (int rt = 0; rt < kWaveRows; rt++) K::codes(rw[rt], C, s4, kh, b0[rt], b1[rt]);
 #pragma unroll
       for (int tt = 0; tt < kWaveTok; tt++) {
-        const uint8_t* base = &xl[cur][((tt * 4 + s4) * 2) * 1024 + lane * 16];
+        const uint8_t* base = &xl[C & 1][((tt * 4 + s4) * 2) * 1024 + lane * 16];
         const v8h ahi = as_v8h(*(const uint4*)base), alo = as_v8h(*(const uint4*)(base + 1024));
 #pragma unroll
         for (int rt = 0; rt < kWaveRows; rt++) {
           acc[rt][tt] = mfma(ahi, b0[rt], acc[rt][tt]);
           acc[rt][tt] = mfma(alo, b0[rt], acc[rt][tt]);
-          if (K::LIMBS == 2) acc[rt][tt] = mfma(ahi, b1[rt], acc[rt][tt]);
+          if constexpr (K::LIMBS == 2) acc[rt][tt] = mfma(ahi, b1[rt], acc[rt][tt]);
         }
       }
       if constexpr (K::GROUP == 32) {
@@ -495,30 +527,28 @@ __global__ __launch_bounds__(W * 64) void prefill_kernel(const uint8_t* __restri
         const int bb = s4 >> 1;
 #pragma unroll
         for (int rt = 0; rt < kWaveRows; rt++) {
-          const float dv = K::d(raw[cur][rt], bb);
+          const float dv = live ? K::d(rw[rt], bb) : 0.0f;
 #pragma unroll
           for (int tt = 0; tt < kWaveTok; tt++) {
             tot[rt][tt] += dv * acc[rt][tt];
             acc[rt][tt] = zero;
           }
           if constexpr (K::MIN == 2) {
-            const int slot = 2 * (st & 3) + bb;  // block of the chunk
-            const uint32_t mb = K::mbits(raw[cur][rt], bb);
-#pragma unroll
-            for (int q = 0; q < 4; q++)
-              if (q == (slot >> 1)) mrec[rt][q] = (slot & 1) ? (mrec[rt][q] | (mb << 16)) : mb;
+            const int slot = 2 * C + bb;  // block of the chunk
+            const uint32_t mb = live ? K::mbits(rw[rt], bb) : 0u;
+            mrec[rt][slot >> 1] = (slot & 1) ? (mrec[rt][slot >> 1] | (mb << 16)) : mb;
           }
         }
        }
       }
     }
     if constexpr (K::GROUP == 256) {
-     if ((st & 3) == 3) {  // a superblock ends
+     if constexpr (C == 3) {  // a superblock ends
 #pragma unroll
       for (int rt = 0; rt < kWaveRows; rt++) {
-        const float dv = K::d(raw[cur][rt]);
-        const float dm = K::dmin(raw[cur][rt]);
-        const v8h bm = K::mins(raw[cur][rt]);
+        const float dv = K::d(rw[rt]);
+        const float dm = K::dmin(rw[rt]);
+        const v8h bm = K::mins(rw[rt]);
 #pragma unroll
         for (int tt = 0; tt < kWaveTok; tt++) {
           tot[rt][tt] += dv * acc[rt][tt];
@@ -532,20 +562,55 @@ __global__ __launch_bounds__(W * 64) void prefill_kernel(const uint8_t* __restri
      }
     }
     if constexpr (K::MIN == 2) {
-     if ((st & 3) == 3 || st + 1 == st1) {  // a chunk of eight blocks ends
+     if constexpr (C == 3) {  // a chunk of eight blocks ends
 #pragma unroll
       for (int rt = 0; rt < kWaveRows; rt++) {
         const v8h bm = as_v8h(make_uint4(mrec[rt][0], mrec[rt][1], mrec[rt][2], mrec[rt][3]));
 #pragma unroll
         for (int tt = 0; tt < kWaveTok; tt++) tot[rt][tt] += 32.0f * mfma(as_v8h(am[tt]), bm, zero);
-#pragma unroll
-        for (int q = 0; q < 4; q++) mrec[rt][q] = 0;
       }
      }
     }
-    if (more) store_x(cur ^ 1);
+  };
+
+  // Pipeline, branch-free within a chunk of four stages: stage st's weights
+  // and activations are loaded three stages ahead into register slot
+  // (st - st0) % 4 (loads past st1 are clamped to its last stage), its
+  // activations move to LDS (double-buffered) one stage ahead, and one
+  // barrier closes each stage.  st0 is a whole chunk.
+#define PF_ISSUE(ST, RW, XD)                                                           \
+  {                                                                                    \
+    const int ist = min((ST), st1 - 1);                                                \
+    PF_LOAD_X(ist, XD)                                                                 \
+    K::load(RW[0], wrow[0], ist, kh);                                                  \
+    K::load(RW[1], wrow[1], ist, kh);                                                  \
+  }
+  PF_ISSUE(st0, raw[0], xr0)
+  PF_ISSUE(st0 + 1, raw[1], xr1)
+  PF_ISSUE(st0 + 2, raw[2], xr2)
+  PF_STORE_X(xr0, 0)
+  __syncthreads();
+  for (int base = st0; base < st1; base += 4) {
+    PF_ISSUE(base + 3, raw[3], xr3)
+    stage(std::integral_constant<int, 0>{}, base, raw[0]);
+    PF_STORE_X(xr1, 1)
+    __syncthreads();
+    PF_ISSUE(base + 4, raw[0], xr0)
+    stage(std::integral_constant<int, 1>{}, base + 1, raw[1]);
+    PF_STORE_X(xr2, 0)
+    __syncthreads();
+    PF_ISSUE(base + 5, raw[1], xr1)
+    stage(std::integral_constant<int, 2>{}, base + 2, raw[2]);
+    PF_STORE_X(xr3, 1)
+    __syncthreads();
+    PF_ISSUE(base + 6, raw[2], xr2)
+    stage(std::integral_constant<int, 3>{}, base + 3, raw[3]);
+    PF_STORE_X(xr0, 0)
     __syncthreads();
   }
+#undef PF_ISSUE
+#undef PF_LOAD_X
+#undef PF_STORE_X
 
   // results: element j of tile (rt, tt) is token 32 (tile0 + tt) + 8 (j / 4) +
   // 4 kh + j % 4, row row_base + 32 rt + n
@@ -641,7 +706,9 @@ int launch_prefill(hipStream_t s, int kind, const void* w, int64_t row_bytes, in
                    const float* x, int32_t tokens, float* y, int64_t ldy, int32_t epi, const float* aux, void* work,
                    size_t work_bytes) {
   const Prep P = prep_layout(cols, tokens);
-  hipLaunchKernelGGL(prefill_x_kernel, dim3(P.ttp * kTileTok), dim3(256), 0, s, x, cols, tokens, (uint8_t*)work);
+  hipLaunchKernelGGL(prefill_scale_kernel, dim3(P.ttp * kTileTok), dim3(256), 0, s, x, cols, tokens,
+                     (uint8_t*)work);
+  hipLaunchKernelGGL(prefill_x_kernel, dim3(P.nch, P.ttp), dim3(256), 0, s, x, cols, tokens, (uint8_t*)work);
   int rc = hip_check(hipGetLastError(), "prefill activation launch");
   if (rc) return rc;
   int splits = choose_splits(rows, cols, tokens);
