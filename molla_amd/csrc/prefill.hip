@@ -59,12 +59,13 @@ constexpr int kChunk = 256;      // values per min-term MFMA / K-quant superbloc
 constexpr int kWaveTok = 2;      // token tiles per wave (and per block)
 constexpr int kWaveRows = 2;     // row tiles per wave (the pipeline below writes out two)
 constexpr int kStageBytes = kWaveTok * 4 * 2 * 1024;  // one LDS buffer
-constexpr int kRing = 4;         // register slots: stages in flight + 1
+constexpr int kRing = 2;         // register slots: the stage computed and the one in flight
 
 __device__ __forceinline__ v16f mfma(v8h a, v8h b, v16f c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
+__device__ __forceinline__ v8h as_v8h4(v4u u) { return __builtin_bit_cast(v8h, u); }
 __device__ __forceinline__ v8h as_v8h(uint4 u) {
   union {
     uint4 u;
@@ -80,16 +81,16 @@ __device__ __forceinline__ uint2 ld8(const uint8_t* p) {
   const uintptr_t a = (uintptr_t)p;
   const uint32_t* q = (const uint32_t*)(a & ~(uintptr_t)3);
   const uint32_t sh = (uint32_t)(a & 3);
-  const uint32_t d0 = q[0], d1 = q[1];
-  if (sh == 0) return make_uint2(d0, d1);
-  const uint32_t d2 = q[2];
+  // branch-free: aligned, the third load repeats the second (in bounds) and
+  // a zero shift passes the low dword through
+  const uint32_t d0 = q[0], d1 = q[1], d2 = q[sh ? 2 : 1];
   return make_uint2(__builtin_amdgcn_alignbyte(d1, d0, sh), __builtin_amdgcn_alignbyte(d2, d1, sh));
 }
 __device__ __forceinline__ uint32_t ld4u(const uint8_t* p) {
   const uintptr_t a = (uintptr_t)p;
   const uint32_t* q = (const uint32_t*)(a & ~(uintptr_t)3);
   const uint32_t sh = (uint32_t)(a & 3);
-  return sh ? __builtin_amdgcn_alignbyte(q[1], q[0], sh) : q[0];
+  return __builtin_amdgcn_alignbyte(q[sh ? 1 : 0], q[0], sh);
 }
 __device__ __forceinline__ uint32_t ld2(const uint8_t* p) { return *(const uint16_t*)p; }
 __device__ __forceinline__ float f16f(uint32_t bits) { return half_bits_to_float(bits & 0xFFFF); }
@@ -428,7 +429,7 @@ __global__ __launch_bounds__(256) void prefill_x_kernel(const float* __restrict_
 
 // ---- the matmul ------------------------------------------------------------
 template <int KIND, int W>
-__global__ __launch_bounds__(W * 64) void prefill_kernel(const uint8_t* __restrict__ w, int64_t rb, int rows,
+__global__ __launch_bounds__(W * 64, KIND == MI_Q6_K ? 2 : 1) void prefill_kernel(const uint8_t* __restrict__ w, int64_t rb, int rows,
                                                          int cols, int tokens, const uint8_t* __restrict__ work,
                                                          int stages_per_split, float* __restrict__ y, int64_t ldy,
                                                          int epi, const float* __restrict__ aux,
@@ -452,7 +453,7 @@ __global__ __launch_bounds__(W * 64) void prefill_kernel(const uint8_t* __restri
   constexpr int kPieces = kStageBytes / 16 / (W * 64);
   static_assert(kPieces * 16 * W * 64 == kStageBytes, "stage copy");
   // the register ring (a native vector type: HIP's uint4 struct is copied through memory)
-  v4u xr0[kPieces], xr1[kPieces], xr2[kPieces], xr3[kPieces];
+  v4u xr0[kPieces], xr1[kPieces];
   // piece q of a stage's activation copy: 16 bytes of tile tt, offset within
   const size_t x_tile = (size_t)P.ks * 2048;
   const uint8_t* xsrc[kPieces];
@@ -488,7 +489,16 @@ __global__ __launch_bounds__(W * 64) void prefill_kernel(const uint8_t* __restri
   for (int rt = 0; rt < kWaveRows; rt++)
 #pragma unroll
     for (int tt = 0; tt < kWaveTok; tt++) tot[rt][tt] = acc[rt][tt] = zero;
-  uint4 am[kWaveTok];  // min-term A fragments of the current chunk
+  // min-term A fragments: the current chunk's, and the next one's in flight
+  // (loaded a chunk ahead so the min MFMA never waits on a fresh load)
+  v4u am[kWaveTok], am_next[kWaveTok];
+  auto load_am = [&](int chunk, v4u (&dst)[kWaveTok]) __attribute__((always_inline)) {
+    chunk = min(chunk, P.nch - 1);
+#pragma unroll
+    for (int tt = 0; tt < kWaveTok; tt++)
+      dst[tt] = *(const v4u*)(work + P.xm + (size_t)((tile0 + tt) * P.nch + chunk) * 1024 + lane * 16);
+  };
+  if (K::MIN) load_am(st0 >> 2, am);
   uint32_t mrec[kWaveRows][4];
 #pragma unroll
   for (int rt = 0; rt < kWaveRows; rt++)
@@ -501,11 +511,7 @@ __global__ __launch_bounds__(W * 64) void prefill_kernel(const uint8_t* __restri
   auto stage = [&](auto cc, int st, const typename K::Raw (&rw)[kWaveRows]) __attribute__((always_inline)) {
     constexpr int C = decltype(cc)::value;
     const bool live = st < st1;
-    if constexpr (K::MIN != 0 && C == 0) {
-#pragma unroll
-      for (int tt = 0; tt < kWaveTok; tt++)
-        am[tt] = *(const uint4*)(work + P.xm + (size_t)((tile0 + tt) * P.nch + (st >> 2)) * 1024 + lane * 16);
-    }
+    if constexpr (K::MIN != 0 && C == 0) load_am((st >> 2) + 1, am_next);
 #pragma unroll
     for (int s4 = 0; s4 < 4; s4++) {
       v8h b0[kWaveRows], b1[kWaveRows];
@@ -514,7 +520,7 @@ __global__ __launch_bounds__(W * 64) void prefill_kernel(const uint8_t* __restri
 #pragma unroll
       for (int tt = 0; tt < kWaveTok; tt++) {
         const uint8_t* base = &xl[C & 1][((tt * 4 + s4) * 2) * 1024 + lane * 16];
-        const v8h ahi = as_v8h(*(const uint4*)base), alo = as_v8h(*(const uint4*)(base + 1024));
+        const v8h ahi = as_v8h4(*(const v4u*)base), alo = as_v8h4(*(const v4u*)(base + 1024));
 #pragma unroll
         for (int rt = 0; rt < kWaveRows; rt++) {
           acc[rt][tt] = mfma(ahi, b0[rt], acc[rt][tt]);
@@ -554,7 +560,7 @@ __global__ __launch_bounds__(W * 64) void prefill_kernel(const uint8_t* __restri
           tot[rt][tt] += dv * acc[rt][tt];
           acc[rt][tt] = zero;
           if constexpr (K::MIN == 1) {
-            const v16f mn = mfma(as_v8h(am[tt]), bm, zero);
+            const v16f mn = mfma(as_v8h4(am[tt]), bm, zero);
             tot[rt][tt] -= (32.0f * dm) * mn;
           }
         }
@@ -567,17 +573,19 @@ __global__ __launch_bounds__(W * 64) void prefill_kernel(const uint8_t* __restri
       for (int rt = 0; rt < kWaveRows; rt++) {
         const v8h bm = as_v8h(make_uint4(mrec[rt][0], mrec[rt][1], mrec[rt][2], mrec[rt][3]));
 #pragma unroll
-        for (int tt = 0; tt < kWaveTok; tt++) tot[rt][tt] += 32.0f * mfma(as_v8h(am[tt]), bm, zero);
+        for (int tt = 0; tt < kWaveTok; tt++) tot[rt][tt] += 32.0f * mfma(as_v8h4(am[tt]), bm, zero);
       }
      }
     }
   };
 
-  // Pipeline, branch-free within a chunk of four stages: stage st's weights
-  // and activations are loaded three stages ahead into register slot
-  // (st - st0) % 4 (loads past st1 are clamped to its last stage), its
-  // activations move to LDS (double-buffered) one stage ahead, and one
-  // barrier closes each stage.  st0 is a whole chunk.
+  // Pipeline, branch-free within a chunk of four stages: stage st + 1's
+  // weights and activations are loaded into the other register slot while
+  // stage st computes (loads past st1 are clamped to its last stage), the
+  // activations then move to the other LDS buffer, and one barrier closes
+  // each stage.  st0 is a whole chunk.  Two slots rather than a deeper ring
+  // keep a wave under 256 registers, so two blocks share a CU and hide each
+  // other's load latency (measured: faster than four slots at one block).
 #define PF_ISSUE(ST, RW, XD)                                                           \
   {                                                                                    \
     const int ist = min((ST), st1 - 1);                                                \
@@ -586,25 +594,27 @@ __global__ __launch_bounds__(W * 64) void prefill_kernel(const uint8_t* __restri
     K::load(RW[1], wrow[1], ist, kh);                                                  \
   }
   PF_ISSUE(st0, raw[0], xr0)
-  PF_ISSUE(st0 + 1, raw[1], xr1)
-  PF_ISSUE(st0 + 2, raw[2], xr2)
   PF_STORE_X(xr0, 0)
   __syncthreads();
   for (int base = st0; base < st1; base += 4) {
-    PF_ISSUE(base + 3, raw[3], xr3)
+    PF_ISSUE(base + 1, raw[1], xr1)
     stage(std::integral_constant<int, 0>{}, base, raw[0]);
     PF_STORE_X(xr1, 1)
     __syncthreads();
-    PF_ISSUE(base + 4, raw[0], xr0)
+    PF_ISSUE(base + 2, raw[0], xr0)
     stage(std::integral_constant<int, 1>{}, base + 1, raw[1]);
-    PF_STORE_X(xr2, 0)
+    PF_STORE_X(xr0, 0)
     __syncthreads();
-    PF_ISSUE(base + 5, raw[1], xr1)
-    stage(std::integral_constant<int, 2>{}, base + 2, raw[2]);
-    PF_STORE_X(xr3, 1)
+    PF_ISSUE(base + 3, raw[1], xr1)
+    stage(std::integral_constant<int, 2>{}, base + 2, raw[0]);
+    PF_STORE_X(xr1, 1)
     __syncthreads();
-    PF_ISSUE(base + 6, raw[2], xr2)
-    stage(std::integral_constant<int, 3>{}, base + 3, raw[3]);
+    PF_ISSUE(base + 4, raw[0], xr0)
+    stage(std::integral_constant<int, 3>{}, base + 3, raw[1]);
+    if (K::MIN) {
+#pragma unroll
+      for (int tt = 0; tt < kWaveTok; tt++) am[tt] = am_next[tt];
+    }
     PF_STORE_X(xr0, 0)
     __syncthreads();
   }
