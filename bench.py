@@ -21,6 +21,10 @@ position per step, then greedy decode of 256 tokens at batch 1 and 4 (and at
 batch 1 over a q8_0 KV cache, `batch_1_q8_cache`), each
 step replayed from one captured HIP graph; tokens/s, ms per step, the eager
 (host-launched) ms per step and the weight-streaming fraction of 8 TB/s.
+
+"prefill" (skipped with --no-prefill): the prefill matmul at a 256-token
+chunk on each matrix of an 8B Q4_K_M layer (TFLOP/s, matrix-core fraction)
+and the matmul-only tokens/s of an 8B prefill.
 """
 
 from __future__ import annotations
@@ -55,6 +59,7 @@ def main():
     ap.add_argument("--prompt", type=int, default=2048)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-batched", action="store_true", help="skip the batch-4/8 matrix-core tile lines")
+    ap.add_argument("--no-prefill", action="store_true", help="skip the 256-token prefill matmul lines")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}).",
@@ -144,9 +149,69 @@ def main():
         line["kinds"] = _kinds(L, h, stream)
     if not args.no_cpu:
         line["cpu_baseline"] = _cpu_baseline(base, kind, rb, x)
+    if not args.no_prefill:
+        line["prefill"] = _prefill(L, h, stream)
     if not args.no_decode:
         line["decode"] = _decode(ctx, args)
     print(json.dumps(line), flush=True)
+
+
+# An 8B Llama layer's matrices at one prompt chunk (gpu.mojo:1695
+# PREFILL_CHUNK = 256 tokens), Q4_K_M kinds: (name, rows, cols, kind, count
+# per layer).  attn_v and ffn_down are Q6_K in half of a Q4_K_M file's layers.
+_PREFILL_SHAPES = [("attn_q", 4096, 4096, 12, 1), ("attn_k", 1024, 4096, 12, 1), ("attn_v", 1024, 4096, 14, 1),
+                   ("attn_output", 4096, 4096, 12, 1), ("ffn_gate", 14336, 4096, 12, 1),
+                   ("ffn_up", 14336, 4096, 12, 1), ("ffn_down", 4096, 14336, 14, 1)]
+
+
+def _prefill(L, h, stream, tokens=256, reps=20):
+    """The prefill matmul (mi_matvec at 256 tokens: prefill.hip) on each of
+    an 8B layer's matrices, timed over `reps` back-to-back calls (activation
+    halves + matrix-core tile + split-K reduce, all inside).  TFLOP/s counts
+    the useful 2 rows cols tokens; the tile issues 2 half-precision MFMA
+    products per useful one (3 for Q6_K), so `mfma_frac` is that work over
+    the 2.5 PFLOP/s dense f16 peak.  `layer_us` sums one layer (attn_v and
+    ffn_down as Q6_K); `matmul_tokens_per_s` = tokens / (32 layers x
+    layer_us): the matmuls of an 8B prefill chunk, attention and the rest of
+    the layer not included."""
+    import torch
+
+    from molla_amd import gpu, synth
+    from molla_amd._lib import check
+
+    ctx = gpu.DeviceContext(0)
+    out, layer_us = {}, 0.0
+    for name, rows, cols, kind, count in _PREFILL_SHAPES:
+        blob = synth.quant_tensor(kind, rows, cols, 31, device="cuda")
+        w = gpu.Tensor.from_bytes(blob, kind, cols, rows)
+        x = synth.normal(tokens * cols, 32, device="cuda")
+        y = torch.empty(tokens * rows, dtype=torch.float32, device="cuda")
+        need = L.mi_matmul_workspace(rows, cols, tokens)
+        work = torch.empty(need + 256, dtype=torch.uint8, device="cuda")
+
+        def call():
+            check(L.mi_matvec(h, kind, w.address, w.row_bytes(), rows, cols, x.data_ptr(), tokens, y.data_ptr(), 0,
+                              None, work.data_ptr(), need))
+        for _ in range(3):
+            call()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            call()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / reps
+        tf = 2.0 * rows * cols * tokens / us / 1e6
+        products = 3 if kind == 14 else 2
+        out[name] = {"rows": rows, "cols": cols, "kind": gpu.KIND_NAMES.get(kind, kind), "us": round(us, 1),
+                     "TFLOP_s": round(tf, 1), "mfma_frac": round(tf * products / 2500.0, 3)}
+        layer_us += us * count
+        del w, blob, work
+    out["tokens"] = tokens
+    out["layer_us"] = round(layer_us, 1)
+    out["matmul_tokens_per_s"] = round(tokens / (32 * layer_us * 1e-6), 0)
+    return out
 
 
 def _batched(L, h, kind, ws, copies, rb, stream, reps=100):

@@ -671,13 +671,14 @@ int launch_kind(hipStream_t s, const void* w, int64_t rb, int rows, int cols, in
 }
 
 // Splits of K (in whole 256-value chunks) for a matmul: enough blocks to put
-// about two waves on every SIMD, each split at least 1024 values long.
+// about two waves on every SIMD (two blocks fit a CU), each split at least
+// one chunk long.
 int choose_splits(int rows, int cols, int tokens) {
   const Prep P = prep_layout(cols, tokens);
   const int64_t blocks = (int64_t)((rows + kBlockRows - 1) / kBlockRows) * (P.ttp / kWaveTok);
   const int chunks = (cols + kChunk - 1) / kChunk;
   int s = 1;
-  while (blocks * s * kWaves < 2048 && (chunks / (2 * s)) >= 4) s *= 2;
+  while (blocks * s * kWaves < 2048 && chunks / (2 * s) >= 1) s *= 2;
   return s;
 }
 

@@ -20,6 +20,8 @@ from ._lib import MiError, MiLayerDesc, MiWeight, check, lib
 
 # ggml type numbers, src/molla/nn/quant.mojo:47-57
 Q_F32, Q_F16, Q_Q4_0, Q_Q4_1, Q_Q5_0, Q_Q5_1, Q_Q8_0, Q_Q4_K, Q_Q5_K, Q_Q6_K = 0, 1, 2, 3, 6, 7, 8, 12, 13, 14
+KIND_NAMES = {0: "F32", 1: "F16", 2: "Q4_0", 3: "Q4_1", 6: "Q5_0", 7: "Q5_1", 8: "Q8_0", 12: "Q4_K", 13: "Q5_K",
+              14: "Q6_K"}
 # epilogues, src/molla/nn/gpu.mojo:781-803
 EPI_NONE, EPI_BIAS, EPI_ADD, EPI_GLU, ACT_BIT = 0, 1, 2, 4, 8
 
