@@ -16,8 +16,9 @@ oracle (a C restatement of molla's serial host matvec, kernel.mojo:316) on the
 same bytes, single thread, over a bounded number of repetitions.
 
 "decode" (skipped with --no-decode) is config 5: a synthetic 8B model (32 Q4_K
-layers, Q6_K head, f32 embedding, random weights), a 2048-token prompt fed one
-position per step, then greedy decode of 256 tokens at batch 1 and 4 (and at
+layers, Q6_K head, f32 embedding, random weights), a 2048-token prompt
+prefilled in 256-token chunks (`prefill_tokens_per_s`), then greedy decode of
+256 tokens at batch 1 and 4 (and at
 batch 1 over a q8_0 KV cache, `batch_1_q8_cache`), each
 step replayed from one captured HIP graph; tokens/s, ms per step, the eager
 (host-launched) ms per step and the weight-streaming fraction of 8 TB/s.
@@ -57,6 +58,7 @@ def main():
     ap.add_argument("--decode-q8", type=int, nargs="*", default=[1],
                     help="decode batch sizes also run over a q8_0 KV cache")
     ap.add_argument("--prompt", type=int, default=2048)
+    ap.add_argument("--prefill-chunk", type=int, default=256, help="prompt tokens per prefill pass (PREFILL_CHUNK)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-batched", action="store_true", help="skip the batch-4/8 matrix-core tile lines")
     ap.add_argument("--no-prefill", action="store_true", help="skip the 256-token prefill matmul lines")
@@ -335,10 +337,12 @@ def _cpu_baseline(w_dev, kind, rb, x_dev):
 
 def _decode(ctx, args):
     """Config 5: synthetic 8B (32 layers, Q4_K, Q6_K head, f32 embedding);
-    a prompt of uniform random ids fed one position per step (prefill as the
-    reference's session does it, engine/session.mojo:119), then greedy decode,
-    at each batch size asked for (independent sequences, one token each per
-    step).  Reported per batch: tokens/s over all sequences and ms per step."""
+    a prompt of uniform random ids prefilled in 256-token chunks through the
+    prefill layer (gpu_block.mojo:1654 forward over a chunk; each sequence of
+    a batch on its own), then greedy decode at each batch size asked for
+    (independent sequences, one token each per step).  Reported per batch:
+    decode tokens/s over all sequences, ms per step, and the prefill's time
+    and prompt tokens/s (HIP events around all of it, head included)."""
     import torch
 
     from molla_amd import block, gpu, synth
@@ -380,20 +384,21 @@ def _decode(ctx, args):
             sess = block.DeviceSession(dctx, model, batch=batch, context=ctxlen, cache_form=form)
             prompt = synth.tokens(args.prompt * batch, vocab, 5 + batch, device=dev).view(args.prompt, batch)
             sess.pos.zero_()
-            t0 = time.perf_counter()
-            # position 0 eagerly (every kernel loaded), the rest of the prompt
-            # through a graph of step + pos += 1 with the ids written before
-            sess.ids.copy_(prompt[0])
-            sess.step()
-            sess.pos.add_(1)
-            gp = sess.capture(advance=False)
-            for p in range(1, args.prompt):
-                sess.ids.copy_(prompt[p])
-                gp.replay()
+            # the prompt in 256-token chunks through the prefill layer, each
+            # sequence on its own (DeviceSession.prefill), then the head over
+            # every sequence's last row; a first small chunk loads the kernels
+            warm = prompt[:16, 0].contiguous()
+            sess.prefill(warm, seq=0, start=0, chunk=16)
             stream.synchronize()
-            prefill_s = time.perf_counter() - t0
             e0 = torch.cuda.Event(enable_timing=True)
             e1 = torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for b in range(batch):
+                sess.prefill(prompt[:, b].contiguous(), seq=b, start=0, chunk=args.prefill_chunk)
+            sess.finish()
+            e1.record(stream)
+            stream.synchronize()
+            prefill_ms = e0.elapsed_time(e1)
             sess.ids.copy_(sess.picks)
             # a few eager steps, for the host-launch cost the graph removes
             e0.record(stream)
@@ -413,8 +418,10 @@ def _decode(ctx, args):
         gbs = wb / (ms_step * 1e-3) / 1e9
         out[f"batch_{batch}" + ("_q8_cache" if form == gpu.CACHE_Q8 else "")] = {"tokens_per_s": round(1000 * batch / ms_step, 2), "ms_per_step": round(ms_step, 3),
                                  "weight_stream_gbs": round(gbs, 1), "frac_of_weight_roofline": round(gbs / PEAK_GBS, 4),
-                                 "eager_ms_per_step": round(eager_ms, 3), "prefill_s": round(prefill_s, 2)}
-        del gp, gd
+                                 "eager_ms_per_step": round(eager_ms, 3),
+                                 "prefill_ms": round(prefill_ms, 2),
+                                 "prefill_tokens_per_s": round(batch * args.prompt / (prefill_ms * 1e-3), 1)}
+        del gd
         del sess
         torch.cuda.empty_cache()
     return out

@@ -185,6 +185,57 @@ class DeviceSession:
                              m.output.cols, xq, self.batch, self.logits.data_ptr(), gpu.EPI_NONE, None))
         check(L.mi_argmax(c.handle, self.logits.data_ptr(), m.vocab, self.batch, self.picks.data_ptr()))
 
+    def prefill(self, ids: torch.Tensor, seq: int = 0, start: int = 0, chunk: int = 256) -> None:
+        """Feed a prompt to sequence `seq` from position `start` in chunks of
+        `chunk` tokens (gpu_block.mojo:1654 forward over a chunk, chunk
+        gpu.mojo:1695 PREFILL_CHUNK): embed the chunk, then every layer over
+        it at once (mi_decoder_layer above 8 tokens runs the prefill matmul;
+        the chunk's tokens are one sequence: cache stride 0 on that
+        sequence's cache).  The prompt's last hidden row lands in x[seq], pos[seq]
+        becomes start + len(ids) and ids[seq] the prompt's last id; finish()
+        then picks every sequence's next token.  ids: device int32.  Queued,
+        not synchronized."""
+        m, s, c = self.model, self.model.spec, self.ctx
+        L = lib()
+        n_all = int(ids.numel())
+        if n_all < 1 or start + n_all > self.context:
+            raise ValueError(f"prompt of {n_all} at {start} does not fit a context of {self.context}")
+        chunk = max(1, min(chunk, n_all))
+        need = max(layer_workspace(l, self.context, chunk) for l in m.layers)
+        if getattr(self, "_pwork", None) is None or self._pwork.numel() < need + 256:
+            self._pwork = torch.empty(need + 256, dtype=torch.uint8, device=c.device)
+            self._px = torch.empty(chunk * s.width, dtype=torch.float32, device=c.device)
+        if self._px.numel() < chunk * s.width:
+            self._px = torch.empty(chunk * s.width, dtype=torch.float32, device=c.device)
+        halves = 2  # the caches are float16 tensors: offsets count halves
+        for c0 in range(0, n_all, chunk):
+            n = min(chunk, n_all - c0)
+            pos = torch.arange(start + c0, start + c0 + n, dtype=torch.int32, device=c.device)
+            check(L.mi_embed(c.handle, m.embedding.data_ptr(), m.embedding.shape[0], s.width,
+                             ids[c0:c0 + n].data_ptr(), n, self._px.data_ptr()))
+            for i in range(len(m.layers)):
+                k = self.k[i].data_ptr() + halves * seq * self.cache_stride
+                v = self.v[i].data_ptr() + halves * seq * self.cache_stride
+                check(L.mi_decoder_layer(c.handle, ctypes.byref(self.descs[i]), self._px.data_ptr(), k, v, 0,
+                                         pos.data_ptr(), self.context, n, self._pwork.data_ptr(),
+                                         self._pwork.numel()))
+        last = (n_all - 1) % chunk  # the last token's row in the last chunk
+        self.x[seq * s.width:(seq + 1) * s.width].copy_(self._px[last * s.width:(last + 1) * s.width])
+        self.pos[seq:seq + 1].fill_(start + n_all)
+        self.ids[seq:seq + 1].copy_(ids[n_all - 1:n_all])
+
+    def finish(self) -> None:
+        """Norm, head and argmax over every sequence's hidden row in x (after
+        prefill) into picks."""
+        m, s, c = self.model, self.model.spec, self.ctx
+        L = lib()
+        xq = self.work.data_ptr()
+        check(L.mi_rms_norm(c.handle, self.x.data_ptr(), m.output_norm.data_ptr(), s.width, self.batch, s.eps,
+                            None, xq))
+        check(L.mi_matvec_xq(c.handle, m.output.kind, m.output.address, m.output.row_bytes(), m.output.rows,
+                             m.output.cols, xq, self.batch, self.logits.data_ptr(), gpu.EPI_NONE, None))
+        check(L.mi_argmax(c.handle, self.logits.data_ptr(), m.vocab, self.batch, self.picks.data_ptr()))
+
     def advance(self) -> None:
         """Greedy decode bookkeeping on the device: next ids = picks, pos += 1."""
         self.ids.copy_(self.picks)

@@ -20,6 +20,9 @@
 //   trig   rope (cos, sin) of this position
 //   xq2    4 * hidden * tokens: the down projection's input, when the gate/up
 //          launch writes it (it cannot share xq, which that launch reads)
+// Above 8 tokens (prefill_layer) the activations stay f32 and the pieces are
+// xn, qkv, attention output, up, act(gate)*up, attention slices and the
+// prefill matmul's own workspace (prefill_carve).
 #include <algorithm>
 
 #include "mi_internal.h"
@@ -58,6 +61,37 @@ Carve carve(const mi_layer_desc* d, int32_t max_count, int32_t tokens) {
   at += up256(sizeof(float) * (size_t)d->rope_dim);
   c.xq2 = at;
   at += up256((size_t)xq_token_bytes(d->hidden) * tokens);
+  c.total = at;
+  return c;
+}
+
+// A prefill chunk (tokens > 8): f32 activations for the prefill matmul.
+struct PrefillCarve {
+  size_t xn, qkv, attn_out, up, h, attn, mm, total;
+};
+
+PrefillCarve prefill_carve(const mi_layer_desc* d, int32_t max_count, int32_t tokens) {
+  const int64_t qw = (int64_t)d->heads * d->head_dim, kvw = (int64_t)d->kv_heads * d->head_dim;
+  PrefillCarve c;
+  size_t at = 0;
+  c.xn = at;
+  at += up256(sizeof(float) * (size_t)d->width * tokens);
+  c.qkv = at;
+  at += up256(sizeof(float) * (size_t)(qw + 2 * kvw) * tokens);
+  c.attn_out = at;
+  at += up256(sizeof(float) * (size_t)qw * tokens);
+  c.up = at;
+  at += up256(sizeof(float) * (size_t)d->hidden * tokens);
+  c.h = at;
+  at += up256(sizeof(float) * (size_t)d->hidden * tokens);
+  c.attn = at;
+  at += up256(attend_workspace(d->heads, d->head_dim, max_count, tokens));
+  c.mm = at;
+  size_t mm = 0;
+  const int32_t shapes[4][2] = {{(int32_t)qw, d->width}, {d->width, (int32_t)qw}, {d->hidden, d->width},
+                                {d->width, d->hidden}};
+  for (auto& sh : shapes) mm = std::max(mm, prefill_workspace(sh[0], sh[1], tokens));
+  at += up256(mm);
   c.total = at;
   return c;
 }
@@ -103,6 +137,55 @@ int check_desc(const mi_layer_desc* d) {
 
 }  // namespace
 
+// The layer over a chunk of more than 8 tokens (a prompt chunk, cache stride
+// or index stride 0, or that many sequences): the same chain on f32
+// activations through the prefill matmul (prefill.hip), the norms writing f32
+// rows, rope and the cache store per token, attention per token over the
+// positions up to its own (the chunk's earlier tokens included).  The gate
+// projection's GLU epilogue reads the up projection's output.
+static int prefill_layer(hipStream_t s, const mi_layer_desc* d, float* resid, uint16_t* k_cache, uint16_t* v_cache,
+                         int64_t cache_stride, const int32_t* kv_index, int64_t index_stride, const int32_t* pos,
+                         int32_t max_count, int32_t tokens, void* work, size_t work_bytes) {
+  const PrefillCarve c = prefill_carve(d, max_count, tokens);
+  if (work_bytes < c.total)
+    return fail(MI_ERR_WORKSPACE, "layer: workspace of %zu bytes (256-aligned), %zu needed", work_bytes, c.total);
+  char* base = (char*)work;
+  float* xn = (float*)(base + c.xn);
+  float* qkv = (float*)(base + c.qkv);
+  float* attn_out = (float*)(base + c.attn_out);
+  float* up = (float*)(base + c.up);
+  float* h = (float*)(base + c.h);
+  void* attn = base + c.attn;
+  void* mm = base + c.mm;
+  const size_t mm_bytes = c.total - c.mm;
+  const int32_t qw = d->heads * d->head_dim, kvw = d->kv_heads * d->head_dim;
+  const int64_t qkv_stride = qw + 2 * (int64_t)kvw;
+  int rc;
+  auto mat = [&](const mi_weight& w, int32_t rows, int32_t cols, const float* x, float* y, int64_t ldy, int32_t epi,
+                 const float* aux) {
+    return matmul_tokens(s, w.kind, w.data, w.row_bytes, rows, cols, x, tokens, y, ldy, epi, aux, mm, mm_bytes);
+  };
+  // attention_layer (block.mojo:319)
+  if ((rc = launch_rms_norm(s, resid, d->attn_norm, d->width, tokens, d->eps, xn, nullptr))) return rc;
+  if ((rc = mat(d->wq, qw, d->width, xn, qkv, qkv_stride, MI_EPI_NONE, nullptr))) return rc;
+  if ((rc = mat(d->wk, kvw, d->width, xn, qkv + qw, qkv_stride, MI_EPI_NONE, nullptr))) return rc;
+  if ((rc = mat(d->wv, kvw, d->width, xn, qkv + qw + kvw, qkv_stride, MI_EPI_NONE, nullptr))) return rc;
+  if ((rc = launch_rope_store(s, qkv, d->heads, d->kv_heads, d->head_dim, d->rope_dim, d->neox, d->rope_steps, pos,
+                              tokens, qkv_stride, k_cache, v_cache, cache_stride, d->rope_factors, d->cache_form,
+                              kv_index, index_stride)))
+    return rc;
+  if ((rc = launch_attend(s, qkv, qkv_stride, k_cache, v_cache, cache_stride, d->heads, d->kv_heads, d->head_dim,
+                          d->attn_scale, pos, -1, max_count, tokens, attn_out, nullptr, attn, d->cache_form,
+                          kv_index, index_stride)))
+    return rc;
+  if ((rc = mat(d->wo, d->width, qw, attn_out, resid, d->width, MI_EPI_ADD, nullptr))) return rc;
+  // mlp_layer (block.mojo:429), gated silu
+  if ((rc = launch_rms_norm(s, resid, d->ffn_norm, d->width, tokens, d->eps, xn, nullptr))) return rc;
+  if ((rc = mat(d->up, d->hidden, d->width, xn, up, d->hidden, MI_EPI_NONE, nullptr))) return rc;
+  if ((rc = mat(d->gate, d->hidden, d->width, xn, h, d->hidden, MI_EPI_GLU, up))) return rc;
+  return mat(d->down, d->width, d->hidden, h, resid, d->width, MI_EPI_ADD, nullptr);
+}
+
 static int decoder_layer(mi_stream stream, const mi_layer_desc* d, float* resid, uint16_t* k_cache,
                          uint16_t* v_cache, int64_t cache_stride, const int32_t* kv_index, int64_t index_stride,
                          const int32_t* pos, int32_t max_count, int32_t tokens, void* work, size_t work_bytes) {
@@ -111,7 +194,7 @@ static int decoder_layer(mi_stream stream, const mi_layer_desc* d, float* resid,
   if (!resid || !k_cache || !v_cache || !pos) return fail(MI_ERR_ARG, "layer: null pointer");
   if (((uintptr_t)k_cache | (uintptr_t)v_cache) & 15 || cache_stride % 8)
     return fail(MI_ERR_ALIGN, "layer: caches must be 16-byte aligned with a stride of a multiple of 8 halves");
-  if (tokens < 1 || tokens > kMaxTokens) return fail(MI_ERR_ARG, "layer: tokens %d outside 1..8", tokens);
+  if (tokens < 1 || tokens > kMaxPrefill) return fail(MI_ERR_ARG, "layer: tokens %d outside 1..%d", tokens, kMaxPrefill);
   if (max_count <= 0) return fail(MI_ERR_SHAPE, "layer: max_count must be positive");
   const int64_t kvw = (int64_t)d->kv_heads * d->head_dim;
   const int64_t crow = cache_row(d->cache_form, (int32_t)kvw);  // halves per position
@@ -124,6 +207,11 @@ static int decoder_layer(mi_stream stream, const mi_layer_desc* d, float* resid,
   if (kv_index && tokens > 1 && index_stride != 0 && index_stride < max_count)
     return fail(MI_ERR_SHAPE, "layer: index stride %lld holds fewer than %d positions", (long long)index_stride,
                 max_count);
+  if (tokens > kMaxTokens) {
+    if (!work || ((uintptr_t)work & 255)) return fail(MI_ERR_ALIGN, "layer: workspace must be 256-byte aligned");
+    return prefill_layer((hipStream_t)stream, d, resid, k_cache, v_cache, cache_stride, kv_index, index_stride, pos,
+                         max_count, tokens, work, work_bytes);
+  }
   const Carve c = carve(d, max_count, tokens);
   if (!work || ((uintptr_t)work & 255) || work_bytes < c.total)
     return fail(MI_ERR_WORKSPACE, "layer: workspace of %zu bytes (256-aligned), %zu needed", work_bytes, c.total);
@@ -263,7 +351,8 @@ static int decoder_layer(mi_stream stream, const mi_layer_desc* d, float* resid,
 extern "C" {
 
 size_t mi_layer_workspace(const mi_layer_desc* desc, int32_t max_count, int32_t tokens) {
-  if (!desc || max_count <= 0 || tokens <= 0) return 0;
+  if (!desc || max_count <= 0 || tokens <= 0 || tokens > kMaxPrefill) return 0;
+  if (tokens > kMaxTokens) return prefill_carve(desc, max_count, tokens).total;
   return carve(desc, max_count, tokens).total;
 }
 

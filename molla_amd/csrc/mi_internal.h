@@ -109,6 +109,11 @@ size_t prefill_workspace(int32_t rows, int32_t cols, int32_t tokens);
 int launch_prefill(hipStream_t s, int kind, const void* w, int64_t row_bytes, int32_t rows, int32_t cols,
                    const float* x, int32_t tokens, float* y, int64_t ldy, int32_t epi, const float* aux, void* work,
                    size_t work_bytes);
+// shim.cpp: the prefill tile where it fits, else the decode kernels eight
+// tokens at a time; y[t * ldy + r]; work as launch_prefill.
+int matmul_tokens(hipStream_t s, int kind, const void* w, int64_t row_bytes, int32_t rows, int32_t cols,
+                  const float* x, int32_t tokens, float* y, int64_t ldy, int32_t epi, const float* aux, void* work,
+                  size_t work_bytes);
 // Every kind and batch: routes to the kernels above or the general
 // matvec_kernel.h.
 int launch_matvec(hipStream_t s, int kind, const void* w, int64_t row_bytes, int32_t rows,

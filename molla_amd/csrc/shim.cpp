@@ -55,6 +55,27 @@ int check_weight(const char* name, int kind, const void* w, int64_t row_bytes, i
   return MI_OK;
 }
 
+// Tokens above the decode batch: the prefill tile where it fits, else the
+// decode kernels over runs of eight tokens (the GLU aux and the output move
+// with the run; a bias does not).  The caller has checked the weight, epi and
+// aux; work holds prefill_prep_bytes(cols, tokens) at least.
+int matmul_tokens(hipStream_t s, int kind, const void* w, int64_t row_bytes, int32_t rows, int32_t cols,
+                  const float* x, int32_t tokens, float* y, int64_t ldy, int32_t epi, const float* aux, void* work,
+                  size_t work_bytes) {
+  if (prefill_fits(kind, cols, row_bytes, w))
+    return launch_prefill(s, kind, w, row_bytes, rows, cols, x, tokens, y, ldy, epi, aux, work, work_bytes);
+  for (int32_t t0 = 0; t0 < tokens; t0 += kMaxTokens) {
+    const int32_t n = tokens - t0 < kMaxTokens ? tokens - t0 : kMaxTokens;
+    int rc = launch_quantize(s, x + (int64_t)t0 * cols, cols, n, work);
+    if (!rc) {
+      const float* a = (epi & MI_EPI_GLU) ? aux + (int64_t)t0 * ldy : aux;
+      rc = launch_matvec(s, kind, w, row_bytes, rows, cols, work, n, y + (int64_t)t0 * ldy, ldy, epi, a);
+    }
+    if (rc) return rc;
+  }
+  return MI_OK;
+}
+
 }  // namespace mi
 
 using namespace mi;
@@ -149,9 +170,6 @@ int mi_matvec_xq(mi_stream stream, int kind, const void* w, int64_t row_bytes, i
   return launch_matvec((hipStream_t)stream, kind, w, row_bytes, rows, cols, xq, tokens, y, rows, epi, aux);
 }
 
-// Tokens above the decode batch: the prefill tile where it fits, else the
-// decode kernels over runs of eight tokens (the GLU aux and the output move
-// with the run; a bias does not).
 static int matmul_many(mi_stream stream, int kind, const void* w, int64_t row_bytes, int32_t rows, int32_t cols,
                        const float* x, int32_t tokens, float* y, int32_t epi, const float* aux, void* work,
                        size_t work_bytes) {
@@ -160,19 +178,8 @@ static int matmul_many(mi_stream stream, int kind, const void* w, int64_t row_by
   if (work_bytes < mi_matvec_workspace(cols, tokens))
     return fail(MI_ERR_WORKSPACE, "matvec: workspace of %zu bytes, %zu needed", work_bytes,
                 mi_matvec_workspace(cols, tokens));
-  hipStream_t s = (hipStream_t)stream;
-  if (prefill_fits(kind, cols, row_bytes, w))
-    return launch_prefill(s, kind, w, row_bytes, rows, cols, x, tokens, y, rows, epi, aux, work, work_bytes);
-  for (int32_t t0 = 0; t0 < tokens; t0 += kMaxTokens) {
-    const int32_t n = tokens - t0 < kMaxTokens ? tokens - t0 : kMaxTokens;
-    int rc = launch_quantize(s, x + (int64_t)t0 * cols, cols, n, work);
-    if (!rc) {
-      const float* a = (epi & MI_EPI_GLU) ? aux + (int64_t)t0 * rows : aux;
-      rc = launch_matvec(s, kind, w, row_bytes, rows, cols, work, n, y + (int64_t)t0 * rows, rows, epi, a);
-    }
-    if (rc) return rc;
-  }
-  return MI_OK;
+  return matmul_tokens((hipStream_t)stream, kind, w, row_bytes, rows, cols, x, tokens, y, rows, epi, aux, work,
+                       work_bytes);
 }
 
 int mi_matvec(mi_stream stream, int kind, const void* w, int64_t row_bytes, int32_t rows, int32_t cols,

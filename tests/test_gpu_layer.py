@@ -148,6 +148,64 @@ def test_small_model_greedy_decode_matches_oracle():
         sess.advance()
 
 
+def test_session_prefill_matches_oracle():
+    """A prompt fed in chunks (DeviceSession.prefill: 16-token chunks through
+    the prefill layer, two sequences of different prompts) leaves the model
+    where the oracle's token-by-token forward leaves it: the next-token logits
+    within 2e-3 of the peak with the same pick, and greedy decode continuing
+    from there picking what the oracle picks (tests/test_gpu_block.mojo:1407
+    gate)."""
+    from molla_amd import block, gpu
+    ctx = gpu.DeviceContext(0)
+    spec = spec_of(256, 512, 4, 2, 64, base=10000.0)
+    vocab, n_layers, plen, gen = 1000, 2, 40, 4
+    hosts = [make_layer_weights(spec, 60 + i) for i in range(n_layers)]
+    emb = synth.normal(vocab * spec["width"], 70).numpy().reshape(vocab, spec["width"])
+    onorm = synth.normal(spec["width"], 71, mean=1.0, std=0.1).numpy()
+    head = synth.quant_tensor(oracle.Q6_K, vocab, spec["width"], 72).numpy()
+    layers = [device_layer_from(h, spec)[1] for h in hosts]
+    bs = layers[0].spec
+    model = block.DeviceModel(bs, torch.from_numpy(emb).cuda(), layers, torch.from_numpy(onorm).cuda(),
+                              gpu.Tensor.from_bytes(torch.from_numpy(head), oracle.Q6_K, spec["width"], vocab))
+    batch, context = 2, plen + gen + 1
+    sess = block.DeviceSession(ctx, model, batch=batch, context=context)
+    rng = np.random.default_rng(73)
+    prompts = rng.integers(0, vocab, size=(batch, plen)).astype(np.int32)
+    for b in range(batch):
+        sess.prefill(torch.from_numpy(prompts[b]).cuda(), seq=b, start=0, chunk=16)
+    sess.finish()
+    ctx.synchronize()
+    keep = []
+    ol = [oracle.make_layer(spec, h, keep) for h in hosts]
+    kvw = bs.kv_width()
+    hd = (oracle.Q6_K, vocab, spec["width"], head)
+    for b in range(batch):
+        ok = [np.zeros(context * kvw, np.float32) for _ in range(n_layers)]
+        ov = [np.zeros(context * kvw, np.float32) for _ in range(n_layers)]
+        for p in range(plen):
+            want = oracle.forward(ol, emb, onorm, hd, int(prompts[b, p]), p, p, ok, ov, f16_store=True)
+        got = sess.logits.cpu().numpy().reshape(batch, vocab)[b]
+        assert np.abs(got - want).max() <= 2e-3 * np.abs(want).max(), b
+        assert int(sess.picks.cpu().numpy()[b]) == oracle.argmax(want), b
+    # decode on from the prefilled caches: the first sequence against the oracle
+    ok = [np.zeros(context * kvw, np.float32) for _ in range(n_layers)]
+    ov = [np.zeros(context * kvw, np.float32) for _ in range(n_layers)]
+    for p in range(plen):
+        want = oracle.forward(ol, emb, onorm, hd, int(prompts[0, p]), p, p, ok, ov, f16_store=True)
+    token = oracle.argmax(want)
+    sess.ids.copy_(sess.picks)
+    for p in range(plen, plen + gen):
+        sess.step()
+        ctx.synchronize()
+        want = oracle.forward(ol, emb, onorm, hd, token, p, p, ok, ov, f16_store=True)
+        got = sess.logits.cpu().numpy().reshape(batch, vocab)[0]
+        assert np.abs(got - want).max() <= 2e-3 * np.abs(want).max(), p
+        pick = int(sess.picks.cpu().numpy()[0])
+        assert pick == oracle.argmax(want), p
+        token = pick
+        sess.advance()
+
+
 def test_graph_replay_matches_eager():
     """The decode step captured as a HIP graph (DeviceSession.capture) gives
     the eager step's logits and picks bit for bit, on every replay, with
@@ -351,13 +409,15 @@ def test_layer_paged_skips_positions_it_does_not_hold():
     assert np.abs(got - xr).max() <= 1e-4 * np.abs(xr).max()
 
 
-@pytest.mark.parametrize("paged", [False, True])
-def test_layer_chunk_of_one_sequence(paged):
+@pytest.mark.parametrize("paged,tokens", [(False, 4), (True, 4), (False, 40), (True, 40), (False, 256)])
+def test_layer_chunk_of_one_sequence(paged, tokens):
     """Stride 0: the tokens are one sequence's chunk at consecutive positions
     (gpu.mojo:617 `bases` all zero).  Each token attends over the positions up
     to its own, the chunk's earlier tokens included; the oracle runs them one
     at a time over the same cache (fed the rows the device stored for the
-    chunk's earlier tokens)."""
+    chunk's earlier tokens).  Above 8 tokens the layer runs the prefill path
+    (f32 activations through the prefill matmul, gpu_block.mojo:1654
+    forward over a chunk)."""
     from molla_amd import block, gpu
     ctx = gpu.DeviceContext(0)
     spec = spec_of(512, 1024, 8, 2, 64)
@@ -365,7 +425,7 @@ def test_layer_chunk_of_one_sequence(paged):
     host["rope_factors"] = llama31_factors(spec["rope_dim"] // 2)
     bs, layer = device_layer_from(host, spec)
     kvw = bs.kv_width()
-    tokens, first = 4, 200
+    first = 200
     count = first + tokens
     keys16 = synth.normal(count * kvw, 80).half().numpy().reshape(count, kvw)
     vals16 = synth.normal(count * kvw, 81).half().numpy().reshape(count, kvw)
