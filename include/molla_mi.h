@@ -215,7 +215,11 @@ typedef struct {
 } mi_layer_desc;
 
 /* One Llama layer for `tokens` independent sequences (batch decode, one token
- * each), in place on resid[t*width ...].  Sequence t owns k_cache/v_cache at
+ * each), in place on resid[t*width ...].  Above 8 tokens (up to 65536; a
+ * prompt chunk when cache_stride is 0, gpu_block.mojo:1654 forward over a
+ * chunk) the same layer runs on f32 activations through the prefill matmul
+ * (see mi_matvec) with rope, the cache store and attention per token;
+ * mi_layer_workspace(desc, max_count, tokens) sizes it for that count.  Sequence t owns k_cache/v_cache at
  * t * cache_stride halves, laid out [slot][kv_heads*head_dim].  Its token sits
  * at position pos[t] (device int32[tokens], read by the kernels so a captured
  * graph can be replayed for the next token), which is also its cache slot (a
