@@ -88,8 +88,8 @@ PrefillCarve prefill_carve(const mi_layer_desc* d, int32_t max_count, int32_t to
   at += up256(attend_workspace(d->heads, d->head_dim, max_count, tokens));
   c.mm = at;
   size_t mm = 0;
-  const int32_t shapes[4][2] = {{(int32_t)qw, d->width}, {d->width, (int32_t)qw}, {d->hidden, d->width},
-                                {d->width, d->hidden}};
+  const int32_t shapes[5][2] = {{(int32_t)(qw + 2 * kvw), d->width}, {(int32_t)qw, d->width},
+                                {d->width, (int32_t)qw}, {d->hidden, d->width}, {d->width, d->hidden}};
   for (auto& sh : shapes) mm = std::max(mm, prefill_workspace(sh[0], sh[1], tokens));
   at += up256(mm);
   c.total = at;
@@ -166,10 +166,28 @@ static int prefill_layer(hipStream_t s, const mi_layer_desc* d, float* resid, ui
     return matmul_tokens(s, w.kind, w.data, w.row_bytes, rows, cols, x, tokens, y, ldy, epi, aux, mm, mm_bytes);
   };
   // attention_layer (block.mojo:319)
+  auto tile = [&](const mi_weight& w) { return prefill_fits(w.kind, w.cols, w.row_bytes, w.data); };
   if ((rc = launch_rms_norm(s, resid, d->attn_norm, d->width, tokens, d->eps, xn, nullptr))) return rc;
-  if ((rc = mat(d->wq, qw, d->width, xn, qkv, qkv_stride, MI_EPI_NONE, nullptr))) return rc;
-  if ((rc = mat(d->wk, kvw, d->width, xn, qkv + qw, qkv_stride, MI_EPI_NONE, nullptr))) return rc;
-  if ((rc = mat(d->wv, kvw, d->width, xn, qkv + qw + kvw, qkv_stride, MI_EPI_NONE, nullptr))) return rc;
+  if (d->wq.kind == d->wk.kind && d->wq.kind == d->wv.kind && tile(d->wq) && tile(d->wk) && tile(d->wv)) {
+    // q|k|v as one launch over their rows end to end, on one activation prep
+    RowSegs sg{};
+    const mi_weight* ws[3] = {&d->wq, &d->wk, &d->wv};
+    const int32_t ends[3] = {qw, qw + kvw, qw + 2 * kvw};
+    for (int i = 0; i < 3; i++) {
+      sg.w[i] = (const uint8_t*)ws[i]->data;
+      sg.rb[i] = ws[i]->row_bytes;
+      sg.end[i] = ends[i];
+    }
+    sg.nseg = 3;
+    if ((rc = prefill_prepare(s, xn, d->width, tokens, mm))) return rc;
+    if ((rc = launch_prefill_segs(s, d->wq.kind, sg, d->width, tokens, qkv, qkv_stride, MI_EPI_NONE, nullptr, mm,
+                                  mm_bytes)))
+      return rc;
+  } else {
+    if ((rc = mat(d->wq, qw, d->width, xn, qkv, qkv_stride, MI_EPI_NONE, nullptr))) return rc;
+    if ((rc = mat(d->wk, kvw, d->width, xn, qkv + qw, qkv_stride, MI_EPI_NONE, nullptr))) return rc;
+    if ((rc = mat(d->wv, kvw, d->width, xn, qkv + qw + kvw, qkv_stride, MI_EPI_NONE, nullptr))) return rc;
+  }
   if ((rc = launch_rope_store(s, qkv, d->heads, d->kv_heads, d->head_dim, d->rope_dim, d->neox, d->rope_steps, pos,
                               tokens, qkv_stride, k_cache, v_cache, cache_stride, d->rope_factors, d->cache_form,
                               kv_index, index_stride)))
@@ -181,8 +199,18 @@ static int prefill_layer(hipStream_t s, const mi_layer_desc* d, float* resid, ui
   if ((rc = mat(d->wo, d->width, qw, attn_out, resid, d->width, MI_EPI_ADD, nullptr))) return rc;
   // mlp_layer (block.mojo:429), gated silu
   if ((rc = launch_rms_norm(s, resid, d->ffn_norm, d->width, tokens, d->eps, xn, nullptr))) return rc;
-  if ((rc = mat(d->up, d->hidden, d->width, xn, up, d->hidden, MI_EPI_NONE, nullptr))) return rc;
-  if ((rc = mat(d->gate, d->hidden, d->width, xn, h, d->hidden, MI_EPI_GLU, up))) return rc;
+  if (tile(d->up) && tile(d->gate)) {  // one activation prep for both
+    if ((rc = prefill_prepare(s, xn, d->width, tokens, mm))) return rc;
+    if ((rc = launch_prefill_segs(s, d->up.kind, rows::one_matrix(d->up.data, d->up.row_bytes, d->hidden),
+                                  d->width, tokens, up, d->hidden, MI_EPI_NONE, nullptr, mm, mm_bytes)))
+      return rc;
+    if ((rc = launch_prefill_segs(s, d->gate.kind, rows::one_matrix(d->gate.data, d->gate.row_bytes, d->hidden),
+                                  d->width, tokens, h, d->hidden, MI_EPI_GLU, up, mm, mm_bytes)))
+      return rc;
+  } else {
+    if ((rc = mat(d->up, d->hidden, d->width, xn, up, d->hidden, MI_EPI_NONE, nullptr))) return rc;
+    if ((rc = mat(d->gate, d->hidden, d->width, xn, h, d->hidden, MI_EPI_GLU, up))) return rc;
+  }
   return mat(d->down, d->width, d->hidden, h, resid, d->width, MI_EPI_ADD, nullptr);
 }
 

@@ -109,6 +109,14 @@ size_t prefill_workspace(int32_t rows, int32_t cols, int32_t tokens);
 int launch_prefill(hipStream_t s, int kind, const void* w, int64_t row_bytes, int32_t rows, int32_t cols,
                    const float* x, int32_t tokens, float* y, int64_t ldy, int32_t epi, const float* aux, void* work,
                    size_t work_bytes);
+// The two halves of launch_prefill, for several matrices over one input
+// (q|k|v, gate and up): prefill_prepare writes the activation halves into
+// work, launch_prefill_segs runs rows of up to three matrices of one kind
+// (RowSegs, matvec_rows.h) against them.
+struct RowSegs;
+int prefill_prepare(hipStream_t s, const float* x, int32_t cols, int32_t tokens, void* work);
+int launch_prefill_segs(hipStream_t s, int kind, const RowSegs& sg, int32_t cols, int32_t tokens, float* y,
+                        int64_t ldy, int32_t epi, const float* aux, void* work, size_t work_bytes);
 // shim.cpp: the prefill tile where it fits, else the decode kernels eight
 // tokens at a time; y[t * ldy + r]; work as launch_prefill.
 int matmul_tokens(hipStream_t s, int kind, const void* w, int64_t row_bytes, int32_t rows, int32_t cols,

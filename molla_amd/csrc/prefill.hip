@@ -44,7 +44,7 @@
 // gpu.mojo:1005 and :2955-2961.
 #include <type_traits>
 
-#include "matvec_units.h"
+#include "matvec_rows.h"
 
 namespace mi {
 namespace {
@@ -429,7 +429,7 @@ __global__ __launch_bounds__(256) void prefill_x_kernel(const float* __restrict_
 
 // ---- the matmul ------------------------------------------------------------
 template <int KIND, int W>
-__global__ __launch_bounds__(W * 64, KIND == MI_Q6_K ? 2 : 1) void prefill_kernel(const uint8_t* __restrict__ w, int64_t rb, int rows,
+__global__ __launch_bounds__(W * 64, KIND == MI_Q6_K ? 2 : 1) void prefill_kernel(const RowSegs sg,
                                                          int cols, int tokens, const uint8_t* __restrict__ work,
                                                          int stages_per_split, float* __restrict__ y, int64_t ldy,
                                                          int epi, const float* __restrict__ aux,
@@ -443,10 +443,11 @@ __global__ __launch_bounds__(W * 64, KIND == MI_Q6_K ? 2 : 1) void prefill_kerne
   const int nst = cols / kStage;
   const int st0 = blockIdx.z * stages_per_split;
   const int st1 = min(st0 + stages_per_split, nst);
+  const int rows = sg.end[sg.nseg - 1];
   const int row_base = (blockIdx.x * W + wave) * (kWaveRows * 32);
   const uint8_t* wrow[kWaveRows];
 #pragma unroll
-  for (int rt = 0; rt < kWaveRows; rt++) wrow[rt] = w + (int64_t)min(row_base + rt * 32 + n, rows - 1) * rb;
+  for (int rt = 0; rt < kWaveRows; rt++) wrow[rt] = rows::seg_row(sg, min(row_base + rt * 32 + n, rows - 1));
 
   // activation stage copy: 16 KB, four 16-byte pieces a thread
   const uint8_t* xp = work + P.xp;
@@ -661,12 +662,13 @@ constexpr int kWaves = 4;
 constexpr int kBlockRows = kWaves * kWaveRows * 32;
 
 template <int KIND>
-int launch_kind(hipStream_t s, const void* w, int64_t rb, int rows, int cols, int tokens, const void* work,
-                int splits, int sps, float* y, int64_t ldy, int epi, const float* aux, float* part) {
+int launch_kind(hipStream_t s, const RowSegs& sg, int cols, int tokens, const void* work, int splits, int sps,
+                float* y, int64_t ldy, int epi, const float* aux, float* part) {
   const Prep P = prep_layout(cols, tokens);
+  const int rows = sg.end[sg.nseg - 1];
   dim3 grid((rows + kBlockRows - 1) / kBlockRows, P.ttp / kWaveTok, splits);
-  hipLaunchKernelGGL((prefill_kernel<KIND, kWaves>), grid, dim3(kWaves * 64), 0, s, (const uint8_t*)w, rb, rows,
-                     cols, tokens, (const uint8_t*)work, sps, y, ldy, epi, aux, splits > 1 ? part : nullptr);
+  hipLaunchKernelGGL((prefill_kernel<KIND, kWaves>), grid, dim3(kWaves * 64), 0, s, sg, cols, tokens,
+                     (const uint8_t*)work, sps, y, ldy, epi, aux, splits > 1 ? part : nullptr);
   return hip_check(hipGetLastError(), "prefill launch");
 }
 
@@ -713,15 +715,18 @@ size_t prefill_workspace(int32_t rows, int32_t cols, int32_t tokens) {
 
 size_t prefill_prep_bytes(int32_t cols, int32_t tokens) { return prep_layout(cols, tokens).total; }
 
-int launch_prefill(hipStream_t s, int kind, const void* w, int64_t row_bytes, int32_t rows, int32_t cols,
-                   const float* x, int32_t tokens, float* y, int64_t ldy, int32_t epi, const float* aux, void* work,
-                   size_t work_bytes) {
+int prefill_prepare(hipStream_t s, const float* x, int32_t cols, int32_t tokens, void* work) {
   const Prep P = prep_layout(cols, tokens);
   hipLaunchKernelGGL(prefill_scale_kernel, dim3(P.ttp * kTileTok), dim3(256), 0, s, x, cols, tokens,
                      (uint8_t*)work);
   hipLaunchKernelGGL(prefill_x_kernel, dim3(P.nch, P.ttp), dim3(256), 0, s, x, cols, tokens, (uint8_t*)work);
-  int rc = hip_check(hipGetLastError(), "prefill activation launch");
-  if (rc) return rc;
+  return hip_check(hipGetLastError(), "prefill activation launch");
+}
+
+int launch_prefill_segs(hipStream_t s, int kind, const RowSegs& sg, int32_t cols, int32_t tokens, float* y,
+                        int64_t ldy, int32_t epi, const float* aux, void* work, size_t work_bytes) {
+  const Prep P = prep_layout(cols, tokens);
+  const int rows = sg.end[sg.nseg - 1];
   int splits = choose_splits(rows, cols, tokens);
   const size_t need = (size_t)splits * tokens * rows * 4;
   if (splits > 1 && work_bytes < P.total + need) splits = 1;  // no room for partial sums
@@ -730,15 +735,16 @@ int launch_prefill(hipStream_t s, int kind, const void* w, int64_t row_bytes, in
   sps = (sps + 3) & ~3;  // whole 256-value chunks
   splits = (nst + sps - 1) / sps;
   float* part = (float*)((uint8_t*)work + P.total);
+  int rc;
   switch (kind) {
-    case MI_Q4_K: rc = launch_kind<MI_Q4_K>(s, w, row_bytes, rows, cols, tokens, work, splits, sps, y, ldy, epi, aux, part); break;
-    case MI_Q5_K: rc = launch_kind<MI_Q5_K>(s, w, row_bytes, rows, cols, tokens, work, splits, sps, y, ldy, epi, aux, part); break;
-    case MI_Q6_K: rc = launch_kind<MI_Q6_K>(s, w, row_bytes, rows, cols, tokens, work, splits, sps, y, ldy, epi, aux, part); break;
-    case MI_Q8_0: rc = launch_kind<MI_Q8_0>(s, w, row_bytes, rows, cols, tokens, work, splits, sps, y, ldy, epi, aux, part); break;
-    case MI_Q4_0: rc = launch_kind<MI_Q4_0>(s, w, row_bytes, rows, cols, tokens, work, splits, sps, y, ldy, epi, aux, part); break;
-    case MI_Q4_1: rc = launch_kind<MI_Q4_1>(s, w, row_bytes, rows, cols, tokens, work, splits, sps, y, ldy, epi, aux, part); break;
-    case MI_Q5_0: rc = launch_kind<MI_Q5_0>(s, w, row_bytes, rows, cols, tokens, work, splits, sps, y, ldy, epi, aux, part); break;
-    case MI_Q5_1: rc = launch_kind<MI_Q5_1>(s, w, row_bytes, rows, cols, tokens, work, splits, sps, y, ldy, epi, aux, part); break;
+    case MI_Q4_K: rc = launch_kind<MI_Q4_K>(s, sg, cols, tokens, work, splits, sps, y, ldy, epi, aux, part); break;
+    case MI_Q5_K: rc = launch_kind<MI_Q5_K>(s, sg, cols, tokens, work, splits, sps, y, ldy, epi, aux, part); break;
+    case MI_Q6_K: rc = launch_kind<MI_Q6_K>(s, sg, cols, tokens, work, splits, sps, y, ldy, epi, aux, part); break;
+    case MI_Q8_0: rc = launch_kind<MI_Q8_0>(s, sg, cols, tokens, work, splits, sps, y, ldy, epi, aux, part); break;
+    case MI_Q4_0: rc = launch_kind<MI_Q4_0>(s, sg, cols, tokens, work, splits, sps, y, ldy, epi, aux, part); break;
+    case MI_Q4_1: rc = launch_kind<MI_Q4_1>(s, sg, cols, tokens, work, splits, sps, y, ldy, epi, aux, part); break;
+    case MI_Q5_0: rc = launch_kind<MI_Q5_0>(s, sg, cols, tokens, work, splits, sps, y, ldy, epi, aux, part); break;
+    case MI_Q5_1: rc = launch_kind<MI_Q5_1>(s, sg, cols, tokens, work, splits, sps, y, ldy, epi, aux, part); break;
     default: return fail(MI_ERR_KIND, "prefill: ggml type %d has no tile", kind);
   }
   if (rc || splits == 1) return rc;
@@ -746,6 +752,15 @@ int launch_prefill(hipStream_t s, int kind, const void* w, int64_t row_bytes, in
   hipLaunchKernelGGL(prefill_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, part, splits, rows,
                      tokens, y, ldy, epi, aux);
   return hip_check(hipGetLastError(), "prefill reduce launch");
+}
+
+int launch_prefill(hipStream_t s, int kind, const void* w, int64_t row_bytes, int32_t rows, int32_t cols,
+                   const float* x, int32_t tokens, float* y, int64_t ldy, int32_t epi, const float* aux, void* work,
+                   size_t work_bytes) {
+  int rc = prefill_prepare(s, x, cols, tokens, work);
+  if (rc) return rc;
+  return launch_prefill_segs(s, kind, rows::one_matrix(w, row_bytes, rows), cols, tokens, y, ldy, epi, aux, work,
+                             work_bytes);
 }
 
 }  // namespace mi
