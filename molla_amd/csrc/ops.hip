@@ -276,20 +276,27 @@ __device__ __forceinline__ int kv_cell(const int32_t* __restrict__ kv_index, int
   return kv_index ? kv_index[t * index_stride + j] : j;
 }
 
+// tq > 1 (one sequence's chunk only: its tokens share the cache): the block
+// stages the slice once and scores tq consecutive tokens against it, each
+// with its own count, so a prefill chunk reads every slice once per tq
+// tokens instead of once per token.
 template <int GROUP>
 __global__ __launch_bounds__(kAttnThreads) void attend_split_kernel(
     const float* __restrict__ q, int64_t q_stride, const __half* __restrict__ kc,
     const __half* __restrict__ vc, int64_t cache_stride, int heads, int kv_heads, int head_dim,
     float scale, const int32_t* __restrict__ pos_dev, int count_host, int max_chunks,
     float* __restrict__ part_acc, float* __restrict__ part_ml, const int32_t* __restrict__ kv_index,
-    int64_t index_stride) {
-  const int c = blockIdx.x, kvh = blockIdx.y, t = blockIdx.z;
-  const int count = pos_dev ? pos_dev[t] + 1 : count_host;  // a position p attends over p + 1 slots
+    int64_t index_stride, int tokens, int tq) {
+  const int c = blockIdx.x, kvh = blockIdx.y;
+  const int t0 = blockIdx.z * tq, t1 = min(t0 + tq, tokens);
+  // a position p attends over p + 1 slots; the block stages for its widest
+  int count_max = 0;
+  for (int t = t0; t < t1; t++) count_max = max(count_max, pos_dev ? pos_dev[t] + 1 : count_host);
   const int kk = attn_slice(head_dim);
   const int start = c * kk;
-  if (start >= count) return;
+  if (start >= count_max) return;
   const int D = head_dim, KS = head_dim + 8;  // LDS key rows padded by 16 bytes
-  const int nk = min(kk, count - start);
+  const int nk_max = min(kk, count_max - start);
   const int kvw = kv_heads * D;
   extern __shared__ uint4 lds4[];
   __half* Ks = (__half*)lds4;
@@ -300,7 +307,7 @@ __global__ __launch_bounds__(kAttnThreads) void attend_split_kernel(
 
   // stage keys, values (16-byte pieces; keys past the end repeat the last
   // live one and are masked below) and the group's queries
-  const int64_t seq = kv_index ? 0 : (int64_t)t * cache_stride;
+  const int64_t seq = kv_index ? 0 : (int64_t)t0 * cache_stride;
   const __half* kbase = kc + seq + (int64_t)kvh * D;
   const __half* vbase = vc + seq + (int64_t)kvh * D;
   // Every load of a batch is issued before any LDS store, with clamped
@@ -309,16 +316,16 @@ __global__ __launch_bounds__(kAttnThreads) void attend_split_kernel(
   const int pieces = D >> 3;
   const int total = kk * pieces;
   constexpr int kBatch = 4;
-  const float4* q4 = (const float4*)(q + (int64_t)t * q_stride + (int64_t)kvh * GROUP * D);
   const int nq4 = GROUP * D / 4;
-  const float4 qv = q4[min(tid, nq4 - 1)];
+  auto q4_of = [&](int t) { return (const float4*)(q + (int64_t)t * q_stride + (int64_t)kvh * GROUP * D); };
+  const float4 qv = q4_of(t0)[min(tid, nq4 - 1)];
   for (int b0 = 0; b0 < total; b0 += kAttnThreads * kBatch) {
     uint4 kv[kBatch], vv[kBatch];
 #pragma unroll
     for (int j = 0; j < kBatch; j++) {
       const int i = min(b0 + tid + j * kAttnThreads, total - 1);
-      const int key = min(i / pieces, nk - 1), pc = i % pieces;
-      const int cell = max(kv_cell(kv_index, index_stride, t, start + key), 0);
+      const int key = min(i / pieces, nk_max - 1), pc = i % pieces;
+      const int cell = max(kv_cell(kv_index, index_stride, t0, start + key), 0);
       const int64_t off = (int64_t)cell * kvw + pc * 8;
       kv[j] = *(const uint4*)(kbase + off);
       vv[j] = *(const uint4*)(vbase + off);
@@ -333,73 +340,289 @@ __global__ __launch_bounds__(kAttnThreads) void attend_split_kernel(
       }
     }
   }
-  if (tid < nq4) ((float4*)Qs)[tid] = qv;
-  for (int i = tid + kAttnThreads; i < nq4; i += kAttnThreads) ((float4*)Qs)[i] = q4[i];
-  __syncthreads();
+  const int halfD = D >> 1;
+  for (int t = t0; t < t1; t++) {
+    const int count = pos_dev ? pos_dev[t] + 1 : count_host;
+    if (start >= count) continue;  // uniform over the block: no keys of this slice for t
+    const int nk = min(kk, count - start);
+    if (t == t0) {
+      if (tid < nq4) ((float4*)Qs)[tid] = qv;
+      for (int i = tid + kAttnThreads; i < nq4; i += kAttnThreads) ((float4*)Qs)[i] = q4_of(t)[i];
+    } else {
+      for (int i = tid; i < nq4; i += kAttnThreads) ((float4*)Qs)[i] = q4_of(t)[i];
+    }
+    __syncthreads();
 
-  const int64_t slot_base = ((int64_t)t * heads + (int64_t)kvh * GROUP) * max_chunks + c;
-  // scores and slice softmax: wave w takes query heads w, w+4, ...; lane = key
-  for (int g = wave; g < GROUP; g += kAttnThreads / kWave) {
-    float sdot = 0.0f;
-    if (lane < kk) {
-      const __half* kr = Ks + lane * KS;
-      const float* qg = Qs + g * D;
-      for (int d = 0; d < D; d += 8) {
-        const uint4 raw = *(const uint4*)(kr + d);
-        const __half2* h2 = (const __half2*)&raw;
-        const float4 qa = *(const float4*)(qg + d), qb = *(const float4*)(qg + d + 4);
-        const float2 k0 = __half22float2(h2[0]), k1 = __half22float2(h2[1]);
-        const float2 k2 = __half22float2(h2[2]), k3 = __half22float2(h2[3]);
-        sdot = fmaf(qa.x, k0.x, sdot);
-        sdot = fmaf(qa.y, k0.y, sdot);
-        sdot = fmaf(qa.z, k1.x, sdot);
-        sdot = fmaf(qa.w, k1.y, sdot);
-        sdot = fmaf(qb.x, k2.x, sdot);
-        sdot = fmaf(qb.y, k2.y, sdot);
-        sdot = fmaf(qb.z, k3.x, sdot);
-        sdot = fmaf(qb.w, k3.y, sdot);
+    const int64_t slot_base = ((int64_t)t * heads + (int64_t)kvh * GROUP) * max_chunks + c;
+    // scores and slice softmax: wave w takes query heads w, w+4, ...; lane = key
+    for (int g = wave; g < GROUP; g += kAttnThreads / kWave) {
+      float sdot = 0.0f;
+      if (lane < kk) {
+        const __half* kr = Ks + lane * KS;
+        const float* qg = Qs + g * D;
+        for (int d = 0; d < D; d += 8) {
+          const uint4 raw = *(const uint4*)(kr + d);
+          const __half2* h2 = (const __half2*)&raw;
+          const float4 qa = *(const float4*)(qg + d), qb = *(const float4*)(qg + d + 4);
+          const float2 k0 = __half22float2(h2[0]), k1 = __half22float2(h2[1]);
+          const float2 k2 = __half22float2(h2[2]), k3 = __half22float2(h2[3]);
+          sdot = fmaf(qa.x, k0.x, sdot);
+          sdot = fmaf(qa.y, k0.y, sdot);
+          sdot = fmaf(qa.z, k1.x, sdot);
+          sdot = fmaf(qa.w, k1.y, sdot);
+          sdot = fmaf(qb.x, k2.x, sdot);
+          sdot = fmaf(qb.y, k2.y, sdot);
+          sdot = fmaf(qb.z, k3.x, sdot);
+          sdot = fmaf(qb.w, k3.y, sdot);
+        }
+      }
+      const bool live = lane < nk && (!kv_index || kv_cell(kv_index, index_stride, t, start + lane) >= 0);
+      const float sc = live ? sdot * scale : -INFINITY;
+      float m = sc;
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+      const float pr = live ? expf(sc - m) : 0.0f;
+      float l = pr;
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) l += __shfl_xor(l, o);
+      if (lane < kk) Ps[g * kk + lane] = pr;
+      if (lane == 0) {
+        part_ml[(slot_base + (int64_t)g * max_chunks) * 2 + 0] = m;
+        part_ml[(slot_base + (int64_t)g * max_chunks) * 2 + 1] = l;
       }
     }
-    const bool live = lane < nk && (!kv_index || kv_cell(kv_index, index_stride, t, start + lane) >= 0);
-    const float sc = live ? sdot * scale : -INFINITY;
-    float m = sc;
+    __syncthreads();
+    // unnormalised weighted values: thread o takes query head g, dims 2e, 2e+1
+    for (int o = tid; o < GROUP * halfD; o += kAttnThreads) {
+      const int g = o / halfD, e = o - g * halfD;
+      const float* pg = Ps + g * kk;
+      float a0 = 0.0f, a1 = 0.0f;
+      // four keys per step: one float4 of weights, four value pairs (keys past
+      // nk have weight 0 and a finite staged row, so they add exactly 0)
+      for (int k = 0; k < nk; k += 4) {
+        const float4 p4 = *(const float4*)(pg + k);
+        const float2 v0 = __half22float2(*(const __half2*)(Vs + (k + 0) * D + 2 * e));
+        const float2 v1 = __half22float2(*(const __half2*)(Vs + (k + 1) * D + 2 * e));
+        const float2 v2 = __half22float2(*(const __half2*)(Vs + (k + 2) * D + 2 * e));
+        const float2 v3 = __half22float2(*(const __half2*)(Vs + (k + 3) * D + 2 * e));
+        a0 = fmaf(p4.x, v0.x, a0);
+        a1 = fmaf(p4.x, v0.y, a1);
+        a0 = fmaf(p4.y, v1.x, a0);
+        a1 = fmaf(p4.y, v1.y, a1);
+        a0 = fmaf(p4.z, v2.x, a0);
+        a1 = fmaf(p4.z, v2.y, a1);
+        a0 = fmaf(p4.w, v3.x, a0);
+        a1 = fmaf(p4.w, v3.y, a1);
+      }
+      *(float2*)(part_acc + (slot_base + (int64_t)g * max_chunks) * D + 2 * e) = make_float2(a0, a1);
+    }
+    __syncthreads();  // Qs and Ps are rewritten for the next token
+  }
+}
+
+// A prefill chunk's attention slice on the matrix cores
+// (v_mfma_f32_16x16x32_f16): one block = one 64-key slice x one key head x
+// 64 query rows, the rows being TQ = 64 / GROUP consecutive tokens times the
+// GROUP query heads of that key head (row r = token r / GROUP, head r %
+// GROUP).  One sequence's chunk only (its tokens share the cache).
+//   S = Q K^T: queries as three halves (q1 = f16(q), q2 = f16(q - q1),
+//   q3 = f16(q - q1 - q2): every bit of the f32 query), keys exact halves,
+//   f32 accumulation.  Two halves (22 bits) were not enough: a softmax feels
+//   a score's absolute error, and scores of a few hundred turned the last
+//   bits of the query into 1e-4 of the output.
+//   P = exp(S*scale - rowmax) per row over the slice's live keys (key <
+//   pos[t] + 1, cell held), written as (m, l) like the VALU kernel.
+//   O = P V with P as two halves and V (staged transposed) exact halves.
+// The partial sums land where attend_split_kernel writes them, so
+// attend_merge_kernel folds them unchanged.
+// MFMA fragments (16x16x32): lane l holds row/column l % 16 and values
+// 8 (l / 16) .. +8 of the 32; the result element i of lane l is row
+// 4 (l / 16) + i, column l % 16.
+typedef _Float16 att_h8 __attribute__((ext_vector_type(8)));
+typedef float att_f4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ att_f4 att_mfma(att_h8 a, att_h8 b, att_f4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+constexpr int kChunkKeys = 64;
+__host__ __device__ __forceinline__ int attn_chunk_pad(int d) { return d + 8; }  // halves per LDS row
+__host__ __device__ __forceinline__ size_t attn_chunk_lds_bytes(int head_dim) {
+  const int dp = attn_chunk_pad(head_dim), kp = kChunkKeys + 8;
+  return 2 * ((size_t)3 * 64 * dp + (size_t)kChunkKeys * dp + (size_t)head_dim * kp + (size_t)2 * 4 * 16 * kp);
+}
+
+template <int GROUP, int D>
+__global__ __launch_bounds__(256) void attend_chunk_kernel(
+    const float* __restrict__ q, int64_t q_stride, const __half* __restrict__ kc, const __half* __restrict__ vc,
+    int heads, int kv_heads, float scale, const int32_t* __restrict__ pos_dev, int max_chunks,
+    float* __restrict__ part_acc, float* __restrict__ part_ml, const int32_t* __restrict__ kv_index, int tokens) {
+  constexpr int TQ = 64 / GROUP;
+  constexpr int DP = D + 8, KP = kChunkKeys + 8;
+  const int c = blockIdx.x, kvh = blockIdx.y, t0 = blockIdx.z * TQ;
+  const int t1 = min(t0 + TQ, tokens);
+  int count_max = 0;
+  for (int t = t0; t < t1; t++) count_max = max(count_max, pos_dev[t] + 1);
+  const int start = c * kChunkKeys;
+  if (start >= count_max) return;
+  const int nk_max = min(kChunkKeys, count_max - start);
+  const int kvw = kv_heads * D;
+  extern __shared__ uint4 lds4[];
+  _Float16* Qh = (_Float16*)lds4;
+  _Float16* Qm = Qh + 64 * DP;
+  _Float16* Ql = Qm + 64 * DP;
+  _Float16* Ks = Ql + 64 * DP;
+  _Float16* Vt = Ks + kChunkKeys * DP;
+  _Float16* Ph = Vt + D * KP;
+  _Float16* Pl = Ph + 4 * 16 * KP;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int lm = lane & 15, lk = lane >> 4;
+
+  // keys (rows) and values (transposed); keys past the end repeat the last
+  // live one (masked below); every load issued before any LDS store
+  const __half* kbase = kc + (int64_t)kvh * D;
+  const __half* vbase = vc + (int64_t)kvh * D;
+  constexpr int pieces = D / 8, total = kChunkKeys * pieces, per = total / 256;
+  static_assert(total % 256 == 0, "whole pieces per thread");
+  uint4 kv[per], vv[per];
 #pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
-    const float pr = live ? expf(sc - m) : 0.0f;
-    float l = pr;
+  for (int j = 0; j < per; j++) {
+    const int i = tid + j * 256;
+    const int key = min(i / pieces, nk_max - 1), pc = i % pieces;
+    const int cell = max(kv_cell(kv_index, 0, t0, start + key), 0);
+    const int64_t off = (int64_t)cell * kvw + pc * 8;
+    kv[j] = *(const uint4*)(kbase + off);
+    vv[j] = *(const uint4*)(vbase + off);
+  }
+  // queries: row r = token t0 + r / GROUP, head kvh * GROUP + r % GROUP
+  constexpr int qper = 64 * D / 4 / 256;  // float4 per thread
+  float4 qv[qper];
 #pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) l += __shfl_xor(l, o);
-    if (lane < kk) Ps[g * kk + lane] = pr;
-    if (lane == 0) {
-      part_ml[(slot_base + (int64_t)g * max_chunks) * 2 + 0] = m;
-      part_ml[(slot_base + (int64_t)g * max_chunks) * 2 + 1] = l;
+  for (int j = 0; j < qper; j++) {
+    const int i = tid + j * 256;  // float4 index over 64 rows x D/4
+    const int r = i / (D / 4), e = i % (D / 4);
+    const int t = t0 + r / GROUP;
+    qv[j] = t < tokens ? *(const float4*)(q + (int64_t)t * q_stride + (int64_t)(kvh * GROUP + r % GROUP) * D + 4 * e)
+                       : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  }
+#pragma unroll
+  for (int j = 0; j < per; j++) {
+    const int i = tid + j * 256;
+    const int key = i / pieces, pc = i % pieces;
+    *(uint4*)(Ks + key * DP + pc * 8) = kv[j];
+    const _Float16* v8 = (const _Float16*)&vv[j];
+#pragma unroll
+    for (int d = 0; d < 8; d++) Vt[(pc * 8 + d) * KP + key] = v8[d];
+  }
+#pragma unroll
+  for (int j = 0; j < qper; j++) {
+    const int i = tid + j * 256;
+    const int r = i / (D / 4), e = i % (D / 4);
+    const float vals[4] = {qv[j].x, qv[j].y, qv[j].z, qv[j].w};
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      const _Float16 h = (_Float16)vals[u];
+      const float r1 = vals[u] - (float)h;  // exact
+      const _Float16 mid = (_Float16)r1;
+      Qh[r * DP + 4 * e + u] = h;
+      Qm[r * DP + 4 * e + u] = mid;
+      Ql[r * DP + 4 * e + u] = (_Float16)(r1 - (float)mid);
     }
   }
   __syncthreads();
-  // unnormalised weighted values: thread o takes query head g, dims 2e, 2e+1
-  const int halfD = D >> 1;
-  for (int o = tid; o < GROUP * halfD; o += kAttnThreads) {
-    const int g = o / halfD, e = o - g * halfD;
-    const float* pg = Ps + g * kk;
-    float a0 = 0.0f, a1 = 0.0f;
-    // four keys per step: one float4 of weights, four value pairs (keys past
-    // nk have weight 0 and a copy of a live row, so they add exactly 0)
-    for (int k = 0; k < nk; k += 4) {
-      const float4 p4 = *(const float4*)(pg + k);
-      const float2 v0 = __half22float2(*(const __half2*)(Vs + (k + 0) * D + 2 * e));
-      const float2 v1 = __half22float2(*(const __half2*)(Vs + (k + 1) * D + 2 * e));
-      const float2 v2 = __half22float2(*(const __half2*)(Vs + (k + 2) * D + 2 * e));
-      const float2 v3 = __half22float2(*(const __half2*)(Vs + (k + 3) * D + 2 * e));
-      a0 = fmaf(p4.x, v0.x, a0);
-      a1 = fmaf(p4.x, v0.y, a1);
-      a0 = fmaf(p4.y, v1.x, a0);
-      a1 = fmaf(p4.y, v1.y, a1);
-      a0 = fmaf(p4.z, v2.x, a0);
-      a1 = fmaf(p4.z, v2.y, a1);
-      a0 = fmaf(p4.w, v3.x, a0);
-      a1 = fmaf(p4.w, v3.y, a1);
+
+  // S for this wave's 16 rows x 64 keys
+  const int row0 = wave * 16;
+  att_f4 sacc[4];
+#pragma unroll
+  for (int nt = 0; nt < 4; nt++) sacc[nt] = att_f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int ks = 0; ks < D / 32; ks++) {
+    const att_h8 ah = *(const att_h8*)(Qh + (row0 + lm) * DP + 32 * ks + 8 * lk);
+    const att_h8 am = *(const att_h8*)(Qm + (row0 + lm) * DP + 32 * ks + 8 * lk);
+    const att_h8 al = *(const att_h8*)(Ql + (row0 + lm) * DP + 32 * ks + 8 * lk);
+#pragma unroll
+    for (int nt = 0; nt < 4; nt++) {
+      const att_h8 b = *(const att_h8*)(Ks + (16 * nt + lm) * DP + 32 * ks + 8 * lk);
+      sacc[nt] = att_mfma(ah, b, sacc[nt]);
+      sacc[nt] = att_mfma(am, b, sacc[nt]);
+      sacc[nt] = att_mfma(al, b, sacc[nt]);
     }
-    *(float2*)(part_acc + (slot_base + (int64_t)g * max_chunks) * D + 2 * e) = make_float2(a0, a1);
+  }
+  // rows 4 lk + i of this wave: token, its count, the slice's live keys
+  float mrow[4], lrow[4];
+  int cnt[4];
+  bool rowlive[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int r = row0 + 4 * lk + i, t = t0 + r / GROUP;
+    rowlive[i] = t < tokens;
+    cnt[i] = rowlive[i] ? pos_dev[t] + 1 : 0;
+    rowlive[i] = rowlive[i] && start < cnt[i];
+  }
+  float pv[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    float m = -INFINITY;
+#pragma unroll
+    for (int nt = 0; nt < 4; nt++) {
+      const int key = start + 16 * nt + lm;
+      const bool live = key < cnt[i] && (!kv_index || kv_cell(kv_index, 0, t0, key) >= 0);
+      pv[i][nt] = live ? sacc[nt][i] * scale : -INFINITY;
+      m = fmaxf(m, pv[i][nt]);
+    }
+#pragma unroll
+    for (int o = 8; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    float l = 0.0f;
+#pragma unroll
+    for (int nt = 0; nt < 4; nt++) {
+      pv[i][nt] = pv[i][nt] == -INFINITY ? 0.0f : expf(pv[i][nt] - m);
+      l += pv[i][nt];
+    }
+#pragma unroll
+    for (int o = 8; o >= 1; o >>= 1) l += __shfl_xor(l, o);
+    mrow[i] = m;
+    lrow[i] = l;
+  }
+  // P into this wave's LDS rows (hi and lo halves), read back as A fragments
+  _Float16* ph = Ph + wave * 16 * KP;
+  _Float16* pl = Pl + wave * 16 * KP;
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int nt = 0; nt < 4; nt++) {
+      const float p = pv[i][nt];
+      const _Float16 h = (_Float16)p;
+      ph[(4 * lk + i) * KP + 16 * nt + lm] = h;
+      pl[(4 * lk + i) * KP + 16 * nt + lm] = (_Float16)(p - (float)h);
+    }
+  // (a wave's LDS operations complete in order: its reads below see these stores)
+  att_f4 oacc[D / 16];
+#pragma unroll
+  for (int nt = 0; nt < D / 16; nt++) oacc[nt] = att_f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int ks = 0; ks < kChunkKeys / 32; ks++) {
+    const att_h8 ah = *(const att_h8*)(ph + lm * KP + 32 * ks + 8 * lk);
+    const att_h8 al = *(const att_h8*)(pl + lm * KP + 32 * ks + 8 * lk);
+#pragma unroll
+    for (int nt = 0; nt < D / 16; nt++) {
+      const att_h8 b = *(const att_h8*)(Vt + (16 * nt + lm) * KP + 32 * ks + 8 * lk);
+      oacc[nt] = att_mfma(ah, b, oacc[nt]);
+      oacc[nt] = att_mfma(al, b, oacc[nt]);
+    }
+  }
+  // the slot of (token, head): as attend_split_kernel
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    if (!rowlive[i]) continue;
+    const int r = row0 + 4 * lk + i, t = t0 + r / GROUP, h = kvh * GROUP + r % GROUP;
+    const int64_t slot = ((int64_t)t * heads + h) * max_chunks + c;
+#pragma unroll
+    for (int nt = 0; nt < D / 16; nt++) part_acc[slot * D + 16 * nt + lm] = oacc[nt][i];
+    if (lm == 0) {
+      part_ml[slot * 2 + 0] = mrow[i];
+      part_ml[slot * 2 + 1] = lrow[i];
+    }
   }
 }
 
@@ -779,7 +1002,45 @@ int launch_attend(hipStream_t s, const float* q, int64_t q_stride, const uint16_
   const size_t acc_bytes = ((size_t)slots * head_dim * sizeof(float) + 255) & ~(size_t)255;
   float* part_ml = (float*)((char*)work + acc_bytes);
   const int group = heads / kv_heads;
-  dim3 grid(chunks, kv_heads, tokens);
+  // one sequence's chunk (its tokens share one cache): 16 tokens per block
+  // over one staged slice (f16 form; the q8 kernel takes one token a block)
+  const bool one_seq = kv_index ? index_stride == 0 : cache_stride == 0;
+  if (one_seq && pos_dev && tokens > kMaxTokens && form != MI_CACHE_Q8 && kk == kChunkKeys &&
+      (head_dim == 64 || head_dim == 128)) {
+    // a prefill chunk: the matrix-core slice kernel, then the same merge
+    dim3 cgrid(chunks, kv_heads, (tokens + 64 / group - 1) / (64 / group));
+    const size_t lds = attn_chunk_lds_bytes(head_dim);
+    // more than 64 KB of dynamic LDS has to be asked for, once per kernel
+#define MI_CHUNK(G, DD)                                                                                        \
+  {                                                                                                            \
+    static const hipError_t big = hipFuncSetAttribute((const void*)attend_chunk_kernel<G, DD>,                \
+                                                      hipFuncAttributeMaxDynamicSharedMemorySize,             \
+                                                      (int)attn_chunk_lds_bytes(DD));                         \
+    if (big != hipSuccess) return hip_check(big, "attend_chunk LDS size");                                    \
+    hipLaunchKernelGGL((attend_chunk_kernel<G, DD>), cgrid, dim3(256), lds, s, q, q_stride,                    \
+                       (const __half*)k_cache, (const __half*)v_cache, heads, kv_heads, scale, pos_dev, chunks, \
+                       part_acc, part_ml, kv_index, tokens);                                                   \
+  }
+#define MI_CHUNK_D(G) \
+  if (head_dim == 64) MI_CHUNK(G, 64) else MI_CHUNK(G, 128)
+    switch (group) {
+      case 1: MI_CHUNK_D(1); break;
+      case 2: MI_CHUNK_D(2); break;
+      case 4: MI_CHUNK_D(4); break;
+      case 8: MI_CHUNK_D(8); break;
+      default: return fail(MI_ERR_SHAPE, "attend: %d query heads per key head is not 1, 2, 4 or 8", group);
+    }
+#undef MI_CHUNK_D
+#undef MI_CHUNK
+    int rc = hip_check(hipGetLastError(), "attend_chunk launch");
+    if (rc) return rc;
+    const size_t mlds = ((size_t)chunks * 2 + (chunks + kMergeBatch - 1) / kMergeBatch * kMergeBatch) * sizeof(float);
+    hipLaunchKernelGGL(attend_merge_kernel, dim3(heads, tokens), dim3(head_dim < 64 ? 64 : head_dim), mlds, s,
+                       part_acc, part_ml, heads, head_dim, pos_dev, count_host, chunks, out, (uint8_t*)xq_out);
+    return hip_check(hipGetLastError(), "attend_merge launch");
+  }
+  const int tq = (one_seq && tokens > kMaxTokens && form != MI_CACHE_Q8) ? 16 : 1;
+  dim3 grid(chunks, kv_heads, (tokens + tq - 1) / tq);
   const __half* kc = (const __half*)k_cache;
   const __half* vc = (const __half*)v_cache;
   const bool q8 = form == MI_CACHE_Q8;
@@ -793,7 +1054,7 @@ int launch_attend(hipStream_t s, const float* q, int64_t q_stride, const uint16_
   else                                                                                                     \
     hipLaunchKernelGGL(attend_split_kernel<G>, grid, dim3(kAttnThreads), shmem, s, q, q_stride, kc, vc,     \
                        cache_stride, heads, kv_heads, head_dim, scale, pos_dev, count_host, chunks,         \
-                       part_acc, part_ml, kv_index, index_stride)
+                       part_acc, part_ml, kv_index, index_stride, tokens, tq)
   switch (group) {
     case 1: MI_ATTEND(1); break;
     case 2: MI_ATTEND(2); break;
