@@ -449,7 +449,7 @@ constexpr int kChunkKeys = 64;
 __host__ __device__ __forceinline__ int attn_chunk_pad(int d) { return d + 8; }  // halves per LDS row
 __host__ __device__ __forceinline__ size_t attn_chunk_lds_bytes(int head_dim) {
   const int dp = attn_chunk_pad(head_dim), kp = kChunkKeys + 8;
-  return 2 * ((size_t)3 * 64 * dp + (size_t)kChunkKeys * dp + (size_t)head_dim * kp + (size_t)2 * 4 * 16 * kp);
+  return 2 * ((size_t)kChunkKeys * dp + (size_t)head_dim * kp + (size_t)2 * 4 * 16 * kp);
 }
 
 template <int GROUP, int D>
@@ -468,10 +468,7 @@ __global__ __launch_bounds__(256) void attend_chunk_kernel(
   const int nk_max = min(kChunkKeys, count_max - start);
   const int kvw = kv_heads * D;
   extern __shared__ uint4 lds4[];
-  _Float16* Qh = (_Float16*)lds4;
-  _Float16* Qm = Qh + 64 * DP;
-  _Float16* Ql = Qm + 64 * DP;
-  _Float16* Ks = Ql + 64 * DP;
+  _Float16* Ks = (_Float16*)lds4;
   _Float16* Vt = Ks + kChunkKeys * DP;
   _Float16* Ph = Vt + D * KP;
   _Float16* Pl = Ph + 4 * 16 * KP;
@@ -494,16 +491,19 @@ __global__ __launch_bounds__(256) void attend_chunk_kernel(
     kv[j] = *(const uint4*)(kbase + off);
     vv[j] = *(const uint4*)(vbase + off);
   }
-  // queries: row r = token t0 + r / GROUP, head kvh * GROUP + r % GROUP
-  constexpr int qper = 64 * D / 4 / 256;  // float4 per thread
-  float4 qv[qper];
+  // this wave's 16 query rows straight into A fragments (row r = token
+  // t0 + r / GROUP, head kvh * GROUP + r % GROUP): lane row lm, values
+  // 32 ks + 8 lk .. +8 of each 32-value step, as three halves
+  const int row0 = wave * 16;
+  float4 qraw[D / 32][2];
+  {
+    const int r = row0 + lm, t = t0 + r / GROUP;
+    const float* qr = q + (int64_t)min(t, tokens - 1) * q_stride + (int64_t)(kvh * GROUP + r % GROUP) * D;
 #pragma unroll
-  for (int j = 0; j < qper; j++) {
-    const int i = tid + j * 256;  // float4 index over 64 rows x D/4
-    const int r = i / (D / 4), e = i % (D / 4);
-    const int t = t0 + r / GROUP;
-    qv[j] = t < tokens ? *(const float4*)(q + (int64_t)t * q_stride + (int64_t)(kvh * GROUP + r % GROUP) * D + 4 * e)
-                       : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (int ks = 0; ks < D / 32; ks++) {
+      qraw[ks][0] = t < tokens ? *(const float4*)(qr + 32 * ks + 8 * lk) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      qraw[ks][1] = t < tokens ? *(const float4*)(qr + 32 * ks + 8 * lk + 4) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
   }
 #pragma unroll
   for (int j = 0; j < per; j++) {
@@ -514,33 +514,26 @@ __global__ __launch_bounds__(256) void attend_chunk_kernel(
 #pragma unroll
     for (int d = 0; d < 8; d++) Vt[(pc * 8 + d) * KP + key] = v8[d];
   }
-#pragma unroll
-  for (int j = 0; j < qper; j++) {
-    const int i = tid + j * 256;
-    const int r = i / (D / 4), e = i % (D / 4);
-    const float vals[4] = {qv[j].x, qv[j].y, qv[j].z, qv[j].w};
-#pragma unroll
-    for (int u = 0; u < 4; u++) {
-      const _Float16 h = (_Float16)vals[u];
-      const float r1 = vals[u] - (float)h;  // exact
-      const _Float16 mid = (_Float16)r1;
-      Qh[r * DP + 4 * e + u] = h;
-      Qm[r * DP + 4 * e + u] = mid;
-      Ql[r * DP + 4 * e + u] = (_Float16)(r1 - (float)mid);
-    }
-  }
   __syncthreads();
 
   // S for this wave's 16 rows x 64 keys
-  const int row0 = wave * 16;
   att_f4 sacc[4];
 #pragma unroll
   for (int nt = 0; nt < 4; nt++) sacc[nt] = att_f4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
   for (int ks = 0; ks < D / 32; ks++) {
-    const att_h8 ah = *(const att_h8*)(Qh + (row0 + lm) * DP + 32 * ks + 8 * lk);
-    const att_h8 am = *(const att_h8*)(Qm + (row0 + lm) * DP + 32 * ks + 8 * lk);
-    const att_h8 al = *(const att_h8*)(Ql + (row0 + lm) * DP + 32 * ks + 8 * lk);
+    att_h8 ah, am, al;
+    const float qf[8] = {qraw[ks][0].x, qraw[ks][0].y, qraw[ks][0].z, qraw[ks][0].w,
+                         qraw[ks][1].x, qraw[ks][1].y, qraw[ks][1].z, qraw[ks][1].w};
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+      const _Float16 h = (_Float16)qf[u];
+      const float r1 = qf[u] - (float)h;  // exact
+      const _Float16 mid = (_Float16)r1;
+      ah[u] = h;
+      am[u] = mid;
+      al[u] = (_Float16)(r1 - (float)mid);
+    }
 #pragma unroll
     for (int nt = 0; nt < 4; nt++) {
       const att_h8 b = *(const att_h8*)(Ks + (16 * nt + lm) * DP + 32 * ks + 8 * lk);
