@@ -36,7 +36,10 @@
 // wave decodes its own rows' weight codes straight from global memory, one
 // stage ahead.  Long reductions over few output tiles split K across
 // blockIdx.z, with partial sums in the workspace and a second kernel adding
-// them in split order (deterministic) before the epilogue.
+// them in split order (deterministic) before the epilogue.  Rows may come
+// from up to three matrices of one kind laid end to end (RowSegs: a layer's
+// q|k|v in one launch), and one activation prep (prefill_prepare) can serve
+// several launches over the same input.
 //
 // Replaces device_matmul_into's batched kernels (src/molla/nn/gpu.mojo:1809
 // planar_matmul_kernel, :2665 planar_nvmma_kernel; dispatch :3015) for
@@ -94,7 +97,6 @@ __device__ __forceinline__ uint32_t ld4u(const uint8_t* p) {
 }
 __device__ __forceinline__ uint32_t ld2(const uint8_t* p) { return *(const uint16_t*)p; }
 __device__ __forceinline__ float f16f(uint32_t bits) { return half_bits_to_float(bits & 0xFFFF); }
-__device__ __forceinline__ uint32_t byte_of(uint2 v, int i) { return ((i < 4 ? v.x : v.y) >> (8 * (i & 3))) & 0xFF; }
 
 // (sc, m) of group j of a K-quant superblock from scales[0..11] in y, z, w
 // (quant.mojo:161 _k_scale).
