@@ -45,6 +45,7 @@
 // planar_matmul_kernel, :2665 planar_nvmma_kernel; dispatch :3015) for
 // tokens above the decode batch; output layout and epilogues as
 // gpu.mojo:1005 and :2955-2961.
+#include <algorithm>
 #include <type_traits>
 
 #include "matvec_rows.h"
@@ -59,9 +60,7 @@ typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 constexpr int kTileTok = 32;     // tokens of one MFMA tile
 constexpr int kStage = 64;       // values of K per LDS stage (4 MFMA steps)
 constexpr int kChunk = 256;      // values per min-term MFMA / K-quant superblock
-constexpr int kWaveTok = 2;      // token tiles per wave (and per block)
-constexpr int kWaveRows = 2;     // row tiles per wave (the pipeline below writes out two)
-constexpr int kStageBytes = kWaveTok * 4 * 2 * 1024;  // one LDS buffer
+constexpr int kPadTiles = 4;     // token tiles the activation prep pads to (the widest block's)
 constexpr int kRing = 2;         // register slots: the stage computed and the one in flight
 
 __device__ __forceinline__ v16f mfma(v8h a, v8h b, v16f c) {
@@ -330,7 +329,7 @@ struct Prep {
 __host__ __device__ inline Prep prep_layout(int cols, int tokens) {
   Prep p;
   const int tt = (tokens + kTileTok - 1) / kTileTok;
-  p.ttp = (tt + kWaveTok - 1) / kWaveTok * kWaveTok;
+  p.ttp = (tt + kPadTiles - 1) / kPadTiles * kPadTiles;
   p.ks = cols / 16;
   p.nch = (cols + kChunk - 1) / kChunk;
   p.xp = 0;
@@ -430,13 +429,15 @@ __global__ __launch_bounds__(256) void prefill_x_kernel(const float* __restrict_
 }
 
 // ---- the matmul ------------------------------------------------------------
-template <int KIND, int W>
+template <int KIND, int W, int RT, int TT>
 __global__ __launch_bounds__(W * 64, KIND == MI_Q6_K ? 2 : 1) void prefill_kernel(const RowSegs sg,
                                                          int cols, int tokens, const uint8_t* __restrict__ work,
                                                          int stages_per_split, float* __restrict__ y, int64_t ldy,
                                                          int epi, const float* __restrict__ aux,
                                                          float* __restrict__ part) {
   using K = typename KindOf<KIND>::T;
+  constexpr int kWaveRows = RT, kWaveTok = TT;  // row and token tiles per wave
+  constexpr int kStageBytes = TT * 4 * 2 * 1024;  // one LDS buffer: TT tiles x 4 steps x 2 halves
   __shared__ __attribute__((aligned(16))) uint8_t xl[2][kStageBytes];
   const Prep P = prep_layout(cols, tokens);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -468,22 +469,13 @@ __global__ __launch_bounds__(W * 64, KIND == MI_Q6_K ? 2 : 1) void prefill_kerne
     xsrc[q] = xp + (tile0 + tt) * x_tile + within * 16;
     xdst[q] = idx * 16;
   }
-  static_assert(kPieces == 4, "the copy below is written out for four pieces");
-#define PF_LOAD_X(ST, DST)                                         \
-  {                                                                \
-    const size_t o_ = (size_t)(ST) * 8192;                         \
-    DST[0] = *(const v4u*)(xsrc[0] + o_);                        \
-    DST[1] = *(const v4u*)(xsrc[1] + o_);                        \
-    DST[2] = *(const v4u*)(xsrc[2] + o_);                        \
-    DST[3] = *(const v4u*)(xsrc[3] + o_);                        \
+#define PF_LOAD_X(ST, DST)                                                       \
+  {                                                                              \
+    const size_t o_ = (size_t)(ST) * 8192;                                       \
+    _Pragma("unroll") for (int q = 0; q < kPieces; q++) DST[q] = *(const v4u*)(xsrc[q] + o_); \
   }
-#define PF_STORE_X(SRC, BUF)                      \
-  {                                               \
-    *(v4u*)(&xl[BUF][xdst[0]]) = SRC[0];        \
-    *(v4u*)(&xl[BUF][xdst[1]]) = SRC[1];        \
-    *(v4u*)(&xl[BUF][xdst[2]]) = SRC[2];        \
-    *(v4u*)(&xl[BUF][xdst[3]]) = SRC[3];        \
-  }
+#define PF_STORE_X(SRC, BUF) \
+  { _Pragma("unroll") for (int q = 0; q < kPieces; q++) *(v4u*)(&xl[BUF][xdst[q]]) = SRC[q]; }
 
   typename K::Raw raw[kRing][kWaveRows];
   v16f tot[kWaveRows][kWaveTok], acc[kWaveRows][kWaveTok];
@@ -593,8 +585,7 @@ __global__ __launch_bounds__(W * 64, KIND == MI_Q6_K ? 2 : 1) void prefill_kerne
   {                                                                                    \
     const int ist = min((ST), st1 - 1);                                                \
     PF_LOAD_X(ist, XD)                                                                 \
-    K::load(RW[0], wrow[0], ist, kh);                                                  \
-    K::load(RW[1], wrow[1], ist, kh);                                                  \
+    _Pragma("unroll") for (int rt = 0; rt < kWaveRows; rt++) K::load(RW[rt], wrow[rt], ist, kh); \
   }
   PF_ISSUE(st0, raw[0], xr0)
   PF_STORE_X(xr0, 0)
@@ -661,15 +652,38 @@ __global__ __launch_bounds__(256) void prefill_reduce_kernel(const float* __rest
 }
 
 constexpr int kWaves = 4;
-constexpr int kBlockRows = kWaves * kWaveRows * 32;
+// Wave tile shapes: (row tiles, token tiles) of 32.  2 x 2 (64 rows x 64
+// tokens) or 1 x 4 (32 rows x 128 tokens: each decoded weight serves twice
+// the tokens, the block's activation stage is twice as large).
+struct Shape {
+  int rt, tt;
+  int block_rows() const { return kWaves * rt * 32; }
+};
+// Measured at 256 tokens: Q6_K (three products per step, the heavier
+// decode) gains from 1 x 4 (4096x14336: 152 against 208 us); Q4_K loses
+// (14336x4096: 140 against 108 us: 195 registers a wave, one wave per SIMD).
+Shape shape_for(int kind, int tokens) {
+  if (kind == MI_Q6_K && tokens > 64) return Shape{1, 4};
+  return Shape{2, 2};
+}
 
 template <int KIND>
 int launch_kind(hipStream_t s, const RowSegs& sg, int cols, int tokens, const void* work, int splits, int sps,
                 float* y, int64_t ldy, int epi, const float* aux, float* part) {
   const Prep P = prep_layout(cols, tokens);
   const int rows = sg.end[sg.nseg - 1];
-  dim3 grid((rows + kBlockRows - 1) / kBlockRows, P.ttp / kWaveTok, splits);
-  hipLaunchKernelGGL((prefill_kernel<KIND, kWaves>), grid, dim3(kWaves * 64), 0, s, sg, cols, tokens,
+  const Shape sh = shape_for(KIND, tokens);
+  const int tiles = (tokens + kTileTok - 1) / kTileTok;
+  dim3 grid((rows + sh.block_rows() - 1) / sh.block_rows(), (tiles + sh.tt - 1) / sh.tt, splits);
+  (void)P;
+  if constexpr (KIND == MI_Q6_K) {
+    if (sh.tt == 4) {
+      hipLaunchKernelGGL((prefill_kernel<KIND, kWaves, 1, 4>), grid, dim3(kWaves * 64), 0, s, sg, cols, tokens,
+                         (const uint8_t*)work, sps, y, ldy, epi, aux, splits > 1 ? part : nullptr);
+      return hip_check(hipGetLastError(), "prefill launch");
+    }
+  }
+  hipLaunchKernelGGL((prefill_kernel<KIND, kWaves, 2, 2>), grid, dim3(kWaves * 64), 0, s, sg, cols, tokens,
                      (const uint8_t*)work, sps, y, ldy, epi, aux, splits > 1 ? part : nullptr);
   return hip_check(hipGetLastError(), "prefill launch");
 }
@@ -681,9 +695,12 @@ int launch_kind(hipStream_t s, const RowSegs& sg, int cols, int tokens, const vo
 // 110 us at 2 splits (448 blocks) against 125 us at 4, while 4096x14336 wants
 // 8 (512 blocks: 212 us) over 4 (232 us).
 constexpr int kBlockSlots = 2 * 256;
-int choose_splits(int rows, int cols, int tokens) {
+int choose_splits(int kind, int rows, int cols, int tokens) {
   const Prep P = prep_layout(cols, tokens);
-  const int64_t blocks = (int64_t)((rows + kBlockRows - 1) / kBlockRows) * (P.ttp / kWaveTok);
+  const Shape sh = shape_for(kind, tokens);
+  const int tiles = (tokens + kTileTok - 1) / kTileTok;
+  const int64_t blocks = (int64_t)((rows + sh.block_rows() - 1) / sh.block_rows()) * ((tiles + sh.tt - 1) / sh.tt);
+  (void)P;
   const int chunks = (cols + kChunk - 1) / kChunk;
   int s = 1;
   while (blocks * 2 * s <= kBlockSlots && chunks >= 2 * s) s *= 2;
@@ -714,7 +731,8 @@ bool prefill_fits(int kind, int32_t cols, int64_t row_bytes, const void* w) {
 
 size_t prefill_workspace(int32_t rows, int32_t cols, int32_t tokens) {
   const Prep P = prep_layout(cols, tokens);
-  const int splits = rows > 0 ? choose_splits(rows, cols, tokens) : 1;
+  int splits = 1;
+  for (int k : {MI_Q4_K, MI_Q6_K}) splits = std::max(splits, rows > 0 ? choose_splits(k, rows, cols, tokens) : 1);
   size_t part = splits > 1 ? (size_t)splits * tokens * rows * 4 : 0;
   return P.total + ((part + 255) & ~(size_t)255);
 }
@@ -733,7 +751,7 @@ int launch_prefill_segs(hipStream_t s, int kind, const RowSegs& sg, int32_t cols
                         int64_t ldy, int32_t epi, const float* aux, void* work, size_t work_bytes) {
   const Prep P = prep_layout(cols, tokens);
   const int rows = sg.end[sg.nseg - 1];
-  int splits = choose_splits(rows, cols, tokens);
+  int splits = choose_splits(kind, rows, cols, tokens);
   const size_t need = (size_t)splits * tokens * rows * 4;
   if (splits > 1 && work_bytes < P.total + need) splits = 1;  // no room for partial sums
   const int nst = cols / kStage;
