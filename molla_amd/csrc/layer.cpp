@@ -168,21 +168,29 @@ static int prefill_layer(hipStream_t s, const mi_layer_desc* d, float* resid, ui
   // attention_layer (block.mojo:319)
   auto tile = [&](const mi_weight& w) { return prefill_fits(w.kind, w.cols, w.row_bytes, w.data); };
   if ((rc = launch_rms_norm(s, resid, d->attn_norm, d->width, tokens, d->eps, xn, nullptr))) return rc;
-  if (d->wq.kind == d->wk.kind && d->wq.kind == d->wv.kind && tile(d->wq) && tile(d->wk) && tile(d->wv)) {
-    // q|k|v as one launch over their rows end to end, on one activation prep
-    RowSegs sg{};
+  if (tile(d->wq) && tile(d->wk) && tile(d->wv)) {
+    // one activation prep for q, k and v; consecutive projections of one
+    // kind as one launch over their rows end to end (q|k|v, or q|k and v
+    // when v is of another kind, as in Q4_K_M files)
+    if ((rc = prefill_prepare(s, xn, d->width, tokens, mm))) return rc;
     const mi_weight* ws[3] = {&d->wq, &d->wk, &d->wv};
     const int32_t ends[3] = {qw, qw + kvw, qw + 2 * kvw};
-    for (int i = 0; i < 3; i++) {
-      sg.w[i] = (const uint8_t*)ws[i]->data;
-      sg.rb[i] = ws[i]->row_bytes;
-      sg.end[i] = ends[i];
+    for (int i = 0; i < 3;) {
+      int j = i + 1;
+      while (j < 3 && ws[j]->kind == ws[i]->kind) j++;
+      RowSegs sg{};
+      const int32_t base_row = i == 0 ? 0 : ends[i - 1];
+      for (int k = i; k < j; k++) {
+        sg.w[k - i] = (const uint8_t*)ws[k]->data;
+        sg.rb[k - i] = ws[k]->row_bytes;
+        sg.end[k - i] = ends[k] - base_row;
+      }
+      sg.nseg = j - i;
+      if ((rc = launch_prefill_segs(s, ws[i]->kind, sg, d->width, tokens, qkv + base_row, qkv_stride, MI_EPI_NONE,
+                                    nullptr, mm, mm_bytes)))
+        return rc;
+      i = j;
     }
-    sg.nseg = 3;
-    if ((rc = prefill_prepare(s, xn, d->width, tokens, mm))) return rc;
-    if ((rc = launch_prefill_segs(s, d->wq.kind, sg, d->width, tokens, qkv, qkv_stride, MI_EPI_NONE, nullptr, mm,
-                                  mm_bytes)))
-      return rc;
   } else {
     if ((rc = mat(d->wq, qw, d->width, xn, qkv, qkv_stride, MI_EPI_NONE, nullptr))) return rc;
     if ((rc = mat(d->wk, kvw, d->width, xn, qkv + qw, qkv_stride, MI_EPI_NONE, nullptr))) return rc;

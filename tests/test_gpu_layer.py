@@ -21,14 +21,17 @@ from molla_amd import synth
 pytestmark = pytest.mark.gpu
 
 
-def make_layer_weights(spec, seed):
-    """Q4_K projections and N(1, 0.1) gains; returns (numpy dict for the oracle, torch dict)."""
+def make_layer_weights(spec, seed, kinds=None):
+    """Q4_K projections (or kinds[name]) and N(1, 0.1) gains: the host dict
+    the oracle and device_layer_from take."""
+    kinds = kinds or {}
     W, H, qw, kvw = spec["width"], spec["hidden"], spec["heads"] * spec["head_dim"], spec["kv_heads"] * spec["head_dim"]
     shapes = {"wq": (qw, W), "wk": (kvw, W), "wv": (kvw, W), "wo": (W, qw), "gate": (H, W), "up": (H, W),
               "down": (W, H)}
     host = {}
     for i, (n, (r, c)) in enumerate(shapes.items()):
-        host[n] = (oracle.Q4_K, r, c, synth.quant_tensor(oracle.Q4_K, r, c, seed * 100 + i).numpy())
+        k = kinds.get(n, oracle.Q4_K)
+        host[n] = (k, r, c, synth.quant_tensor(k, r, c, seed * 100 + i).numpy())
     host["attn_norm"] = synth.normal(W, seed * 100 + 10, mean=1.0, std=0.1).numpy()
     host["ffn_norm"] = synth.normal(W, seed * 100 + 11, mean=1.0, std=0.1).numpy()
     return host
@@ -41,7 +44,7 @@ def device_layer_from(host, spec):
     bs = block.BlockSpec(width=spec["width"], hidden=spec["hidden"], heads=spec["heads"],
                          kv_heads=spec["kv_heads"], head_dim=spec["head_dim"], rope_dim=spec["rope_dim"],
                          rope_base=spec["rope_base"], neox=bool(spec["neox"]), eps=spec["eps"])
-    weights = {n: gpu.Tensor.from_bytes(torch.from_numpy(host[n][3]), oracle.Q4_K, host[n][2], host[n][1])
+    weights = {n: gpu.Tensor.from_bytes(torch.from_numpy(host[n][3]), host[n][0], host[n][2], host[n][1])
                for n in block.DeviceLayer.NAMES}
     steps = torch.from_numpy(gpu.rope_steps(spec["rope_dim"], spec["rope_base"])).cuda()
     factors = host.get("rope_factors")
@@ -413,7 +416,8 @@ def test_layer_paged_skips_positions_it_does_not_hold():
                                                (False, 40, (512, 1024, 8, 2, 64)), (True, 40, (512, 1024, 8, 2, 64)),
                                                (False, 256, (512, 1024, 8, 2, 64)),
                                                (False, 72, (1024, 1024, 8, 4, 128)),
-                                               (True, 33, (512, 1024, 4, 4, 128))])
+                                               (True, 33, (512, 1024, 4, 4, 128)),
+                                               (False, 48, "q4_k_m")])
 def test_layer_chunk_of_one_sequence(paged, tokens, dims):
     """Stride 0: the tokens are one sequence's chunk at consecutive positions
     (gpu.mojo:617 `bases` all zero).  Each token attends over the positions up
@@ -424,8 +428,11 @@ def test_layer_chunk_of_one_sequence(paged, tokens, dims):
     forward over a chunk)."""
     from molla_amd import block, gpu
     ctx = gpu.DeviceContext(0)
+    kinds = None
+    if dims == "q4_k_m":  # a Q4_K_M file's mix: v and down Q6_K (q|k one launch, v its own)
+        dims, kinds = (512, 1024, 8, 2, 64), {"wv": oracle.Q6_K, "down": oracle.Q6_K, "wo": oracle.Q5_K}
     spec = spec_of(*dims)
-    host = make_layer_weights(spec, 17)
+    host = make_layer_weights(spec, 17, kinds)
     host["rope_factors"] = llama31_factors(spec["rope_dim"] // 2)
     # Attention logits of a real model's size: with N(1, 0.1) gains these
     # random Q4_K projections make q and k elements ~50 and scaled scores of
