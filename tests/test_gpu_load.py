@@ -77,4 +77,19 @@ def test_gguf_model_decodes_like_the_oracle(tmp_path, tied, factors, kinds):
         token = pick
         sess.advance()
     del sess
+    # the same file prefilling a 20-token prompt in chunks of 16 (the prefill
+    # layer at 16 tokens, then at 4): next-token logits and pick as the oracle
+    prompt = np.array([(11 + 37 * i) % vocab for i in range(20)], dtype=np.int32)
+    sess = block.DeviceSession(ctx, model, batch=1, context=len(prompt) + 1)
+    sess.prefill(torch.from_numpy(prompt).cuda(), seq=0, start=0, chunk=16)
+    sess.finish()
+    ctx.synchronize()
+    ok = [np.zeros((len(prompt) + 1) * kvw, np.float32) for _ in layers]
+    ov = [np.zeros((len(prompt) + 1) * kvw, np.float32) for _ in layers]
+    for p, tok in enumerate(prompt):
+        want = oracle.forward(layers, emb, onorm, head, int(tok), p, p, ok, ov, f16_store=True)
+    logits = sess.logits.cpu().numpy()
+    assert np.abs(logits - want).max() <= 2e-3 * np.abs(want).max()
+    assert int(sess.picks.cpu().numpy()[0]) == oracle.argmax(want)
+    del sess
     torch.cuda.empty_cache()
