@@ -346,6 +346,16 @@ static int decoder_layer(mi_stream stream, const mi_layer_desc* d, float* resid,
     return rc;
 
   // mlp_layer (block.mojo:429), gated silu
+  if (tokens == 1 && d->gate.kind == MI_Q4_K && d->up.kind == MI_Q4_K && d->gate.row_bytes == d->up.row_bytes &&
+      q4k_glu_norm_fits(d->hidden, d->width, resid, d->ffn_norm)) {
+    // the norm inside the gate|up launch, which also writes down's input
+    void* xq2 = base + c.xq2;
+    if ((rc = launch_q4k_glu_norm(s, d->gate.data, d->up.data, d->gate.row_bytes, d->hidden, d->width, resid,
+                                  d->ffn_norm, d->eps, gate, xq2)))
+      return rc;
+    return launch_matvec(s, d->down.kind, d->down.data, d->down.row_bytes, d->width, d->hidden, xq2, tokens,
+                         resid, d->width, MI_EPI_ADD, nullptr);
+  }
   if ((rc = launch_rms_norm(s, resid, d->ffn_norm, d->width, tokens, d->eps, nullptr, xq))) return rc;
   if (tokens == 1 && d->gate.kind == MI_Q4_K && d->up.kind == MI_Q4_K && d->gate.row_bytes == d->up.row_bytes &&
       q4k_rows_fits(d->width)) {

@@ -55,6 +55,14 @@ struct QkvRope {
   const int32_t* kv_index;  // paged: the cell of position pos[0] is kv_index[pos[0]]; null: slot pos[0]
 };
 
+// The RMSNorm that glu_norm_kernel applies to its input row itself (the
+// residual x, the norm's gain and epsilon) instead of reading xq.
+struct NormIn {
+  const float* x;
+  const float* gain;
+  float eps;
+};
+
 namespace rows {
 using namespace mv;
 
@@ -75,6 +83,20 @@ __device__ __forceinline__ const uint8_t* seg_row(const RowSegs& sg, int row) {
   const int s = row < sg.end[0] ? 0 : (row < sg.end[1] ? 1 : 2);
   const int start = s == 0 ? 0 : sg.end[s - 1];
   return sg.w[s] + (int64_t)(row - start) * sg.rb[s];
+}
+
+// The activation of unit u (groups 2u, 2u + 1) into a lane's registers.
+template <bool L23, class XA>
+__device__ __forceinline__ void load_x(XUnitRegs<L23>& xr, const XA& xa, int u) {
+#pragma unroll
+  for (int e = 0; e < 2; e++) {
+#pragma unroll
+    for (int j = 0; j < 3; j++)
+#pragma unroll
+      for (int hh = 0; hh < 2; hh++) xr.l[e][j][hh] = xa.limb(0, j, hh, 2 * u + e);
+    xr.m[e] = xa.meta(0, 2 * u + e);
+    if constexpr (L23) xr.s23[e] = xa.lsum23(0, 2 * u + e);
+  }
 }
 
 // GLU: sg.w[0] = gate, sg.w[1] = up, both with sg.end[0] rows.  KIND is
@@ -102,17 +124,8 @@ __global__ __launch_bounds__(GQ ? 32 / RPW * 64 : KS * 64) void rows_kernel(
 
   constexpr bool kL23 = KIND == MI_Q4_0 || KIND == MI_Q5_0;  // kinds with a fixed offset
   XUnitRegs<kL23> xr;
-  const XAcc xa{xq, 4 * (int64_t)cols, (int64_t)(cols >> 5) * 16};
-#pragma unroll
-  for (int e = 0; e < 2; e++) {
-#pragma unroll
-    for (int j = 0; j < 3; j++)
-#pragma unroll
-      for (int hh = 0; hh < 2; hh++) xr.l[e][j][hh] = xa.limb(0, j, hh, 2 * u + e);
-    xr.m[e] = xa.meta(0, 2 * u + e);
-    if constexpr (kL23) xr.s23[e] = xa.lsum23(0, 2 * u + e);
-  }
   typename UnitOf<KIND, 1>::type un[NR];
+  load_x(xr, XAcc{xq, 4 * (int64_t)cols, (int64_t)(cols >> 5) * 16}, u);
 #pragma unroll
   for (int r = 0; r < NR; r++) {
     const int row = min(row0 + (GLU ? r % RPW : r), rows - 1);

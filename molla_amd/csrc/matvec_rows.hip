@@ -2,12 +2,106 @@
 // matrix of Q4_K, Q4_0 or Q8_0 (the other kinds in matvec_rows_more.hip), up
 // to three Q4_K matrices concatenated by rows (a layer's q, k, v), and the
 // gate/up pair with the GLU applied (a layer's MLP input side).
+#include <algorithm>
+
 #include "matvec_rows.h"
 
 namespace mi {
 using rows::launch_any;
 using rows::launch_rk;
 using rows::rows_kernel;
+
+namespace {
+using namespace mv;
+
+// The gate|up GLU of one decoding token with the layer's ffn RMSNorm folded
+// in (Q4_K, cols <= 4096).  A block is 8 waves, each owning four rows of
+// gate and of up in a 32-row group, as rows_kernel<Q4_K, 4, 1, GLU, -, GQ>;
+// the grid is at most one block per CU and a block loops over groups
+// blockIdx.x, blockIdx.x + gridDim.x, ...  The block issues the row's loads,
+// then its first group's weight loads, then normalises the row into LDS in
+// matvec form (norm_row_to_lds) while those weights stream in, and keeps the
+// activation in registers for every group it takes: the norm costs no launch
+// and is computed once per CU, not once per group.  After each group, wave 0
+// writes its act(gate) * up in matvec form for the down projection.
+__global__ __launch_bounds__(8 * 64) void glu_norm_kernel(const RowSegs sg, int cols, float* __restrict__ y,
+                                                          int epi, const NormIn nm, uint8_t* __restrict__ xq_out) {
+  constexpr int RPW = 4, NR = 2 * RPW, kNT = 8 * 64;
+  __shared__ __align__(16) uint8_t xs[4 * 4096];
+  __shared__ double red[kNT / 64];
+  __shared__ float grp[2][32];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int rows = sg.end[0];
+  const int groups = rows >> 5;
+  const int units = cols >> 6;
+  const bool act = lane < units;
+  const int u = act ? lane : units - 1;
+
+  rows::XUnitRegs<false> xr;
+  UnitOf<MI_Q4_K, 1>::type un[NR];
+  const NormRow nr = norm_row_load(nm.x, nm.gain, cols);
+  __builtin_amdgcn_sched_barrier(0);
+  int g = blockIdx.x;
+#pragma unroll
+  for (int r = 0; r < NR; r++) {
+    const int row = (g * 8 + wave) * RPW + r % RPW;
+    un[r].load(sg.w[r / RPW] + (int64_t)row * sg.rb[r / RPW], 0, 0, 0, u);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  norm_row_to_lds<kNT>(nr, cols, nm.eps, xs, red);
+  rows::load_x(xr, XLds{xs, 0, (cols >> 5) * 16}, u);
+  for (int it = 0;; it++) {
+    float acc[NR];
+#pragma unroll
+    for (int r = 0; r < NR; r++) {
+      float a[1][1] = {{0.0f}};
+      un[r].template compute<1>(xr, u, a);
+      acc[r] = act ? a[0][0] : 0.0f;
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int r = 0; r < NR; r++) acc[r] = wave_sum(acc[r]);
+    float v = acc[0];
+#pragma unroll
+    for (int r = 1; r < NR; r++)
+      if (lane == r) v = acc[r];
+    const float upv = __shfl_down(v, RPW);
+    const float o = ((epi & MI_ACT_GELU) ? gelu(v) : silu(v)) * upv;
+    const int row0 = (g * 8 + wave) * RPW;
+    if (lane < RPW) {
+      if (epi & MI_EPI_ADD) y[row0 + lane] += o;
+      else y[row0 + lane] = o;
+      grp[it & 1][wave * RPW + lane] = o;
+    }
+    // grp alternates between two buffers: a group's buffer is written again
+    // two groups later, after every wave has passed the next group's barrier,
+    // which wave 0 reaches only once it has read this one.
+    __syncthreads();
+    if (wave == 0) quantize_group32(grp[it & 1][lane & 31], lane & 31, g, groups, xq_out, lane < 32);
+    g += gridDim.x;
+    if (g >= groups) break;
+#pragma unroll
+    for (int r = 0; r < NR; r++) {
+      const int row = (g * 8 + wave) * RPW + r % RPW;
+      un[r].load(sg.w[r / RPW] + (int64_t)row * sg.rb[r / RPW], 0, 0, 0, u);
+    }
+  }
+}
+
+int cu_count() {
+  static int cus[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cus[dev]) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cus[dev] = n;
+  }
+  return cus[dev];
+}
+
+}  // namespace
 
 bool rows_fits(int kind, int32_t cols) {
   const bool k = kind == MI_Q4_K || kind == MI_Q5_K;
@@ -61,6 +155,27 @@ int launch_q4k_glu(hipStream_t s, const void* gate, const void* up, int64_t row_
     return hip_check(hipGetLastError(), "matvec launch");
   }
   return launch_any<MI_Q4_K, true>(s, sg, rows, cols, xq, y, epi, nullptr);
+}
+
+int launch_q4k_glu_norm(hipStream_t s, const void* gate, const void* up, int64_t row_bytes, int32_t rows,
+                        int32_t cols, const float* x, const float* gain, float eps, float* y, void* xq_out) {
+  if (!q4k_glu_norm_fits(rows, cols, x, gain))
+    return fail(MI_ERR_SHAPE, "matvec: no normed GLU for %d x %d", rows, cols);
+  RowSegs sg{};
+  sg.w[0] = (const uint8_t*)gate;
+  sg.w[1] = sg.w[2] = (const uint8_t*)up;
+  sg.rb[0] = sg.rb[1] = sg.rb[2] = row_bytes;
+  sg.end[0] = sg.end[1] = sg.end[2] = rows;
+  sg.nseg = 2;
+  hipLaunchKernelGGL(glu_norm_kernel, dim3(std::min(rows / 32, cu_count())), dim3(8 * 64), 0, s, sg, cols, y,
+                     MI_EPI_NONE,
+                     NormIn{x, gain, eps}, (uint8_t*)xq_out);
+  return hip_check(hipGetLastError(), "matvec launch");
+}
+
+bool q4k_glu_norm_fits(int32_t rows, int32_t cols, const void* x, const void* gain) {
+  // 512 threads of 8 values cover 4096 columns; the row loads are float4
+  return rows % 32 == 0 && rows > 0 && rows_fits(MI_Q4_K, cols) && cols <= 4096 && !(((uintptr_t)x | (uintptr_t)gain) & 15);
 }
 
 }  // namespace mi

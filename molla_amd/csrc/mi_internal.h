@@ -70,6 +70,11 @@ int launch_q4k_qkv_rope(hipStream_t s, const RowSegs& sg, int32_t cols, const vo
 // in matvec form, each block quantizing the 32-row group it owns.
 int launch_q4k_glu(hipStream_t s, const void* gate, const void* up, int64_t row_bytes, int32_t rows,
                    int32_t cols, const void* xq, float* y, int32_t epi, void* xq_out = nullptr);
+// The same with the grouped xq_out, taking the RMSNorm of x (gain, eps)
+// itself instead of an xq input: the layer's ffn norm needs no launch.
+bool q4k_glu_norm_fits(int32_t rows, int32_t cols, const void* x, const void* gain);
+int launch_q4k_glu_norm(hipStream_t s, const void* gate, const void* up, int64_t row_bytes, int32_t rows,
+                        int32_t cols, const float* x, const float* gain, float eps, float* y, void* xq_out);
 // Batch-1 Q6_K matvec for up to 4096 columns (matvec_q6k_rows.hip).
 bool q6k_rows_fits(int32_t cols, int64_t row_bytes);
 int launch_q6k_rows(hipStream_t s, const void* w, int64_t row_bytes, int32_t rows, int32_t cols, const void* xq,

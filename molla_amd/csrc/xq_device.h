@@ -64,6 +64,111 @@ __device__ __forceinline__ void quantize_group32(float v, int lane32, int g, int
   }
 }
 
+// RMSNorm of one row folded into a matvec block, in two steps: a thread
+// first issues the loads of its 8 values of the row x and of the norm's gain
+// (norm_row_load; n <= 8 NT values, n a multiple of 32, both pointers
+// 16-byte aligned), the caller then issues its own weight loads, and only
+// then does norm_row_to_lds wait for the row.  Vector-memory loads of a wave
+// complete in issue order, so the row's loads must go out first.
+//
+// norm_row_to_lds: the NT threads normalise the row with rms_norm_kernel's
+// arithmetic (float64 sum of squares, scale = f32(1/sqrt(sum/n + eps)), x *
+// scale * gain) and write it in matvec form into the LDS `xs` (4 n bytes,
+// the planes of an xq token), byte for byte what quantize_group32 writes.
+// Thread t holds values 8t..8t+7, so a 32-value group is 4 lanes and its
+// reductions are two shuffles.  Every block sums in the same order, so every
+// block derives the same scale.  `red` is NT / 64 doubles of LDS; the step
+// ends with a barrier.
+struct NormRow {
+  float4 x0, x1, g0, g1;
+};
+
+__device__ __forceinline__ NormRow norm_row_load(const float* __restrict__ x, const float* __restrict__ gain,
+                                                 int n) {
+  const int at = min((int)threadIdx.x * 8, n - 8);
+  NormRow r;
+  r.x0 = *(const float4*)(x + at);
+  r.x1 = *(const float4*)(x + at + 4);
+  r.g0 = *(const float4*)(gain + at);
+  r.g1 = *(const float4*)(gain + at + 4);
+  return r;
+}
+
+template <int NT>
+__device__ __forceinline__ void norm_row_to_lds(const NormRow& nr, int n, float eps, uint8_t* xs, double* red) {
+#pragma clang fp contract(off)
+  const int t = threadIdx.x;
+  const int i0 = t * 8;
+  const bool live = i0 < n;
+  const float4 x0 = nr.x0, x1 = nr.x1, g0 = nr.g0, g1 = nr.g1;
+  float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+  const float g[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+  double acc = 0.0;
+#pragma unroll
+  for (int k = 0; k < 8; k++) acc += live ? (double)v[k] * (double)v[k] : 0.0;
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) acc += __shfl_xor(acc, m);
+  if ((t & 63) == 0) red[t >> 6] = acc;
+  __syncthreads();
+  double sum = 0.0;
+#pragma unroll
+  for (int i = 0; i < NT / 64; i++) sum += red[i];
+  const float scale = (float)(1.0 / sqrt(sum / (double)n + (double)eps));
+  float a = 0.0f;
+#pragma unroll
+  for (int k = 0; k < 8; k++) {
+    v[k] = v[k] * scale * g[k];
+    a = fmaxf(a, fabsf(v[k]));
+  }
+  a = fmaxf(a, __shfl_xor(a, 1));
+  a = fmaxf(a, __shfl_xor(a, 2));
+  int E;
+  (void)frexpf(a, &E);
+  const int e = (a > 0.0f) ? E - 22 : 0;
+  uint32_t w[3][2] = {{0, 0}, {0, 0}, {0, 0}};
+  int s1 = 0, s23 = 0, sx = 0;
+#pragma unroll
+  for (int k = 0; k < 8; k++) {
+    const int X = (int)rintf(ldexpf(v[k], -e));
+    const int L3 = (int)(int8_t)(X & 0xFF);
+    const int X1 = (X - L3) >> 8;
+    const int L2 = (int)(int8_t)(X1 & 0xFF);
+    const int L1 = (X1 - L2) >> 8;
+    s1 += L1;
+    s23 += L2 * 256 + L3;
+    sx += X;
+    const int sh = (k & 3) * 8;
+    w[0][k >> 2] |= ((uint32_t)L1 & 0xFFu) << sh;
+    w[1][k >> 2] |= ((uint32_t)L2 & 0xFFu) << sh;
+    w[2][k >> 2] |= ((uint32_t)L3 & 0xFFu) << sh;
+  }
+  // lanes 4q, 4q+1 hold half 0 of group q, lanes 4q+2, 4q+3 half 1
+  s1 += __shfl_xor(s1, 1);
+  s23 += __shfl_xor(s23, 1);
+  sx += __shfl_xor(sx, 1);
+  sx += __shfl_xor(sx, 2);
+  const int other1 = __shfl_xor(s1, 2);
+  const int other23 = __shfl_xor(s23, 2);
+  if (live) {
+    const int grp = i0 >> 5, k4 = t & 3, hh = k4 >> 1;
+    const int plane = (n >> 5) * 16;
+    uint8_t* e0 = xs + grp * 16 + (k4 & 1) * 8;
+#pragma unroll
+    for (int j = 0; j < 3; j++) *(uint2*)(e0 + (j * 2 + hh) * plane) = make_uint2(w[j][0], w[j][1]);
+    if (k4 == 0) {
+      const float sc = ldexpf(1.0f, e);
+      XMeta mt;
+      mt.scale = sc;
+      mt.xsum = sc * (float)sx;
+      mt.lsum1[0] = s1;
+      mt.lsum1[1] = other1;
+      *(XMeta*)(xs + 6 * plane + grp * 16) = mt;
+      *(int4*)(xs + 7 * plane + grp * 16) = make_int4(s23, other23, 0, 0);
+    }
+  }
+  __syncthreads();
+}
+
 // Plane accessors.  `xt` = token base, G = groups per token.
 struct XPlanes {
   const uint8_t* __restrict__ xt;
