@@ -283,9 +283,6 @@ static int decoder_layer(mi_stream stream, const mi_layer_desc* d, float* resid,
     // norm (plus this position's rope table), then q|k|v with the rope and
     // the cache store in its epilogue: no separate rope launch
     float* trig = (float*)(base + c.trig);
-    if ((rc = launch_rms_norm_trig(s, resid, d->attn_norm, d->width, d->eps, xq, pos, d->rope_steps,
-                                   d->rope_factors, d->rope_dim / 2, trig)))
-      return rc;
     QkvRope rp{};
     rp.qw = qw;
     rp.kvw = (int)kvw;
@@ -296,7 +293,17 @@ static int decoder_layer(mi_stream stream, const mi_layer_desc* d, float* resid,
     rp.k_cache = (__half*)k_cache;
     rp.v_cache = (__half*)v_cache;
     rp.kv_index = kv_index;
-    if ((rc = launch_q4k_qkv_rope(s, sg, d->width, xq, qkv, rp))) return rc;
+    rp.steps = d->rope_steps;
+    rp.factors = d->rope_factors;
+    if (q4k_qkv_norm_fits(d->width, d->head_dim, d->rope_dim, resid, d->attn_norm)) {
+      // the norm and the rope angles inside the q|k|v launch
+      if ((rc = launch_q4k_qkv_norm(s, sg, d->width, resid, d->attn_norm, d->eps, qkv, rp))) return rc;
+    } else {
+      if ((rc = launch_rms_norm_trig(s, resid, d->attn_norm, d->width, d->eps, xq, pos, d->rope_steps,
+                                     d->rope_factors, d->rope_dim / 2, trig)))
+        return rc;
+      if ((rc = launch_q4k_qkv_rope(s, sg, d->width, xq, qkv, rp))) return rc;
+    }
   } else {
     if ((rc = launch_rms_norm(s, resid, d->attn_norm, d->width, tokens, d->eps, nullptr, xq))) return rc;
     const bool tile_qkv = tokens > 1 && d->wq.kind == MI_Q4_K && d->wk.kind == MI_Q4_K &&

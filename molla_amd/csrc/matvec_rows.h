@@ -53,6 +53,8 @@ struct QkvRope {
   __half* k_cache;
   __half* v_cache;
   const int32_t* kv_index;  // paged: the cell of position pos[0] is kv_index[pos[0]]; null: slot pos[0]
+  const float* steps;       // qkv_norm_kernel computes (cos, sin) itself from these
+  const float* factors;     // rope_freqs.weight, or null
 };
 
 // The RMSNorm that glu_norm_kernel applies to its input row itself (the

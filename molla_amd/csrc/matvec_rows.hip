@@ -89,6 +89,101 @@ __global__ __launch_bounds__(8 * 64) void glu_norm_kernel(const RowSegs sg, int 
   }
 }
 
+// The q|k|v matvec of one decoding token with the layer's attention RMSNorm
+// folded in (Q4_K, cols <= 4096), and the rope and cache store of
+// rows_kernel<…, ROPE> in its epilogue.  A block is 12 waves of two rows
+// (one rope pair) each; the grid is at most one block per CU, each block
+// looping over 24-row groups.  The block issues the row's loads, then its
+// weight loads, then normalises the row into LDS in matvec form
+// (norm_row_to_lds) while the weights arrive.  A wave's (cos, sin) comes
+// from scalar loads of pos, steps and factors and float64 trig, as
+// rms_norm_kernel computes its table, so it never waits for weights.
+__global__ __launch_bounds__(12 * 64) void qkv_norm_kernel(const RowSegs sg, int cols, float* __restrict__ y,
+                                                           const NormIn nm, const QkvRope rp) {
+#pragma clang fp contract(off)
+  constexpr int W = 12, RPW = 2, kNT = W * 64;
+  __shared__ __align__(16) uint8_t xs[4 * 4096];
+  __shared__ double red[kNT / 64];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int rows = sg.end[sg.nseg - 1];
+  const int groups = (rows + W * RPW - 1) / (W * RPW);
+  const int units = cols >> 6;
+  const bool act = lane < units;
+  const int u = act ? lane : units - 1;
+  const int pos = rp.pos[0];
+
+  // Group g's wave rows, and whether (and which pair) the rope rotates them.
+  struct Pair {
+    int row0;
+    bool is_q, is_k, rot;
+    int pair;
+  };
+  auto pair_of = [&](int gg) __attribute__((always_inline)) {
+    Pair p;
+    p.row0 = (gg * W + wave) * RPW;  // even: a wave's two rows are one rope pair
+    p.is_q = p.row0 < rp.qw;
+    p.is_k = !p.is_q && p.row0 < rp.qw + rp.kvw;
+    const int e0 = (p.is_q ? p.row0 : p.row0 - rp.qw) % rp.head_dim;
+    p.rot = (p.is_q || p.is_k) && e0 < rp.rope_dim;
+    p.pair = p.rot ? e0 >> 1 : 0;
+    return p;
+  };
+
+  rows::XUnitRegs<false> xr;
+  UnitOf<MI_Q4_K, 1>::type un[RPW];
+  int g = blockIdx.x;
+  Pair pr = pair_of(g);
+  // the row, this group's rope step and factor, then the weights: loads
+  // complete in issue order, so nothing waited for before the compute
+  // waits for a weight
+  const NormRow nr = norm_row_load(nm.x, nm.gain, cols);
+  float step = rp.steps[pr.pair], factor = rp.factors ? rp.factors[pr.pair] : 1.0f;
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int r = 0; r < RPW; r++) un[r].load(rows::seg_row(sg, min(pr.row0 + r, rows - 1)), 0, 0, 0, u);
+  __builtin_amdgcn_sched_barrier(0);
+  norm_row_to_lds<kNT>(nr, cols, nm.eps, xs, red);
+  rows::load_x(xr, XLds{xs, 0, (cols >> 5) * 16}, u);
+  const int64_t slot = (int64_t)(rp.kv_index ? rp.kv_index[pos] : pos) * rp.kvw;
+  for (;;) {
+    // rope_theta's arithmetic on the preloaded step and factor
+    float c = 1.0f, sn = 0.0f;
+    if (pr.rot) {
+      float theta = (float)pos * step;
+      if (rp.factors) theta = theta / factor;
+      c = (float)cos((double)theta);
+      sn = (float)sin((double)theta);
+    }
+    float acc[RPW];
+#pragma unroll
+    for (int r = 0; r < RPW; r++) {
+      float a[1][1] = {{0.0f}};
+      un[r].template compute<1>(xr, u, a);
+      acc[r] = act ? a[0][0] : 0.0f;
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int r = 0; r < RPW; r++) acc[r] = wave_sum(acc[r]);
+    // rope.mojo:294 rotate_scaled, adjacent pairs: (a, b) <- (a c - b s, a s + b c)
+    const float a = acc[0], b = acc[1];
+    const float o = !pr.rot ? (lane == 0 ? a : b) : (lane == 0 ? a * c - b * sn : a * sn + b * c);
+    const int row = pr.row0 + lane;
+    if (lane < RPW && row < rows) {
+      if (pr.is_q) y[row] = o;
+      else if (pr.is_k) rp.k_cache[slot + (row - rp.qw)] = __float2half_rn(o);
+      else rp.v_cache[slot + (row - rp.qw - rp.kvw)] = __float2half_rn(o);
+    }
+    g += gridDim.x;
+    if (g >= groups) break;
+    pr = pair_of(g);
+    step = rp.steps[pr.pair];
+    factor = rp.factors ? rp.factors[pr.pair] : 1.0f;
+#pragma unroll
+    for (int r = 0; r < RPW; r++) un[r].load(rows::seg_row(sg, min(pr.row0 + r, rows - 1)), 0, 0, 0, u);
+  }
+}
+
 int cu_count() {
   static int cus[64];
   int dev = 0;
@@ -170,6 +265,21 @@ int launch_q4k_glu_norm(hipStream_t s, const void* gate, const void* up, int64_t
   hipLaunchKernelGGL(glu_norm_kernel, dim3(std::min(rows / 32, cu_count())), dim3(8 * 64), 0, s, sg, cols, y,
                      MI_EPI_NONE,
                      NormIn{x, gain, eps}, (uint8_t*)xq_out);
+  return hip_check(hipGetLastError(), "matvec launch");
+}
+
+bool q4k_qkv_norm_fits(int32_t cols, int32_t head_dim, int32_t rope_dim, const void* x, const void* gain) {
+  return q4k_qkv_rope_fits(cols, head_dim, rope_dim) && !(((uintptr_t)x | (uintptr_t)gain) & 15);
+}
+
+int launch_q4k_qkv_norm(hipStream_t s, const RowSegs& sg, int32_t cols, const float* x, const float* gain,
+                        float eps, float* q, const QkvRope& rp) {
+  if (!q4k_qkv_norm_fits(cols, rp.head_dim, rp.rope_dim, x, gain) || !rp.steps)
+    return fail(MI_ERR_SHAPE, "matvec: no normed q|k|v for %d columns, head_dim %d", cols, rp.head_dim);
+  const int rows = sg.end[sg.nseg - 1];
+  const int groups = (rows + 23) / 24;
+  hipLaunchKernelGGL(qkv_norm_kernel, dim3(std::min(groups, cu_count())), dim3(12 * 64), 0, s, sg, cols, q,
+                     NormIn{x, gain, eps}, rp);
   return hip_check(hipGetLastError(), "matvec launch");
 }
 

@@ -25,15 +25,6 @@ namespace {
 // the slowest part.  All loads are issued before any arithmetic.
 constexpr int kNormThreads = 256;
 
-// rope.mojo:253 angle with scale 1 and no YaRN mix: f32(pos) * step / freq,
-// freq being the pair's rope_freqs.weight factor (none: 1, no division).
-__device__ __forceinline__ float rope_theta(int pos, const float* __restrict__ steps,
-                                            const float* __restrict__ factors, int pair) {
-#pragma clang fp contract(off)
-  const float theta = (float)pos * steps[pair];
-  return factors ? theta / factors[pair] : theta;
-}
-
 // With `trig`, the last block also writes (cos, sin) of the angle of pair p at
 // pos[0] for p < pairs, in float64 as rope.mojo:253-285, for the layer's fused
 // q|k|v rope; it has no other use for its spare threads' time.

@@ -169,6 +169,16 @@ __device__ __forceinline__ void norm_row_to_lds(const NormRow& nr, int n, float 
   __syncthreads();
 }
 
+// rope.mojo:253 angle with scale 1 and no YaRN mix: f32(pos) * step / freq,
+// freq being the pair's rope_freqs.weight factor (none: 1, no division).
+// Shared by the norm, rope and fused q|k|v kernels.
+__device__ __forceinline__ float rope_theta(int pos, const float* __restrict__ steps,
+                                            const float* __restrict__ factors, int pair) {
+#pragma clang fp contract(off)
+  const float theta = (float)pos * steps[pair];
+  return factors ? theta / factors[pair] : theta;
+}
+
 // Plane accessors.  `xt` = token base, G = groups per token.
 struct XPlanes {
   const uint8_t* __restrict__ xt;
