@@ -94,32 +94,17 @@ __device__ __forceinline__ NormRow norm_row_load(const float* __restrict__ x, co
   return r;
 }
 
-template <int NT>
-__device__ __forceinline__ void norm_row_to_lds(const NormRow& nr, int n, float eps, uint8_t* xs, double* red) {
+// Thread t's 8 consecutive values v (of a row of n, n a multiple of 32)
+// in matvec form into the LDS `xs` (4 n bytes, the planes of an xq token),
+// byte for byte what quantize_group32 writes for them: a 32-value group is
+// 4 lanes, so its reductions are two shuffles.  Every lane of the wave takes
+// part; only `live` ones write.  No barrier.
+__device__ __forceinline__ void quantize8_to_lds(const float (&v)[8], bool live, int t, int n, uint8_t* xs) {
 #pragma clang fp contract(off)
-  const int t = threadIdx.x;
   const int i0 = t * 8;
-  const bool live = i0 < n;
-  const float4 x0 = nr.x0, x1 = nr.x1, g0 = nr.g0, g1 = nr.g1;
-  float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-  const float g[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
-  double acc = 0.0;
-#pragma unroll
-  for (int k = 0; k < 8; k++) acc += live ? (double)v[k] * (double)v[k] : 0.0;
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) acc += __shfl_xor(acc, m);
-  if ((t & 63) == 0) red[t >> 6] = acc;
-  __syncthreads();
-  double sum = 0.0;
-#pragma unroll
-  for (int i = 0; i < NT / 64; i++) sum += red[i];
-  const float scale = (float)(1.0 / sqrt(sum / (double)n + (double)eps));
   float a = 0.0f;
 #pragma unroll
-  for (int k = 0; k < 8; k++) {
-    v[k] = v[k] * scale * g[k];
-    a = fmaxf(a, fabsf(v[k]));
-  }
+  for (int k = 0; k < 8; k++) a = fmaxf(a, fabsf(v[k]));
   a = fmaxf(a, __shfl_xor(a, 1));
   a = fmaxf(a, __shfl_xor(a, 2));
   int E;
@@ -166,6 +151,31 @@ __device__ __forceinline__ void norm_row_to_lds(const NormRow& nr, int n, float 
       *(int4*)(xs + 7 * plane + grp * 16) = make_int4(s23, other23, 0, 0);
     }
   }
+}
+
+template <int NT>
+__device__ __forceinline__ void norm_row_to_lds(const NormRow& nr, int n, float eps, uint8_t* xs, double* red) {
+#pragma clang fp contract(off)
+  const int t = threadIdx.x;
+  const int i0 = t * 8;
+  const bool live = i0 < n;
+  const float4 x0 = nr.x0, x1 = nr.x1, g0 = nr.g0, g1 = nr.g1;
+  float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+  const float g[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+  double acc = 0.0;
+#pragma unroll
+  for (int k = 0; k < 8; k++) acc += live ? (double)v[k] * (double)v[k] : 0.0;
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) acc += __shfl_xor(acc, m);
+  if ((t & 63) == 0) red[t >> 6] = acc;
+  __syncthreads();
+  double sum = 0.0;
+#pragma unroll
+  for (int i = 0; i < NT / 64; i++) sum += red[i];
+  const float scale = (float)(1.0 / sqrt(sum / (double)n + (double)eps));
+#pragma unroll
+  for (int k = 0; k < 8; k++) v[k] = v[k] * scale * g[k];
+  quantize8_to_lds(v, live, t, n, xs);
   __syncthreads();
 }
 
