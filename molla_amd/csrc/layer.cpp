@@ -39,7 +39,7 @@ namespace {
 size_t up256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 struct Carve {
-  size_t xq, qkv, up, gate, attn, trig, xq2, total;
+  size_t xq, qkv, up, gate, attn, trig, xq2, part, total;
 };
 
 Carve carve(const mi_layer_desc* d, int32_t max_count, int32_t tokens) {
@@ -61,6 +61,8 @@ Carve carve(const mi_layer_desc* d, int32_t max_count, int32_t tokens) {
   at += up256(sizeof(float) * (size_t)d->rope_dim);
   c.xq2 = at;
   at += up256((size_t)xq_token_bytes(d->hidden) * tokens);
+  c.part = at;  // split-K partial sums of the down projection (batch 2..8)
+  at += tokens > 1 ? up256(q4k_tile_split_bytes(d->width, tokens)) : 0;
   c.total = at;
   return c;
 }
@@ -386,6 +388,10 @@ static int decoder_layer(mi_stream stream, const mi_layer_desc* d, float* resid,
     if ((rc = launch_q4k_tile_glu(s, d->gate.data, d->up.data, d->gate.row_bytes, d->hidden, d->width, xq, tokens,
                                   gate, d->hidden, MI_EPI_NONE, xq2)))
       return rc;
+    if (d->down.kind == MI_Q4_K && q4k_tile_split_fits(d->width, d->hidden, tokens))
+      // 128 tiles over a 14336-value K: two blocks per tile and an ordered reduce
+      return launch_q4k_tile_split(s, d->down.data, d->down.row_bytes, d->width, d->hidden, xq2, tokens, resid,
+                                   d->width, MI_EPI_ADD, nullptr, (float*)(base + c.part));
     return launch_matvec(s, d->down.kind, d->down.data, d->down.row_bytes, d->width, d->hidden, xq2, tokens,
                          resid, d->width, MI_EPI_ADD, nullptr);
   } else {

@@ -80,7 +80,10 @@ __global__ __launch_bounds__(KW * 64) void q4k_tile_kernel(const RowSegs sg, int
   wrow[0] = GLU ? sg.w[0] + (int64_t)row * sg.rb[0] : rows::seg_row(sg, row);
   if (GLU) wrow[NP - 1] = sg.w[1] + (int64_t)row * sg.rb[1];
   const int nsb = cols >> 8, G = cols >> 5;
-  const int sb0 = wave * SBW;
+  // gridDim.y > 1 splits K over blocks: block y takes waves y * ks .. of the
+  // row and writes its raw sums to y + blockIdx.y * tn * ldy (epi NONE)
+  const int sb0 = (blockIdx.y * ks + wave) * SBW;
+  if (gridDim.y > 1) y += (int64_t)blockIdx.y * tn * ldy;
   // activation offsets in 32 bits (8 tokens of 16384 values are 512 KB), so
   // each load is one base register plus a 32-bit offset
   const int tok = 4 * cols, plane = (cols >> 5) * 16;
@@ -203,6 +206,32 @@ __global__ __launch_bounds__(KW * 64) void q4k_tile_kernel(const RowSegs sg, int
   }
 }
 
+// Split-K partials in y order: out = epilogue(part[0] + part[1]) (the two K
+// halves added in that order, so the result does not depend on timing).
+__global__ void tile_split_reduce_kernel(const float* __restrict__ part, int tn, int rows, float* __restrict__ y,
+                                         int64_t ldy, int epi, const float* __restrict__ aux) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= tn * rows) return;
+  const int t = i / rows, r = i - t * rows;
+  const float v = part[i] + part[(int64_t)tn * rows + i];
+  epilogue(y, aux, epi, (int64_t)t * ldy + r, r, v);
+}
+
+template <int T, int SBW>
+int launch_split(hipStream_t s, const RowSegs& sg, int rows, int cols, int tn, const void* xq, float* y,
+                 int64_t ldy, int epi, const float* aux, float* part) {
+  const int waves = (cols / 256 + SBW - 1) / SBW;
+  const int ks = (waves + 1) / 2;
+  const size_t shm = (size_t)T * (cols / 32) * sizeof(float2);
+  hipLaunchKernelGGL((q4k_tile_kernel<T, SBW, false, kWideWaves>), dim3((rows + 31) / 32, 2), dim3(ks * 64), shm, s,
+                     sg, cols, tn, (const uint8_t*)xq, part, (int64_t)rows, MI_EPI_NONE, nullptr, nullptr);
+  int rc = hip_check(hipGetLastError(), "matvec launch");
+  if (rc) return rc;
+  hipLaunchKernelGGL(tile_split_reduce_kernel, dim3((tn * rows + 255) / 256), dim3(256), 0, s, part, tn, rows, y,
+                     ldy, epi, aux);
+  return hip_check(hipGetLastError(), "matvec split reduce");
+}
+
 template <int T, int SBW, bool GLU, int KW>
 int launch_ts(hipStream_t s, const RowSegs& sg, int rows, int cols, int tn, const void* xq, float* y, int64_t ldy,
               int epi, const float* aux, void* xq_out) {
@@ -252,6 +281,35 @@ int launch_g(hipStream_t s, const RowSegs& sg, int rows, int cols, const void* x
 }
 
 }  // namespace
+
+// K split over two blocks per 32-row tile: for matrices of few tiles and a
+// long K (the down projection: 128 tiles, 14336 values), so that all 256
+// CUs share the VALU work of the tiles instead of 128.
+bool q4k_tile_split_fits(int32_t rows, int32_t cols, int32_t tokens) {
+  const int nsb = cols / 256;
+  const int sbw = tokens > 4 ? 2 : 4;
+  return q4k_tile_fits(cols, tokens) && rows <= 4096 && nsb >= 32 && (nsb + sbw - 1) / sbw <= 2 * kWideWaves;
+}
+
+size_t q4k_tile_split_bytes(int32_t rows, int32_t tokens) { return sizeof(float) * 2 * (size_t)rows * tokens; }
+
+int launch_q4k_tile_split(hipStream_t s, const void* w, int64_t row_bytes, int32_t rows, int32_t cols,
+                          const void* xq, int32_t tokens, float* y, int64_t ldy, int32_t epi, const float* aux,
+                          float* part) {
+  if (!q4k_tile_split_fits(rows, cols, tokens))
+    return fail(MI_ERR_SHAPE, "matvec: no split-K tile for %d x %d at %d tokens", rows, cols, tokens);
+  RowSegs sg{};
+  sg.w[0] = sg.w[1] = sg.w[2] = (const uint8_t*)w;
+  sg.rb[0] = sg.rb[1] = sg.rb[2] = row_bytes;
+  sg.end[0] = sg.end[1] = sg.end[2] = rows;
+  sg.nseg = 1;
+  switch (tokens) {
+    case 2: return launch_split<2, 4>(s, sg, rows, cols, 2, xq, y, ldy, epi, aux, part);
+    case 3: return launch_split<3, 4>(s, sg, rows, cols, 3, xq, y, ldy, epi, aux, part);
+    case 4: return launch_split<4, 4>(s, sg, rows, cols, 4, xq, y, ldy, epi, aux, part);
+    default: return launch_split<8, 2>(s, sg, rows, cols, tokens, xq, y, ldy, epi, aux, part);
+  }
+}
 
 bool q4k_tile_fits(int32_t cols, int32_t tokens) {
   return tokens >= 2 && tokens <= 8 && cols % 256 == 0 && cols / 256 <= 8 * kTileWaves;

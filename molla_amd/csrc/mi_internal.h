@@ -85,6 +85,13 @@ bool q6k_rows_fits(int32_t cols, int64_t row_bytes);
 int launch_q6k_rows(hipStream_t s, const void* w, int64_t row_bytes, int32_t rows, int32_t cols, const void* xq,
                     float* y, int32_t epi, const float* aux);
 // Batched (2..8 tokens) Q4_K matvec on the matrix cores (matvec_tile.hip).
+// The tile with K split over two blocks and an ordered reduce launch
+// (part: q4k_tile_split_bytes of scratch), for few tiles over a long K.
+bool q4k_tile_split_fits(int32_t rows, int32_t cols, int32_t tokens);
+size_t q4k_tile_split_bytes(int32_t rows, int32_t tokens);
+int launch_q4k_tile_split(hipStream_t s, const void* w, int64_t row_bytes, int32_t rows, int32_t cols,
+                          const void* xq, int32_t tokens, float* y, int64_t ldy, int32_t epi, const float* aux,
+                          float* part);
 bool q4k_tile_fits(int32_t cols, int32_t tokens);
 int launch_q4k_tile(hipStream_t s, const void* w, int64_t row_bytes, int32_t rows, int32_t cols, const void* xq,
                     int32_t tokens, float* y, int64_t ldy, int32_t epi, const float* aux);

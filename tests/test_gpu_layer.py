@@ -71,6 +71,9 @@ def llama31_factors(pairs):
     ((512, 1024, 8, 2, 64), 300, 3, False),
     ((512, 1024, 8, 2, 64), 300, 3, True),
     ((4096, 14336, 32, 8, 128), 4096, 1, False),   # config 4
+    # an MLP of 8192: the batched down projection splits K over two blocks
+    ((1024, 8192, 8, 2, 128), 200, 4, False),
+    ((1024, 8192, 8, 2, 128), 200, 8, False),
 ])
 def test_layer_matches_oracle(dims, pos, tokens, factors):
     from molla_amd import block, gpu
