@@ -308,6 +308,7 @@ static int decoder_layer(mi_stream stream, const mi_layer_desc* d, float* resid,
     }
   } else {
     if ((rc = launch_rms_norm(s, resid, d->attn_norm, d->width, tokens, d->eps, nullptr, xq))) return rc;
+    bool roped = false;
     const bool tile_qkv = tokens > 1 && d->wq.kind == MI_Q4_K && d->wk.kind == MI_Q4_K &&
                           d->wv.kind == MI_Q4_K && q4k_tile_fits(d->width, tokens);
     if (fused_qkv) {
@@ -326,7 +327,26 @@ static int decoder_layer(mi_stream stream, const mi_layer_desc* d, float* resid,
       tg.end[1] = qw + (int32_t)kvw;
       tg.end[2] = qw + 2 * (int32_t)kvw;
       tg.nseg = 3;
-      if ((rc = launch_q4k_tile_segs(s, tg, d->width, xq, tokens, qkv, qkv_stride))) return rc;
+      if (!d->neox && !q8) {
+        // the rope and the f16 cache store in the tile's epilogue
+        QkvRope rp{};
+        rp.qw = qw;
+        rp.kvw = (int)kvw;
+        rp.head_dim = d->head_dim;
+        rp.rope_dim = d->rope_dim;
+        rp.pos = pos;
+        rp.k_cache = (__half*)k_cache;
+        rp.v_cache = (__half*)v_cache;
+        rp.kv_index = kv_index;
+        rp.steps = d->rope_steps;
+        rp.factors = d->rope_factors;
+        rp.cache_stride = cache_stride;
+        rp.index_stride = index_stride;
+        if ((rc = launch_q4k_tile_qkv_rope(s, tg, d->width, xq, tokens, qkv, qkv_stride, rp))) return rc;
+        roped = true;
+      } else if ((rc = launch_q4k_tile_segs(s, tg, d->width, xq, tokens, qkv, qkv_stride))) {
+        return rc;
+      }
     } else {
       if ((rc = launch_matvec(s, d->wq.kind, d->wq.data, d->wq.row_bytes, qw, d->width, xq, tokens, qkv,
                               qkv_stride, MI_EPI_NONE, nullptr)))
@@ -340,7 +360,7 @@ static int decoder_layer(mi_stream stream, const mi_layer_desc* d, float* resid,
     }
     // rotate q and k; k and v into the cache (f16, or q8_0 blocks encoded by
     // the same launch once it holds every rotated key)
-    if ((rc = launch_rope_store(s, qkv, d->heads, d->kv_heads, d->head_dim, d->rope_dim, d->neox,
+    if (!roped && (rc = launch_rope_store(s, qkv, d->heads, d->kv_heads, d->head_dim, d->rope_dim, d->neox,
                                 d->rope_steps, pos, tokens, qkv_stride, k_cache, v_cache, cache_stride,
                                 d->rope_factors, d->cache_form, kv_index, index_stride)))
       return rc;

@@ -53,8 +53,12 @@ struct QkvRope {
   __half* k_cache;
   __half* v_cache;
   const int32_t* kv_index;  // paged: the cell of position pos[0] is kv_index[pos[0]]; null: slot pos[0]
-  const float* steps;       // qkv_norm_kernel computes (cos, sin) itself from these
+  const float* steps;       // qkv_norm_kernel and the batched tile compute (cos, sin) from these
   const float* factors;     // rope_freqs.weight, or null
+  // batched tile: token t's cache row is kv_index[t * index_stride + pos[t]]
+  // (paged) or t * cache_stride + pos[t] * kvw halves (stride 0: one
+  // sequence's chunk)
+  int64_t cache_stride, index_stride;
 };
 
 // The RMSNorm that glu_norm_kernel applies to its input row itself (the

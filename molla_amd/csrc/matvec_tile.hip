@@ -60,12 +60,15 @@ constexpr int kWideWaves = 16;  // ... and for few (<= 8192 rows): more waves sp
 // gate, sg.w[1] = up, both with sg.end[0] rows; every wave walks its
 // superblocks of the gate row, then of the up row, and the block writes
 // act(gate) * up.
-template <int T, int SBW, bool GLU, int KW>
+// ROPE (q|k|v, Llama pairing, f16 cache): the epilogue rotates q and k rows
+// with each token's own position and writes q to y, k and v to the cache, as
+// rope_store_kernel does after an unrotated q|k|v; no separate launch.
+template <int T, int SBW, bool GLU, int KW, bool ROPE = false>
 __global__ __launch_bounds__(KW * 64) void q4k_tile_kernel(const RowSegs sg, int cols, int tn,
                                                                    const uint8_t* __restrict__ xq,
                                                                    float* __restrict__ y, int64_t ldy, int epi,
                                                                    const float* __restrict__ aux,
-                                                                   uint8_t* __restrict__ xq_out) {
+                                                                   uint8_t* __restrict__ xq_out, const QkvRope rp) {
   constexpr int GW = 8 / T;    // groups per window
   constexpr int NW = 8 / GW;   // windows per superblock
   constexpr int NSL = GW * T;  // slots in use
@@ -189,6 +192,34 @@ __global__ __launch_bounds__(KW * 64) void q4k_tile_kernel(const RowSegs sg, int
     float v = 0.0f;
     for (int k = 0; k < ks; k++) v += red[0][k][t][nn];
     const int r = blockIdx.x * 32 + nn;
+    if constexpr (ROPE) {
+#pragma clang fp contract(off)
+      // rope.mojo:294 rotate_scaled, adjacent pairs: (a, b) <- (a c - b s, a s + b c);
+      // the partner row is the neighbouring lane (o ^ 1, the same token)
+      const float partner = __shfl_xor(v, 1);
+      if (r >= rows) continue;
+      const int p = rp.pos[t];
+      const bool is_q = r < rp.qw, is_k = !is_q && r < rp.qw + rp.kvw;
+      float out = v;
+      if (is_q || is_k) {
+        const int e = (is_q ? r : r - rp.qw) % rp.head_dim;
+        if (e < rp.rope_dim) {
+          const float theta = rope_theta(p, rp.steps, rp.factors, e >> 1);
+          const float c = (float)cos((double)theta), sn = (float)sin((double)theta);
+          const float a = (e & 1) ? partner : v, b = (e & 1) ? v : partner;
+          out = (e & 1) ? a * sn + b * c : a * c - b * sn;
+        }
+      }
+      if (is_q) {
+        y[(int64_t)t * ldy + r] = out;
+      } else {
+        const int64_t at = rp.kv_index ? (int64_t)rp.kv_index[t * rp.index_stride + p] * rp.kvw
+                                       : (int64_t)t * rp.cache_stride + (int64_t)p * rp.kvw;
+        if (is_k) rp.k_cache[at + (r - rp.qw)] = __float2half_rn(out);
+        else rp.v_cache[at + (r - rp.qw - rp.kvw)] = __float2half_rn(out);
+      }
+      continue;
+    }
     if (r >= rows) continue;
     if constexpr (GLU) {
       float u = 0.0f;
@@ -224,7 +255,7 @@ int launch_split(hipStream_t s, const RowSegs& sg, int rows, int cols, int tn, c
   const int ks = (waves + 1) / 2;
   const size_t shm = (size_t)T * (cols / 32) * sizeof(float2);
   hipLaunchKernelGGL((q4k_tile_kernel<T, SBW, false, kWideWaves>), dim3((rows + 31) / 32, 2), dim3(ks * 64), shm, s,
-                     sg, cols, tn, (const uint8_t*)xq, part, (int64_t)rows, MI_EPI_NONE, nullptr, nullptr);
+                     sg, cols, tn, (const uint8_t*)xq, part, (int64_t)rows, MI_EPI_NONE, nullptr, nullptr, QkvRope{});
   int rc = hip_check(hipGetLastError(), "matvec launch");
   if (rc) return rc;
   hipLaunchKernelGGL(tile_split_reduce_kernel, dim3((tn * rows + 255) / 256), dim3(256), 0, s, part, tn, rows, y,
@@ -234,11 +265,18 @@ int launch_split(hipStream_t s, const RowSegs& sg, int rows, int cols, int tn, c
 
 template <int T, int SBW, bool GLU, int KW>
 int launch_ts(hipStream_t s, const RowSegs& sg, int rows, int cols, int tn, const void* xq, float* y, int64_t ldy,
-              int epi, const float* aux, void* xq_out) {
+              int epi, const float* aux, void* xq_out, const QkvRope* rp = nullptr) {
   const int ks = (cols / 256 + SBW - 1) / SBW;
   const size_t shm = (size_t)T * (cols / 32) * sizeof(float2);
+  if constexpr (!GLU) {
+    if (rp) {
+      hipLaunchKernelGGL((q4k_tile_kernel<T, SBW, false, KW, true>), dim3((rows + 31) / 32), dim3(ks * 64), shm, s,
+                         sg, cols, tn, (const uint8_t*)xq, y, ldy, MI_EPI_NONE, nullptr, nullptr, *rp);
+      return hip_check(hipGetLastError(), "matvec launch");
+    }
+  }
   hipLaunchKernelGGL((q4k_tile_kernel<T, SBW, GLU, KW>), dim3((rows + 31) / 32), dim3(ks * 64), shm, s, sg, cols, tn,
-                     (const uint8_t*)xq, y, ldy, epi, aux, (uint8_t*)xq_out);
+                     (const uint8_t*)xq, y, ldy, epi, aux, (uint8_t*)xq_out, QkvRope{});
   return hip_check(hipGetLastError(), "matvec launch");
 }
 
@@ -246,7 +284,7 @@ int launch_ts(hipStream_t s, const RowSegs& sg, int rows, int cols, int tn, cons
 // are live and the rest of the slots stay empty.
 template <int T, bool GLU>
 int launch_t(hipStream_t s, const RowSegs& sg, int rows, int cols, int tn, const void* xq, float* y,
-             int64_t ldy, int epi, const float* aux, void* xq_out) {
+             int64_t ldy, int epi, const float* aux, void* xq_out, const QkvRope* rp = nullptr) {
   const int nsb = cols / 256;
   // Few tiles (a 4096-row matrix is 128 blocks for 256 CUs): up to 16 waves
   // per block split K, so the whole chip streams.
@@ -254,28 +292,28 @@ int launch_t(hipStream_t s, const RowSegs& sg, int rows, int cols, int tn, const
   // only one superblock per wave, the 8-token plain form two.)
   constexpr int kWideSbw = T == 8 ? (GLU ? 1 : 2) : 4;
   if (rows <= 8192 && nsb <= kWideSbw * kWideWaves) {
-    if (nsb <= kWideWaves) return launch_ts<T, 1, GLU, kWideWaves>(s, sg, rows, cols, tn, xq, y, ldy, epi, aux, xq_out);
+    if (nsb <= kWideWaves) return launch_ts<T, 1, GLU, kWideWaves>(s, sg, rows, cols, tn, xq, y, ldy, epi, aux, xq_out, rp);
     if constexpr (kWideSbw >= 2)
       if (nsb <= 2 * kWideWaves)
-        return launch_ts<T, 2, GLU, kWideWaves>(s, sg, rows, cols, tn, xq, y, ldy, epi, aux, xq_out);
-    if constexpr (kWideSbw >= 4) return launch_ts<T, 4, GLU, kWideWaves>(s, sg, rows, cols, tn, xq, y, ldy, epi, aux, xq_out);
+        return launch_ts<T, 2, GLU, kWideWaves>(s, sg, rows, cols, tn, xq, y, ldy, epi, aux, xq_out, rp);
+    if constexpr (kWideSbw >= 4) return launch_ts<T, 4, GLU, kWideWaves>(s, sg, rows, cols, tn, xq, y, ldy, epi, aux, xq_out, rp);
   }
-  if (nsb <= 2 * kTileWaves) return launch_ts<T, 2, GLU, kTileWaves>(s, sg, rows, cols, tn, xq, y, ldy, epi, aux, xq_out);
-  if (nsb <= 4 * kTileWaves) return launch_ts<T, 4, GLU, kTileWaves>(s, sg, rows, cols, tn, xq, y, ldy, epi, aux, xq_out);
-  return launch_ts<T, 8, GLU, kTileWaves>(s, sg, rows, cols, tn, xq, y, ldy, epi, aux, xq_out);
+  if (nsb <= 2 * kTileWaves) return launch_ts<T, 2, GLU, kTileWaves>(s, sg, rows, cols, tn, xq, y, ldy, epi, aux, xq_out, rp);
+  if (nsb <= 4 * kTileWaves) return launch_ts<T, 4, GLU, kTileWaves>(s, sg, rows, cols, tn, xq, y, ldy, epi, aux, xq_out, rp);
+  return launch_ts<T, 8, GLU, kTileWaves>(s, sg, rows, cols, tn, xq, y, ldy, epi, aux, xq_out, rp);
 }
 
 template <bool GLU>
 int launch_g(hipStream_t s, const RowSegs& sg, int rows, int cols, const void* xq, int tokens, float* y,
-             int64_t ldy, int epi, const float* aux, void* xq_out = nullptr) {
+             int64_t ldy, int epi, const float* aux, void* xq_out = nullptr, const QkvRope* rp = nullptr) {
   switch (tokens) {
-    case 2: return launch_t<2, GLU>(s, sg, rows, cols, 2, xq, y, ldy, epi, aux, xq_out);
-    case 3: return launch_t<3, GLU>(s, sg, rows, cols, 3, xq, y, ldy, epi, aux, xq_out);
-    case 4: return launch_t<4, GLU>(s, sg, rows, cols, 4, xq, y, ldy, epi, aux, xq_out);
+    case 2: return launch_t<2, GLU>(s, sg, rows, cols, 2, xq, y, ldy, epi, aux, xq_out, rp);
+    case 3: return launch_t<3, GLU>(s, sg, rows, cols, 3, xq, y, ldy, epi, aux, xq_out, rp);
+    case 4: return launch_t<4, GLU>(s, sg, rows, cols, 4, xq, y, ldy, epi, aux, xq_out, rp);
     case 5:
     case 6:
     case 7:
-    case 8: return launch_t<8, GLU>(s, sg, rows, cols, tokens, xq, y, ldy, epi, aux, xq_out);
+    case 8: return launch_t<8, GLU>(s, sg, rows, cols, tokens, xq, y, ldy, epi, aux, xq_out, rp);
   }
   return fail(MI_ERR_ARG, "matvec: tokens %d outside 2..8 for the batched tile", tokens);
 }
@@ -328,6 +366,13 @@ int launch_q4k_tile(hipStream_t s, const void* w, int64_t row_bytes, int32_t row
 int launch_q4k_tile_segs(hipStream_t s, const RowSegs& sg, int32_t cols, const void* xq, int32_t tokens, float* y,
                          int64_t ldy) {
   return launch_g<false>(s, sg, sg.end[sg.nseg - 1], cols, xq, tokens, y, ldy, MI_EPI_NONE, nullptr);
+}
+
+int launch_q4k_tile_qkv_rope(hipStream_t s, const RowSegs& sg, int32_t cols, const void* xq, int32_t tokens,
+                             float* q, int64_t ldq, const QkvRope& rp) {
+  if (rp.head_dim % 2 || rp.rope_dim % 2 || !rp.steps || !rp.pos)
+    return fail(MI_ERR_SHAPE, "matvec: no fused rope for head_dim %d, rope_dim %d", rp.head_dim, rp.rope_dim);
+  return launch_g<false>(s, sg, sg.end[sg.nseg - 1], cols, xq, tokens, q, ldq, MI_EPI_NONE, nullptr, nullptr, &rp);
 }
 
 int launch_q4k_tile_glu(hipStream_t s, const void* gate, const void* up, int64_t row_bytes, int32_t rows,

@@ -86,6 +86,10 @@ int launch_q6k_rows(hipStream_t s, const void* w, int64_t row_bytes, int32_t row
                     float* y, int32_t epi, const float* aux);
 // Batched (2..8 tokens) Q4_K matvec on the matrix cores (matvec_tile.hip).
 // The tile with K split over two blocks and an ordered reduce launch
+// q|k|v on the tile with the rope and the f16 cache store in its epilogue
+// (Llama pairing): q rotated into q (row stride ldq), k and v into the cache.
+int launch_q4k_tile_qkv_rope(hipStream_t s, const RowSegs& sg, int32_t cols, const void* xq, int32_t tokens,
+                             float* q, int64_t ldq, const QkvRope& rp);
 // (part: q4k_tile_split_bytes of scratch), for few tiles over a long K.
 bool q4k_tile_split_fits(int32_t rows, int32_t cols, int32_t tokens);
 size_t q4k_tile_split_bytes(int32_t rows, int32_t tokens);
