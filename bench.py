@@ -23,6 +23,9 @@ batch 1 over a q8_0 KV cache, `batch_1_q8_cache`), each
 step replayed from one captured HIP graph; tokens/s, ms per step, the eager
 (host-launched) ms per step and the weight-streaming fraction of 8 TB/s.
 
+"head" (with the batched lines): config 3, the Q6_K 128256 x 4096 output
+head at batch 1 and 8 and the argmax after it.
+
 "prefill" (skipped with --no-prefill): the prefill matmul at a 256-token
 chunk on each matrix of an 8B Q4_K_M layer (TFLOP/s, matrix-core fraction)
 and the matmul-only tokens/s of an 8B prefill.
@@ -149,6 +152,7 @@ def main():
     if not args.no_batched:
         line["batched"] = _batched(L, h, kind, ws, copies, rb, stream)
         line["kinds"] = _kinds(L, h, stream)
+        line["head"] = _head(L, h, stream)
     if not args.no_cpu:
         line["cpu_baseline"] = _cpu_baseline(base, kind, rb, x)
     if not args.no_prefill:
@@ -253,6 +257,48 @@ def _batched(L, h, kind, ws, copies, rb, stream, reps=100):
                                    "frac_hbm_peak": round(algo / us / 1e3 / PEAK_GBS, 4),
                                    "mfma_int8_TOPs": round(ops / us / 1e6, 2),
                                    "mfma_util_of_5POPs": round(ops / us / 1e6 / 5000.0, 5)}
+    return out
+
+
+def _head(L, h, stream, reps=20):
+    """Config 3: the Q6_K output head, 128256 x 4096, at batch 1 and 8, then
+    argmax.  The weights (431 MB) are larger than the 256 MB Infinity Cache,
+    so every launch streams them from HBM."""
+    import torch
+
+    from molla_amd import gpu, synth
+    from molla_amd._lib import check
+
+    rows, cols, kind = 128256, 4096, gpu.Q_Q6_K
+    rb = gpu.row_bytes(kind, cols)
+    w = synth.quant_tensor(kind, rows, cols, 79, device="cuda")
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    out = {}
+    for tokens in (1, 8):
+        x = synth.normal(tokens * cols, 23 + tokens, device="cuda")
+        xq = torch.empty(L.mi_matvec_workspace(cols, tokens), dtype=torch.uint8, device="cuda")
+        y = torch.empty(tokens * rows, dtype=torch.float32, device="cuda")
+        picks = torch.empty(tokens, dtype=torch.int32, device="cuda")
+        check(L.mi_quantize(h, x.data_ptr(), cols, tokens, xq.data_ptr()))
+
+        def timed(fn):
+            for _ in range(3):
+                fn()
+            torch.cuda.synchronize()
+            e0.record(stream)
+            for _ in range(reps):
+                fn()
+            e1.record(stream)
+            torch.cuda.synchronize()
+            return e0.elapsed_time(e1) * 1e3 / reps
+
+        us = timed(lambda: check(L.mi_matvec_xq(h, kind, w.data_ptr(), rb, rows, cols, xq.data_ptr(), tokens,
+                                                y.data_ptr(), 0, None)))
+        am = timed(lambda: check(L.mi_argmax(h, y.data_ptr(), rows, tokens, picks.data_ptr())))
+        gbs = rows * rb / us / 1e3
+        out[f"tokens_{tokens}"] = {"logits_us": round(us, 2), "GB_s": round(gbs, 1),
+                                   "frac_hbm_peak": round(gbs / PEAK_GBS, 4), "argmax_us": round(am, 2)}
     return out
 
 

@@ -94,7 +94,12 @@ struct Q6Meta {
   int l1[2], l23[2];
 };
 
-template <int T, int SBW>
+// STAGE: the block first copies every token's activation limbs (3 cols bytes
+// a token) into LDS, and the group loop reads them from there.  A wave's
+// vector loads complete in issue order, so a limb load issued in the group
+// loop, after the weight loads of the superblocks ahead, would wait for those
+// weights too; from LDS it waits for nothing.
+template <int T, int SBW, bool STAGE>
 __global__ __launch_bounds__(kQ6Waves * 64) void q6k_tile_kernel(const uint8_t* __restrict__ w, int64_t rb,
                                                                  int rows, int cols, const uint8_t* __restrict__ xq,
                                                                  float* __restrict__ y, int64_t ldy, int epi,
@@ -111,6 +116,26 @@ __global__ __launch_bounds__(kQ6Waves * 64) void q6k_tile_kernel(const uint8_t* 
   const int nsb = cols >> 8, G = cols >> 5;
   const int sb0 = wave * SBW;
   const int tok = 4 * cols, plane = (cols >> 5) * 16;
+  uint8_t* xs = (uint8_t*)(meta6 + T * G);  // STAGE: [T][3 cols] limb bytes
+  if constexpr (STAGE) {
+    // all of a thread's loads first, clamped (a duplicate store of the last
+    // vector is harmless), then the stores
+    const int per_tok = 3 * cols / 16, total = T * per_tok;
+    for (int base = 0; base < total; base += 8 * (int)blockDim.x) {
+      uint4 v[8];
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        const int i = min(base + j * (int)blockDim.x + (int)threadIdx.x, total - 1);
+        const int t = i / per_tok;
+        v[j] = *(const uint4*)(xq + (uint32_t)(t * tok + (i - t * per_tok) * 16));
+      }
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        const int i = min(base + j * (int)blockDim.x + (int)threadIdx.x, total - 1);
+        ((uint4*)xs)[i] = v[j];
+      }
+    }
+  }
 
   Q6Lane wl[2];
   q6_load(wl[0], wrow + (int64_t)min(sb0, nsb - 1) * 210, kh);
@@ -174,7 +199,9 @@ __global__ __launch_bounds__(kQ6Waves * 64) void q6k_tile_kernel(const uint8_t* 
       for (int c = 0; c < NC; c++) {
         const int tt = c * TC + a_t;
         uint4 av = make_uint4(0, 0, 0, 0);
-        if (a_live && tt < T) av = ld16(xq + (uint32_t)(tt * tok + a_off + gabs * 16));
+        if (a_live && tt < T)
+          av = STAGE ? *(const uint4*)(xs + tt * 3 * cols + a_off + gabs * 16)
+                     : ld16(xq + (uint32_t)(tt * tok + a_off + gabs * 16));
         v16i C = {};
         C = __builtin_amdgcn_mfma_i32_32x32x32_i8(as_v4i(av.x, av.y, av.z, av.w), as_v4i(bq[0], bq[1], bq[2], bq[3]),
                                                   C, 0, 0, 0);
@@ -225,13 +252,30 @@ __global__ __launch_bounds__(kQ6Waves * 64) void q6k_tile_kernel(const uint8_t* 
   }
 }
 
+// Dynamic LDS the staged form may take (the static part, red, is 8 KB at most).
+constexpr size_t kQ6StageLds = 144 * 1024;
+
 template <int T, int SBW>
 int launch_ts(hipStream_t s, const void* w, int64_t rb, int rows, int cols, const void* xq, float* y, int64_t ldy,
               int epi, const float* aux) {
   const int ks = (cols / 256 + SBW - 1) / SBW;
-  const size_t shm = (size_t)T * (cols / 32) * sizeof(Q6Meta);
-  hipLaunchKernelGGL((q6k_tile_kernel<T, SBW>), dim3((rows + 31) / 32), dim3(ks * 64), shm, s, (const uint8_t*)w,
-                     rb, rows, cols, (const uint8_t*)xq, y, ldy, epi, aux);
+  const size_t meta = (size_t)T * (cols / 32) * sizeof(Q6Meta);
+  const size_t staged = meta + (size_t)T * 3 * cols;
+  if (staged <= kQ6StageLds) {
+    static bool attr = false;  // once per instantiation: allow more than 64 KB
+    if (!attr) {
+      int rc = hip_check(hipFuncSetAttribute((const void*)q6k_tile_kernel<T, SBW, true>,
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)kQ6StageLds),
+                         "q6k tile LDS attribute");
+      if (rc) return rc;
+      attr = true;
+    }
+    hipLaunchKernelGGL((q6k_tile_kernel<T, SBW, true>), dim3((rows + 31) / 32), dim3(ks * 64), staged, s,
+                       (const uint8_t*)w, rb, rows, cols, (const uint8_t*)xq, y, ldy, epi, aux);
+  } else {
+    hipLaunchKernelGGL((q6k_tile_kernel<T, SBW, false>), dim3((rows + 31) / 32), dim3(ks * 64), meta, s,
+                       (const uint8_t*)w, rb, rows, cols, (const uint8_t*)xq, y, ldy, epi, aux);
+  }
   return hip_check(hipGetLastError(), "matvec launch");
 }
 
