@@ -117,6 +117,44 @@ def test_layer_matches_oracle(dims, pos, tokens, factors):
         assert np.allclose(got_v[t, pos], vr[pos], rtol=2e-3, atol=1e-3)
 
 
+def test_layer_unaligned_residual_runs_separate_norms():
+    """A residual row that is not 16-byte aligned makes the batch-1 layer run
+    both norms as launches of their own (the kernels with the norm folded in
+    load the row as float4): the same result as the aligned call, and the
+    oracle's."""
+    from molla_amd import block, gpu
+    ctx = gpu.DeviceContext(0)
+    spec = spec_of(512, 1024, 8, 2, 64)
+    host = make_layer_weights(spec, 9)
+    bs, layer = device_layer_from(host, spec)
+    kvw, pos = bs.kv_width(), 300
+    count = pos + 1
+    keys16 = synth.normal(count * kvw, 43).half()
+    vals16 = synth.normal(count * kvw, 44).half()
+    x = synth.normal(bs.width, 45).numpy()
+    posd = torch.full((1,), pos, dtype=torch.int32, device="cuda")
+    outs = []
+    for offset in (0, 1):
+        buf = torch.zeros(bs.width + 4, device="cuda")
+        xd = buf[offset:offset + bs.width]
+        xd.copy_(torch.from_numpy(x))
+        assert (xd.data_ptr() % 16 != 0) == (offset == 1)
+        kd, vd = keys16.clone().cuda(), vals16.clone().cuda()
+        block.device_layer(ctx, layer, xd, kd, vd, count * kvw, posd, count, 1)
+        ctx.synchronize()
+        outs.append((xd.cpu().numpy().astype(np.float64), kd.cpu().float().numpy(), vd.cpu().float().numpy()))
+    xr = x.copy()
+    kr = keys16.float().numpy().copy()
+    vr = vals16.float().numpy().copy()
+    keep = []
+    oracle.layer_step(oracle.make_layer(spec, host, keep), xr, kr, vr, pos, pos, f16_store=True, threads=8)
+    peak = np.abs(xr).max()
+    for got_x, got_k, got_v in outs:
+        assert np.abs(got_x - xr).max() <= 1e-4 * peak
+        assert np.allclose(got_k, kr, rtol=2e-3, atol=1e-3) and np.allclose(got_v, vr, rtol=2e-3, atol=1e-3)
+    assert np.abs(outs[0][0] - outs[1][0]).max() <= 1e-5 * peak
+
+
 def test_small_model_greedy_decode_matches_oracle():
     """A 2-layer model decodes 12 tokens greedily; every logit row within
     2e-3 of the peak and every pick identical (tests/test_gpu_block.mojo:1407)."""
