@@ -262,14 +262,10 @@ int launch_ts(hipStream_t s, const void* w, int64_t rb, int rows, int cols, cons
   const size_t meta = (size_t)T * (cols / 32) * sizeof(Q6Meta);
   const size_t staged = meta + (size_t)T * 3 * cols;
   if (staged <= kQ6StageLds) {
-    static bool attr = false;  // once per instantiation: allow more than 64 KB
-    if (!attr) {
-      int rc = hip_check(hipFuncSetAttribute((const void*)q6k_tile_kernel<T, SBW, true>,
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)kQ6StageLds),
-                         "q6k tile LDS attribute");
-      if (rc) return rc;
-      attr = true;
-    }
+    static bool done[kMaxDevices];  // more than 64 KB has to be asked for
+    if (int rc = allow_lds((const void*)q6k_tile_kernel<T, SBW, true>, (int)kQ6StageLds, done,
+                           "q6k tile LDS attribute"))
+      return rc;
     hipLaunchKernelGGL((q6k_tile_kernel<T, SBW, true>), dim3((rows + 31) / 32), dim3(ks * 64), staged, s,
                        (const uint8_t*)w, rb, rows, cols, (const uint8_t*)xq, y, ldy, epi, aux);
   } else {

@@ -43,6 +43,11 @@ struct XMeta {
 // ---- error state (shim.cpp) ----------------------------------------------
 int fail(int code, const char* fmt, ...);
 int hip_check(hipError_t e, const char* what);
+// Raises fn's dynamic-LDS limit to `bytes` on the current device, once per
+// device (the attribute belongs to the device's copy of the kernel); `done`
+// is the call site's own kMaxDevices flags.
+constexpr int kMaxDevices = 64;
+int allow_lds(const void* fn, int bytes, bool* done, const char* what);
 
 // ---- launchers (no validation beyond what the kernel itself assumes; the
 // ---- C-ABI layer in shim.cpp checks shapes before calling these) ----------

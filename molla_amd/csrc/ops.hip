@@ -994,13 +994,13 @@ int launch_attend(hipStream_t s, const float* q, int64_t q_stride, const uint16_
     // a prefill chunk: the matrix-core slice kernel, then the same merge
     dim3 cgrid(chunks, kv_heads, (tokens + 64 / group - 1) / (64 / group));
     const size_t lds = attn_chunk_lds_bytes(head_dim);
-    // more than 64 KB of dynamic LDS has to be asked for, once per kernel
+    // more than 64 KB of dynamic LDS has to be asked for, once per kernel and device
 #define MI_CHUNK(G, DD)                                                                                        \
   {                                                                                                            \
-    static const hipError_t big = hipFuncSetAttribute((const void*)attend_chunk_kernel<G, DD>,                \
-                                                      hipFuncAttributeMaxDynamicSharedMemorySize,             \
-                                                      (int)attn_chunk_lds_bytes(DD));                         \
-    if (big != hipSuccess) return hip_check(big, "attend_chunk LDS size");                                    \
+    static bool done[kMaxDevices];                                                                            \
+    if (int rc = allow_lds((const void*)attend_chunk_kernel<G, DD>, (int)attn_chunk_lds_bytes(DD), done,      \
+                           "attend_chunk LDS size"))                                                          \
+      return rc;                                                                                              \
     hipLaunchKernelGGL((attend_chunk_kernel<G, DD>), cgrid, dim3(256), lds, s, q, q_stride,                    \
                        (const __half*)k_cache, (const __half*)v_cache, heads, kv_heads, scale, pos_dev, chunks, \
                        part_acc, part_ml, kv_index, tokens);                                                   \

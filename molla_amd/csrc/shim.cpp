@@ -27,6 +27,17 @@ int hip_check(hipError_t e, const char* what) {
   return fail(MI_ERR_DEVICE, "%s: %s", what, hipGetErrorString(e));
 }
 
+int allow_lds(const void* fn, int bytes, bool* done, const char* what) {
+  int dev = 0;
+  int rc = hip_check(hipGetDevice(&dev), what);
+  if (rc) return rc;
+  if (dev < 0 || dev >= kMaxDevices) return fail(MI_ERR_DEVICE, "%s: device %d beyond %d", what, dev, kMaxDevices);
+  if (done[dev]) return MI_OK;
+  rc = hip_check(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, bytes), what);
+  if (!rc) done[dev] = true;
+  return rc;
+}
+
 static bool quant_kind(int kind) {
   return kind == MI_Q4_0 || kind == MI_Q4_1 || kind == MI_Q5_0 || kind == MI_Q5_1 || kind == MI_Q8_0 ||
          kind == MI_Q4_K || kind == MI_Q5_K || kind == MI_Q6_K;
