@@ -143,7 +143,7 @@ def main():
                    "rows": ROWS, "cols": COLS, "tokens": 1, "weight_bytes": wbytes,
                    "algorithmic_bytes_per_step": algo, "parallelism": "single GPU"},
         "pct_of_hbm_peak": round(100 * value / PEAK_GBS, 1),
-        "roofline": {"bound": "hbm", "kernel": "q4k_rows_kernel<4,1> (matvec_rows.h)",
+        "roofline": {"bound": "hbm", "kernel": "rows_kernel<Q4_K, 4, 1> (matvec_rows.h)",
                      "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / PEAK_GBS, 4), "traffic": _traffic_from_profile(),
                      "kernel_avg_us": round(k_avg_ms * 1e3, 3)},
