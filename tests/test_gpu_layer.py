@@ -74,6 +74,11 @@ def llama31_factors(pairs):
     # an MLP of 8192: the batched down projection splits K over two blocks
     ((1024, 8192, 8, 2, 128), 200, 4, False),
     ((1024, 8192, 8, 2, 128), 200, 8, False),
+    # full multi-head attention: a q|k|v of 12288 rows is more 24-row groups
+    # than CUs, so the folded-norm q|k|v kernel loops (rope step and factor
+    # reloaded per group)
+    ((4096, 1024, 32, 32, 128), 50, 1, False),
+    ((4096, 1024, 32, 32, 128), 50, 1, True),
 ])
 def test_layer_matches_oracle(dims, pos, tokens, factors):
     from molla_amd import block, gpu
