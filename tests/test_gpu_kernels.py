@@ -147,6 +147,39 @@ def test_matvec_epilogues(ctx, kind):
     assert (o[:7] == 0).all() and np.abs(o[7:] - dot).max() <= tol
 
 
+@pytest.mark.parametrize("kind", [oracle.Q4_K, oracle.Q6_K])
+@pytest.mark.parametrize("tokens", [5, 6, 7, 8])
+def test_matmul_tokens_epilogues(ctx, kind, tokens):
+    """Batches of 5..8 tokens with every epilogue.  Above four tokens the Q6_K
+    tile makes two passes over the weights (3 + 2 .. 4 + 4 tokens), the second
+    with the tokens' activation, output and GLU aux moved along and a bias
+    (one value a row) not."""
+    from molla_amd import gpu
+    rows, cols = 260, 1024
+    blob = synth.quant_tensor(kind, rows, cols, 130 + kind + tokens).numpy()
+    x = synth.normal(tokens * cols, 131 + tokens).numpy()
+    dot = oracle.matvec(kind, blob, rows, cols, x.reshape(tokens, cols), threads=8).astype(np.float64)
+    dot = dot.reshape(tokens, rows)
+    w = upload(blob, kind, cols, rows)
+    dx = torch.from_numpy(x).cuda()
+    bias = synth.normal(rows, 132).numpy()
+    gate_aux = synth.normal(tokens * rows, 133).numpy()
+    base = synth.normal(tokens * rows, 134).numpy()
+    tol = 1e-5 * np.abs(dot).max() + 1e-4 * np.abs(dot)
+
+    def run(epi, aux=None, start=None):
+        out = torch.from_numpy(start.copy()).cuda() if start is not None else torch.zeros(tokens * rows, device="cuda")
+        gpu.device_matmul_into(ctx, w, dx, out, tokens, epi=epi, aux=None if aux is None else torch.from_numpy(aux).cuda())
+        ctx.synchronize()
+        return out.cpu().numpy().reshape(tokens, rows)
+
+    assert (np.abs(run(gpu.EPI_NONE) - dot) <= tol).all()
+    assert (np.abs(run(gpu.EPI_BIAS, bias) - (dot + bias[None, :])) <= tol).all()
+    assert (np.abs(run(gpu.EPI_ADD, start=base) - (dot + base.reshape(tokens, rows))) <= tol).all()
+    silu = dot / (1.0 + np.exp(-np.clip(dot, -80, 80)))
+    assert (np.abs(run(gpu.EPI_GLU, gate_aux) - silu * gate_aux.reshape(tokens, rows)) <= 4 * tol + 1e-6).all()
+
+
 @pytest.mark.parametrize("kind,rows,cols,tokens", [
     (oracle.Q8_0, 4864, 896, 1),        # config 1
     (oracle.Q4_K, 14336, 4096, 1),      # config 2 gate/up
