@@ -396,25 +396,7 @@ def _decode(ctx, args):
     spec = block.BlockSpec()
     vocab = 128256
     dev = "cuda"
-    steps = torch.from_numpy(gpu.rope_steps(spec.rope_dim, spec.rope_base)).to(dev)
-    layers = []
-    seed = 1000
-    qw, kvw = spec.q_width(), spec.kv_width()
-    shapes = {"wq": (qw, spec.width), "wk": (kvw, spec.width), "wv": (kvw, spec.width), "wo": (spec.width, qw),
-              "gate": (spec.hidden, spec.width), "up": (spec.hidden, spec.width), "down": (spec.width, spec.hidden)}
-    for li in range(32):
-        ws = {}
-        for n, (r, c) in shapes.items():
-            seed += 1
-            ws[n] = gpu.Tensor.from_bytes(synth.quant_tensor(gpu.Q_Q4_K, r, c, seed, device=dev), gpu.Q_Q4_K, c, r)
-        an = synth.normal(spec.width, seed + 7, device=dev, mean=1.0, std=0.1)
-        fn = synth.normal(spec.width, seed + 8, device=dev, mean=1.0, std=0.1)
-        layers.append(block.DeviceLayer(spec, an, fn, ws, steps))
-    emb = synth.normal(vocab * spec.width, 77, device=dev).view(vocab, spec.width)
-    onorm = synth.normal(spec.width, 78, device=dev, mean=1.0, std=0.1)
-    head = gpu.Tensor.from_bytes(synth.quant_tensor(gpu.Q_Q6_K, vocab, spec.width, 79, device=dev), gpu.Q_Q6_K,
-                                 spec.width, vocab)
-    model = block.DeviceModel(spec, emb, layers, onorm, head)
+    model = block.synthetic_model(spec, 32, vocab, device=dev)
     wb = model.weight_bytes()
     out = {"metric": "8B Q4_K decode tokens/sec", "prompt": args.prompt, "generated": args.decode_tokens,
            "weight_bytes_per_step": wb}

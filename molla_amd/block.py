@@ -141,6 +141,38 @@ class DeviceModel:
         return sum(l.weight_bytes() for l in self.layers) + self.output.rows * self.output.row_bytes()
 
 
+LAYER_SHAPES = ("wq", "wk", "wv", "wo", "gate", "up", "down")
+
+
+def synthetic_model(spec: BlockSpec, n_layers: int, vocab: int, kind: int = gpu.Q_Q4_K, head_kind: int = gpu.Q_Q6_K,
+                    seed: int = 1000, device="cuda") -> DeviceModel:
+    """The seeded synthetic Llama of the benchmark's decode config: every
+    projection of `kind` (synth.quant_tensor: the config's block
+    distributions), gains N(1, 0.1), an f32 N(0, 1) embedding and a
+    `head_kind` output head.  Tensors are generated on `device` from
+    per-tensor seeds, so the same call gives the same bytes every time."""
+    from . import synth
+
+    steps = torch.from_numpy(gpu.rope_steps(spec.rope_dim, spec.rope_base)).to(device)
+    qw, kvw = spec.q_width(), spec.kv_width()
+    shapes = {"wq": (qw, spec.width), "wk": (kvw, spec.width), "wv": (kvw, spec.width), "wo": (spec.width, qw),
+              "gate": (spec.hidden, spec.width), "up": (spec.hidden, spec.width), "down": (spec.width, spec.hidden)}
+    layers = []
+    for _ in range(n_layers):
+        ws = {}
+        for n, (r, c) in shapes.items():
+            seed += 1
+            ws[n] = gpu.Tensor.from_bytes(synth.quant_tensor(kind, r, c, seed, device=device), kind, c, r)
+        an = synth.normal(spec.width, seed + 7, device=device, mean=1.0, std=0.1)
+        fn = synth.normal(spec.width, seed + 8, device=device, mean=1.0, std=0.1)
+        layers.append(DeviceLayer(spec, an, fn, ws, steps))
+    emb = synth.normal(vocab * spec.width, 77, device=device).view(vocab, spec.width)
+    onorm = synth.normal(spec.width, 78, device=device, mean=1.0, std=0.1)
+    head = gpu.Tensor.from_bytes(synth.quant_tensor(head_kind, vocab, spec.width, 79, device=device), head_kind,
+                                 spec.width, vocab)
+    return DeviceModel(spec, emb, layers, onorm, head)
+
+
 class DeviceSession:
     """KV caches and scratch for `batch` sequences decoding together
     (engine/device.mojo:194 DeviceKvCache + :809 DeviceSession)."""

@@ -1,0 +1,110 @@
+"""A float64 numpy decoder layer, written from block.mojo:319-482 as prose.
+
+Test infrastructure shared by the oracle's own tests (tests/test_oracle_layer.py)
+and the GPU layer tests: weights are dequantized by tests/npquant.py (not the
+oracle), products are float64, rope angles come from float64 powers
+(rope.mojo:253 angle with its frequency factor).  `layer64` can also return the
+intermediates a per-element error bound needs (the attention output that
+feeds wo and the gated activation that feeds down).
+"""
+
+import numpy as np
+
+import oracle
+from tests import npquant
+
+F32 = np.float32
+
+
+def rope64(x, heads, head_dim, rope_dim, base, neox, pos, factors):
+    """rope.mojo:253 angle / :294 rotate_scaled in float64: the angle of pair
+    p is pos * base^(-2p/rope_dim) / factor[p]; elements past rope_dim stay."""
+    x = x.reshape(heads, head_dim).copy()
+    pairs = rope_dim // 2
+    p = np.arange(pairs, dtype=np.float64)
+    theta = pos * base ** (-2.0 * p / rope_dim)
+    if factors is not None:
+        theta = theta / np.asarray(factors[:pairs], np.float64)
+    c, s = np.cos(theta), np.sin(theta)
+    if neox:
+        lo, hi = p.astype(int), p.astype(int) + pairs
+    else:
+        lo, hi = 2 * p.astype(int), 2 * p.astype(int) + 1
+    a, b = x[:, lo].copy(), x[:, hi].copy()
+    x[:, lo] = a * c - b * s
+    x[:, hi] = a * s + b * c
+    return x.reshape(-1)
+
+
+def rms64(x, gain, eps):
+    return x / np.sqrt(np.mean(x * x) + eps) * gain
+
+
+def attend64(q, keys, values, count, heads, kv_heads, head_dim, scale, interleave=False):
+    group = heads // kv_heads
+    K = keys.reshape(-1, kv_heads * head_dim)[:count].reshape(count, kv_heads, head_dim)
+    V = values.reshape(-1, kv_heads * head_dim)[:count].reshape(count, kv_heads, head_dim)
+    out = np.zeros((heads, head_dim))
+    for h in range(heads):
+        kh = h % kv_heads if interleave else h // group
+        s = K[:, kh, :] @ q[h * head_dim:(h + 1) * head_dim] * scale
+        p = np.exp(s - s.max())
+        out[h] = (p / p.sum()) @ V[:, kh, :]
+    return out.reshape(-1)
+
+
+def dq(w):
+    kind, rows, cols, blob = w
+    if kind == oracle.F32:
+        return np.ascontiguousarray(blob).view(F32).reshape(rows, cols).astype(np.float64)
+    return npquant.dequant(kind, blob, rows * cols).reshape(rows, cols).astype(np.float64)
+
+
+def layer64(spec, weights, x, keys, values, slot, pos, interleave=False, parts=False):
+    """One layer in float64; keys/values float64 [slots, kv_width], updated at
+    slot.  parts: also return {"W": the dequantized matrices, "attn": the
+    attention output wo reads, "act": the gated activation down reads}."""
+    H, KV, HD = spec["heads"], spec["kv_heads"], spec["head_dim"]
+    W = {k: dq(weights[k]) for k in ("wq", "wk", "wv", "wo", "gate", "up", "down")}
+    fac = weights.get("rope_factors")
+    x = x.astype(np.float64)
+    n = rms64(x, weights["attn_norm"].astype(np.float64), spec["eps"])
+    q = W["wq"] @ n
+    keys[slot] = W["wk"] @ n
+    values[slot] = W["wv"] @ n
+    q = rope64(q, H, HD, spec["rope_dim"], spec["rope_base"], spec["neox"], pos, fac)
+    keys[slot] = rope64(keys[slot], KV, HD, spec["rope_dim"], spec["rope_base"], spec["neox"], pos, fac)
+    heads_out = attend64(q, keys.reshape(-1), values.reshape(-1), slot + 1, H, KV, HD, spec["attn_scale"],
+                         interleave)
+    x = x + W["wo"] @ heads_out
+    n = rms64(x, weights["ffn_norm"].astype(np.float64), spec["eps"])
+    g = W["gate"] @ n
+    u = W["up"] @ n
+    with np.errstate(over="ignore"):
+        act = g / (1 + np.exp(-g)) * u
+    out = x + W["down"] @ act
+    if parts:
+        return out, {"W": W, "attn": heads_out, "act": act}
+    return out
+
+
+def layer_bound(parts, rel=1e-4):
+    """Per-element tolerance of a layer's output: rel times the absolute sums
+    the two last projections add into the residual, sum_j |wo_ij a_j| +
+    sum_j |down_ij h_j| -- the matvec gate (1e-4 sum |w x| per row,
+    tests/test_kernel.mojo:473) carried through wo and down, which also
+    covers what the rounding upstream of them (norm, q|k|v, attention)
+    moves their inputs by."""
+    W = parts["W"]
+    return rel * (np.abs(W["wo"]) @ np.abs(parts["attn"]) + np.abs(W["down"]) @ np.abs(parts["act"]))
+
+
+def envelope_close(got, want, rel):
+    """|got - want| <= rel * (|want| + rms(want)) elementwise: relative where
+    an element is large, relative to the vector's scale where it is near 0."""
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    bound = rel * (np.abs(want) + np.sqrt(np.mean(want * want)))
+    return float((np.abs(got - want) / bound).max())
+
+

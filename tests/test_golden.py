@@ -67,3 +67,23 @@ def test_layer_vector(g):
     assert np.abs(x - want).max() <= 1e-6 * np.abs(want).max()
     assert (k.reshape(38, 128)[37] == g["layer_k_new"]).all()
     assert (v.reshape(38, 128)[37] == g["layer_v_new"]).all()
+
+
+def test_layer_vector_against_float64(g):
+    """The committed layer output is the oracle's; here it is also held to
+    the float64 layer of tests/layer64.py (independent of the oracle), within
+    the per-element layer gate.  The float64 layer keeps the new key and value
+    unrounded where the vector rounded them through f16, which the gate
+    absorbs (one of 38 attended positions, weight about 1/38)."""
+    from tests import layer64 as l64
+    spec = dict(width=256, hidden=512, heads=4, kv_heads=2, head_dim=64, rope_dim=64, neox=0, eps=1e-5,
+                rope_base=500000.0, attn_scale=float(np.float32(1 / math.sqrt(64))))
+    host = {n: (oracle.Q4_K, *shape, g[f"layer_{n}"]) for n, shape in
+            {"wq": (256, 256), "wk": (128, 256), "wv": (128, 256), "wo": (256, 256), "gate": (512, 256),
+             "up": (512, 256), "down": (256, 512)}.items()}
+    host["attn_norm"], host["ffn_norm"] = g["layer_attn_norm"], g["layer_ffn_norm"]
+    k = g["layer_k16"].astype(np.float64).reshape(38, 128).copy()
+    v = g["layer_v16"].astype(np.float64).reshape(38, 128).copy()
+    want, parts = l64.layer64(spec, host, g["layer_x"], k, v, 37, 37, parts=True)
+    assert (np.abs(g["layer_x_out"] - want) <= l64.layer_bound(parts)).all()
+    assert np.abs(g["layer_k_new"] - k[37]).max() <= 1e-3 * np.abs(k[37]).max()

@@ -185,8 +185,11 @@ def test_matmul_tokens_epilogues(ctx, kind, tokens):
     (oracle.Q4_K, 14336, 4096, 1),      # config 2 gate/up
     (oracle.Q4_K, 4096, 14336, 1),      # config 2 down
     (oracle.Q4_0, 14336, 4096, 1),
+    (oracle.Q4_0, 4096, 14336, 1),
+    (oracle.Q4_0, 14336, 4096, 4),
     (oracle.Q4_0, 4096, 14336, 4),
     (oracle.Q4_K, 14336, 4096, 4),
+    (oracle.Q4_K, 4096, 14336, 4),
 ])
 def test_matvec_config_shapes(ctx, kind, rows, cols, tokens):
     from molla_amd import gpu
@@ -220,9 +223,9 @@ def test_q6k_head_and_argmax(ctx, tokens):
         ref = oracle.argmax(want[t])
         top2 = np.sort(want[t])[-2:]
         margin = float(top2[1] - top2[0])
-        print(f"token {t}: argmax {ref} top-2 margin {margin:.3e} max err {err[t].max():.3e}")
-        if margin > 2 * err[t].max():
-            assert picks[t] == ref
+        print(f"token {t}: argmax {ref} top-2 margin {margin:.3e} max err {err[t].max():.3e}", flush=True)
+        # the config asks for the reference's pick exactly, on these seeded inputs
+        assert picks[t] == ref, (t, margin)
         assert picks[t] == oracle.argmax(got[t])
 
 

@@ -28,7 +28,7 @@ import numpy as np
 import pytest
 
 import oracle
-from tests import npquant
+from tests import layer64 as l64
 
 F32 = np.float32
 
@@ -179,72 +179,7 @@ def test_layer_against_written_reference(heads, kv_heads):
         "the slots before the new one are not written to"
 
 
-# ---- an independent float64 layer (block.mojo:319-482) -----------------------
-
-def _rope64(x, heads, head_dim, rope_dim, base, neox, pos, factors):
-    """rope.mojo:253 angle / :294 rotate_scaled in float64: the angle of pair
-    p is pos * base^(-2p/rope_dim) / factor[p]; elements past rope_dim stay."""
-    x = x.reshape(heads, head_dim).copy()
-    pairs = rope_dim // 2
-    p = np.arange(pairs, dtype=np.float64)
-    theta = pos * base ** (-2.0 * p / rope_dim)
-    if factors is not None:
-        theta = theta / np.asarray(factors[:pairs], np.float64)
-    c, s = np.cos(theta), np.sin(theta)
-    if neox:
-        lo, hi = p.astype(int), p.astype(int) + pairs
-    else:
-        lo, hi = 2 * p.astype(int), 2 * p.astype(int) + 1
-    a, b = x[:, lo].copy(), x[:, hi].copy()
-    x[:, lo] = a * c - b * s
-    x[:, hi] = a * s + b * c
-    return x.reshape(-1)
-
-
-def _rms64(x, gain, eps):
-    return x / np.sqrt(np.mean(x * x) + eps) * gain
-
-
-def _attend64(q, keys, values, count, heads, kv_heads, head_dim, scale, interleave=False):
-    group = heads // kv_heads
-    K = keys.reshape(-1, kv_heads * head_dim)[:count].reshape(count, kv_heads, head_dim)
-    V = values.reshape(-1, kv_heads * head_dim)[:count].reshape(count, kv_heads, head_dim)
-    out = np.zeros((heads, head_dim))
-    for h in range(heads):
-        kh = h % kv_heads if interleave else h // group
-        s = K[:, kh, :] @ q[h * head_dim:(h + 1) * head_dim] * scale
-        p = np.exp(s - s.max())
-        out[h] = (p / p.sum()) @ V[:, kh, :]
-    return out.reshape(-1)
-
-
-def _dq(w):
-    kind, rows, cols, blob = w
-    if kind == oracle.F32:
-        return np.ascontiguousarray(blob).view(F32).reshape(rows, cols).astype(np.float64)
-    return npquant.dequant(kind, blob, rows * cols).reshape(rows, cols).astype(np.float64)
-
-
-def _layer64(spec, weights, x, keys, values, slot, pos, interleave=False):
-    """One layer in float64; keys/values float64 [slots, kv_width], updated at slot."""
-    H, KV, HD = spec["heads"], spec["kv_heads"], spec["head_dim"]
-    W = {k: _dq(weights[k]) for k in ("wq", "wk", "wv", "wo", "gate", "up", "down")}
-    fac = weights.get("rope_factors")
-    x = x.astype(np.float64)
-    n = _rms64(x, weights["attn_norm"].astype(np.float64), spec["eps"])
-    q = W["wq"] @ n
-    keys[slot] = W["wk"] @ n
-    values[slot] = W["wv"] @ n
-    q = _rope64(q, H, HD, spec["rope_dim"], spec["rope_base"], spec["neox"], pos, fac)
-    keys[slot] = _rope64(keys[slot], KV, HD, spec["rope_dim"], spec["rope_base"], spec["neox"], pos, fac)
-    heads_out = _attend64(q, keys.reshape(-1), values.reshape(-1), slot + 1, H, KV, HD, spec["attn_scale"],
-                         interleave)
-    x = x + W["wo"] @ heads_out
-    n = _rms64(x, weights["ffn_norm"].astype(np.float64), spec["eps"])
-    g = W["gate"] @ n
-    u = W["up"] @ n
-    return x + W["down"] @ (g / (1 + np.exp(-g)) * u)
-
+# ---- the float64 layer (tests/layer64.py, block.mojo:319-482) -----------------
 
 def _quant(kind, rows, cols, seed):
     from molla_amd import synth
@@ -270,15 +205,6 @@ def _model_layer(seed, width=256, hidden=512, heads=8, kv_heads=2, head_dim=32, 
     return spec, weights
 
 
-def _envelope_close(got, want, rel):
-    """|got - want| <= rel * (|want| + rms(want)) elementwise: relative where
-    an element is large, relative to the vector's scale where it is near 0."""
-    got = np.asarray(got, np.float64)
-    want = np.asarray(want, np.float64)
-    bound = rel * (np.abs(want) + np.sqrt(np.mean(want * want)))
-    return float((np.abs(got - want) / bound).max())
-
-
 @pytest.mark.parametrize("pos", [37, 1000])
 def test_layer_against_float64(pos):
     """Quantized weights (Q4_K, Q6_K, Q8_0), 8 query heads over 2 key heads,
@@ -295,11 +221,11 @@ def test_layer_against_float64(pos):
     x = rng.standard_normal(spec["width"]).astype(F32)
     k64 = keys.astype(np.float64).reshape(pos + 1, kvw)
     v64 = values.astype(np.float64).reshape(pos + 1, kvw)
-    want = _layer64(spec, weights, x, k64, v64, pos, pos)
+    want = l64.layer64(spec, weights, x, k64, v64, pos, pos)
     oracle.layer_step(L, x, keys, values, pos, pos)
-    assert _envelope_close(x, want, 1e-5) <= 1.0
-    assert _envelope_close(keys[pos * kvw:], k64[pos], 1e-5) <= 1.0
-    assert _envelope_close(values[pos * kvw:], v64[pos], 1e-5) <= 1.0
+    assert l64.envelope_close(x, want, 1e-5) <= 1.0
+    assert l64.envelope_close(keys[pos * kvw:], k64[pos], 1e-5) <= 1.0
+    assert l64.envelope_close(values[pos * kvw:], v64[pos], 1e-5) <= 1.0
 
 
 def test_layer_float64_catches_the_plausible_mistakes():
@@ -314,32 +240,32 @@ def test_layer_float64_catches_the_plausible_mistakes():
     keys = rng.standard_normal((pos + 1, kvw))
     values = rng.standard_normal((pos + 1, kvw))
     x = rng.standard_normal(spec["width"]).astype(F32)
-    good = _layer64(spec, weights, x, keys.copy(), values.copy(), pos, pos)
+    good = l64.layer64(spec, weights, x, keys.copy(), values.copy(), pos, pos)
     swapped = dict(weights, gate=weights["up"], up=weights["gate"])
     variants = {
-        "gate/up swapped": _layer64(spec, swapped, x, keys.copy(), values.copy(), pos, pos),
-        "no factors": _layer64(spec, {k: v for k, v in weights.items() if k != "rope_factors"}, x, keys.copy(),
+        "gate/up swapped": l64.layer64(spec, swapped, x, keys.copy(), values.copy(), pos, pos),
+        "no factors": l64.layer64(spec, {k: v for k, v in weights.items() if k != "rope_factors"}, x, keys.copy(),
                                values.copy(), pos, pos),
-        "neox pairs": _layer64(dict(spec, neox=1), weights, x, keys.copy(), values.copy(), pos, pos),
-        "query head h on key head h mod kv_heads": _layer64(spec, weights, x, keys.copy(), values.copy(), pos,
+        "neox pairs": l64.layer64(dict(spec, neox=1), weights, x, keys.copy(), values.copy(), pos, pos),
+        "query head h on key head h mod kv_heads": l64.layer64(spec, weights, x, keys.copy(), values.copy(), pos,
                                                             pos, interleave=True),
     }
     for name, v in variants.items():
-        assert _envelope_close(v, good, 1e-5) > 10.0, name
+        assert l64.envelope_close(v, good, 1e-5) > 10.0, name
     # k not rotated: rebuild by hand
     H, KV, HD = spec["heads"], spec["kv_heads"], spec["head_dim"]
-    W = {k: _dq(weights[k]) for k in ("wq", "wk", "wv", "wo", "gate", "up", "down")}
-    n = _rms64(x.astype(np.float64), weights["attn_norm"], spec["eps"])
+    W = {k: l64.dq(weights[k]) for k in ("wq", "wk", "wv", "wo", "gate", "up", "down")}
+    n = l64.rms64(x.astype(np.float64), weights["attn_norm"], spec["eps"])
     k2, v2 = keys.copy(), values.copy()
     k2[pos] = W["wk"] @ n
     v2[pos] = W["wv"] @ n
-    q = _rope64(W["wq"] @ n, H, HD, spec["rope_dim"], spec["rope_base"], 0, pos, weights["rope_factors"])
-    ho = _attend64(q, k2.reshape(-1), v2.reshape(-1), pos + 1, H, KV, HD, spec["attn_scale"])
+    q = l64.rope64(W["wq"] @ n, H, HD, spec["rope_dim"], spec["rope_base"], 0, pos, weights["rope_factors"])
+    ho = l64.attend64(q, k2.reshape(-1), v2.reshape(-1), pos + 1, H, KV, HD, spec["attn_scale"])
     r = x + W["wo"] @ ho
-    n2 = _rms64(r, weights["ffn_norm"], spec["eps"])
+    n2 = l64.rms64(r, weights["ffn_norm"], spec["eps"])
     g, u = W["gate"] @ n2, W["up"] @ n2
     no_krope = r + W["down"] @ (g / (1 + np.exp(-g)) * u)
-    assert _envelope_close(no_krope, good, 1e-5) > 10.0
+    assert l64.envelope_close(no_krope, good, 1e-5) > 10.0
 
 
 # ---- forward: tests/test_nnmodel.mojo:291-421 --------------------------------
@@ -412,8 +338,8 @@ def _forward64(spec, layer_ws, emb, onorm, head, tokens):
     for pos, tok in enumerate(tokens):
         x = emb[tok].astype(np.float64)
         for li, w in enumerate(layer_ws):
-            x = _layer64(spec, w, x, K[li], V[li], pos, pos)
-        out.append(_dq(head) @ _rms64(x, onorm.astype(np.float64), spec["eps"]))
+            x = l64.layer64(spec, w, x, K[li], V[li], pos, pos)
+        out.append(l64.dq(head) @ l64.rms64(x, onorm.astype(np.float64), spec["eps"]))
     return out
 
 
@@ -441,5 +367,5 @@ def test_forward_against_float64():
     values = [np.zeros(len(tokens) * kvw, F32) for _ in layers]
     for pos, tok in enumerate(tokens):
         got = oracle.forward(layers, emb, onorm, head, tok, pos, pos, keys, values)
-        assert _envelope_close(got, want[pos], 1e-5) <= 1.0, f"logits at position {pos}"
+        assert l64.envelope_close(got, want[pos], 1e-5) <= 1.0, f"logits at position {pos}"
         assert int(np.argmax(got)) == int(np.argmax(want[pos]))
