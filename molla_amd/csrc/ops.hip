@@ -761,7 +761,7 @@ __global__ __launch_bounds__(256) void store_kv_q8_kernel(const float* __restric
 // Every wave reduces the (max, sum) pairs identically; the weights
 // exp(m_c - M) are computed once per slice into LDS (zero past the last
 // slice) and the values are folded in slice order.
-constexpr int kMergeBatch = 32;
+constexpr int kMergeBatch = 64;
 __global__ void attend_merge_kernel(const float* __restrict__ part_acc, const float* __restrict__ part_ml,
                                     int heads, int head_dim, const int32_t* __restrict__ pos_dev,
                                     int count_host, int max_chunks, float* __restrict__ out,
@@ -809,6 +809,143 @@ __global__ void attend_merge_kernel(const float* __restrict__ part_acc, const fl
   if (xq)
     quantize_group32(o, threadIdx.x & 31, (h * head_dim + d) >> 5, width >> 5,
                      xq + (int64_t)t * xq_token_bytes(width), live);
+}
+
+// ---- decode attention slices ------------------------------------------------
+// attend_wide_kernel: the slice half of attention.mojo:144 attend
+// (gpu_ops.mojo:929 attend_split_kernel) for one query token per sequence
+// over an f16 cache, head_dim 64 or 128.  A block takes one (64-key slice,
+// key head, token) as attend_split_kernel does, with 1024 threads instead of
+// 256, so every stage is spread over 16 waves:
+//   * the slice's keys and values go to LDS with one load per thread;
+//   * each (query head, key) score is SPL threads of DPT dimensions each,
+//     added by shuffles;
+//   * the slice softmax is one wave per query head (lane = key);
+//   * each weighted value pair (query head, 2 dims) is KQ threads over
+//     interleaved keys, added by shuffles.
+// It writes each slice's (max, sum) and unnormalised values exactly where
+// attend_split_kernel does, and attend_merge_kernel folds them.
+constexpr int kWideThreads = 1024;
+constexpr int kWideKeys = 64;
+
+template <int GROUP, int D>
+struct WideShape {
+  static constexpr int KS = D + 8;   // K rows in halves (16-byte pad)
+  static constexpr int VS = D + 32;  // V rows: 16 dwords of pad, so the KQ lanes
+                                     // reading one dim pair hit distinct banks
+  static constexpr int SPL = (16 / GROUP) < (D / 8) ? (16 / GROUP) : (D / 8);  // threads per score
+  static constexpr int DPT = D / SPL;                                         // dims per score thread
+  static constexpr int KQ = 2 * kWideThreads / (GROUP * D);                   // threads per output pair
+};
+
+template <int GROUP, int D>
+__global__ __launch_bounds__(kWideThreads) void attend_wide_kernel(
+    const float* __restrict__ q, int64_t q_stride, const __half* __restrict__ kc, const __half* __restrict__ vc,
+    int64_t cache_stride, int heads, int kv_heads, float scale, const int32_t* __restrict__ pos_dev,
+    int count_host, int max_chunks, float* __restrict__ part_acc, float* __restrict__ part_ml,
+    const int32_t* __restrict__ kv_index, int64_t index_stride) {
+  using S = WideShape<GROUP, D>;
+  constexpr int KK = kWideKeys, PIECES = D / 8, TOTAL = KK * PIECES, PAIRS = D / 2;
+  static_assert(TOTAL <= kWideThreads && GROUP * D <= kWideThreads && S::KQ >= 1 && S::KQ <= 64, "shape");
+  __shared__ __align__(16) __half Ks[KK * S::KS];
+  __shared__ __align__(16) __half Vs[KK * S::VS];
+  __shared__ __align__(16) float Qs[GROUP * D];
+  __shared__ float Ss[GROUP * KK];
+  const int c = blockIdx.x, kvh = blockIdx.y, t = blockIdx.z;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int count = pos_dev ? pos_dev[t] + 1 : count_host;  // a position p attends over p + 1 slots
+  const int start = c * KK;
+  if (start >= count) return;
+  const int nk = min(KK, count - start);
+  const int kvw = kv_heads * D;
+
+  // stage: the group's queries, one 16-byte piece of a key and of a value
+  // per thread (keys past the end repeat the last live one; masked below)
+  const float* qg = q + (int64_t)t * q_stride + (int64_t)kvh * GROUP * D;
+  const bool has_q = tid < GROUP * D / 4;
+  const float4 qv = ((const float4*)qg)[has_q ? tid : 0];
+  const int64_t seq = kv_index ? 0 : (int64_t)t * cache_stride;
+  const int skey = min(tid / PIECES, KK - 1), pc = tid % PIECES;
+  const int cell = max(kv_cell(kv_index, index_stride, t, start + min(skey, nk - 1)), 0);
+  const int64_t off = seq + (int64_t)cell * kvw + (int64_t)kvh * D + pc * 8;
+  const uint4 kraw = *(const uint4*)(kc + off);
+  const uint4 vraw = *(const uint4*)(vc + off);
+  if (has_q) ((float4*)Qs)[tid] = qv;
+  if (tid < TOTAL) {
+    *(uint4*)(Ks + skey * S::KS + pc * 8) = kraw;
+    *(uint4*)(Vs + skey * S::VS + pc * 8) = vraw;
+  }
+  __syncthreads();
+
+  // scores: thread = (query head g, key, part of DPT dims)
+  {
+    const int dot = tid / S::SPL, part = tid % S::SPL;
+    const int g = dot / KK, key = dot % KK;
+    float sdot = 0.0f;
+    if (dot < GROUP * KK) {
+      const __half* kr = Ks + key * S::KS + part * S::DPT;
+      const float* qq = Qs + g * D + part * S::DPT;
+#pragma unroll
+      for (int d = 0; d < S::DPT; d += 8) {
+        const uint4 raw = *(const uint4*)(kr + d);
+        const __half2* h2 = (const __half2*)&raw;
+        const float4 qa = *(const float4*)(qq + d), qb = *(const float4*)(qq + d + 4);
+        const float2 k0 = __half22float2(h2[0]), k1 = __half22float2(h2[1]);
+        const float2 k2 = __half22float2(h2[2]), k3 = __half22float2(h2[3]);
+        sdot = fmaf(qa.x, k0.x, sdot);
+        sdot = fmaf(qa.y, k0.y, sdot);
+        sdot = fmaf(qa.z, k1.x, sdot);
+        sdot = fmaf(qa.w, k1.y, sdot);
+        sdot = fmaf(qb.x, k2.x, sdot);
+        sdot = fmaf(qb.y, k2.y, sdot);
+        sdot = fmaf(qb.z, k3.x, sdot);
+        sdot = fmaf(qb.w, k3.y, sdot);
+      }
+    }
+#pragma unroll
+    for (int o = 1; o < S::SPL; o <<= 1) sdot += __shfl_xor(sdot, o);
+    if (part == 0 && dot < GROUP * KK) {
+      const bool live = key < nk && (!kv_index || kv_cell(kv_index, index_stride, t, start + key) >= 0);
+      Ss[g * KK + key] = live ? sdot * scale : -INFINITY;
+    }
+  }
+  __syncthreads();
+  const int64_t slot0 = ((int64_t)t * heads + (int64_t)kvh * GROUP) * max_chunks;
+  // slice softmax: wave g takes query head g, lane = key
+  if (wave < GROUP) {
+    const float sc = Ss[wave * KK + lane];
+    float m = sc;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    const float pr = sc == -INFINITY ? 0.0f : expf(sc - m);
+    float l = pr;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) l += __shfl_xor(l, o);
+    Ss[wave * KK + lane] = pr;
+    if (lane == 0) *(float2*)(part_ml + (slot0 + (int64_t)wave * max_chunks + c) * 2) = make_float2(m, l);
+  }
+  __syncthreads();
+  // unnormalised weighted values: thread = (query head, dim pair, key residue kq)
+  const int kq = tid % S::KQ, oe = tid / S::KQ;
+  const int g = oe / PAIRS, e = oe % PAIRS;
+  float a0 = 0.0f, a1 = 0.0f;
+  if (oe < GROUP * PAIRS) {
+    const float* pg = Ss + g * KK;
+#pragma unroll 4
+    for (int k = kq; k < KK; k += S::KQ) {
+      const float p = pg[k];
+      const float2 v = __half22float2(*(const __half2*)(Vs + k * S::VS + 2 * e));
+      a0 = fmaf(p, v.x, a0);
+      a1 = fmaf(p, v.y, a1);
+    }
+  }
+#pragma unroll
+  for (int o = 1; o < S::KQ; o <<= 1) {
+    a0 += __shfl_xor(a0, o);
+    a1 += __shfl_xor(a1, o);
+  }
+  if (kq == 0 && oe < GROUP * PAIRS)
+    *(float2*)(part_acc + (slot0 + (int64_t)g * max_chunks + c) * D + 2 * e) = make_float2(a0, a1);
 }
 
 // ---- argmax ----------------------------------------------------------------
@@ -986,6 +1123,33 @@ int launch_attend(hipStream_t s, const float* q, int64_t q_stride, const uint16_
   const size_t acc_bytes = ((size_t)slots * head_dim * sizeof(float) + 255) & ~(size_t)255;
   float* part_ml = (float*)((char*)work + acc_bytes);
   const int group = heads / kv_heads;
+  const size_t merge_lds =
+      ((size_t)chunks * 2 + (chunks + kMergeBatch - 1) / kMergeBatch * kMergeBatch) * sizeof(float);
+  // decode (at most 8 tokens, one each per sequence, f16 cache): the
+  // 1024-thread slice kernel
+  if (tokens <= kMaxTokens && form != MI_CACHE_Q8 && (head_dim == 64 || head_dim == 128)) {
+    dim3 grid(chunks, kv_heads, tokens);
+#define MI_WIDE(G, DD)                                                                                       \
+  hipLaunchKernelGGL((attend_wide_kernel<G, DD>), grid, dim3(kWideThreads), 0, s, q, q_stride,               \
+                     (const __half*)k_cache, (const __half*)v_cache, cache_stride, heads, kv_heads, scale,     \
+                     pos_dev, count_host, chunks, part_acc, part_ml, kv_index, index_stride)
+#define MI_WIDE_D(G) \
+  if (head_dim == 64) MI_WIDE(G, 64); else MI_WIDE(G, 128)
+    switch (group) {
+      case 1: MI_WIDE_D(1); break;
+      case 2: MI_WIDE_D(2); break;
+      case 4: MI_WIDE_D(4); break;
+      case 8: MI_WIDE_D(8); break;
+      default: return fail(MI_ERR_SHAPE, "attend: %d query heads per key head is not 1, 2, 4 or 8", group);
+    }
+#undef MI_WIDE_D
+#undef MI_WIDE
+    int rc = hip_check(hipGetLastError(), "attend_wide launch");
+    if (rc) return rc;
+    hipLaunchKernelGGL(attend_merge_kernel, dim3(heads, tokens), dim3(head_dim < 64 ? 64 : head_dim), merge_lds, s,
+                       part_acc, part_ml, heads, head_dim, pos_dev, count_host, chunks, out, (uint8_t*)xq_out);
+    return hip_check(hipGetLastError(), "attend_merge launch");
+  }
   // one sequence's chunk (its tokens share one cache): 16 tokens per block
   // over one staged slice (f16 form; the q8 kernel takes one token a block)
   const bool one_seq = kv_index ? index_stride == 0 : cache_stride == 0;
@@ -1049,7 +1213,6 @@ int launch_attend(hipStream_t s, const float* q, int64_t q_stride, const uint16_
 #undef MI_ATTEND
   int rc = hip_check(hipGetLastError(), "attend_split launch");
   if (rc) return rc;
-  const size_t merge_lds = ((size_t)chunks * 2 + (chunks + kMergeBatch - 1) / kMergeBatch * kMergeBatch) * sizeof(float);
   hipLaunchKernelGGL(attend_merge_kernel, dim3(heads, tokens), dim3(head_dim < 64 ? 64 : head_dim), merge_lds, s,
                      part_acc, part_ml, heads, head_dim, pos_dev,
                      count_host, chunks, out, (uint8_t*)xq_out);
