@@ -109,6 +109,19 @@ int mi_matvec(mi_stream stream, int kind, const void* w, int64_t row_bytes,
               int32_t rows, int32_t cols, const float* x, int32_t tokens,
               float* y, int32_t epi, const float* aux, void* work, size_t work_bytes);
 
+/* No counterpart in the reference: mi_matvec without a workspace argument,
+ * for callers that cannot allocate device memory (code under HIP graph
+ * capture, serving loops that forbid hipMalloc).  The workspace is a static
+ * per-device scratch array of MI_MATVEC_NOALLOC_BYTES, whose address is
+ * resolved once per device on first use; the call itself allocates nothing.
+ * Shapes whose mi_matvec_workspace(cols, tokens) is larger are refused
+ * (MI_ERR_WORKSPACE).  Every call on one GPU shares that array: calls that
+ * overlap on one GPU race. */
+#define MI_MATVEC_NOALLOC_BYTES (32u << 20)
+int mi_matvec_noalloc(mi_stream stream, int kind, const void* w, int64_t row_bytes,
+                      int32_t rows, int32_t cols, const float* x, int32_t tokens,
+                      float* y, int32_t epi, const float* aux);
+
 /* The two halves of mi_matvec, for callers that reuse one quantized
  * activation across several matrices (q/k/v share the normed input; gate and
  * up share it too).  xq holds mi_matvec_workspace(cols, tokens) bytes. */

@@ -40,6 +40,7 @@ SIGNATURES = {
     "mi_matvec_workspace": (SZ, [I32, I32]),
     "mi_matmul_workspace": (SZ, [I32, I32, I32]),
     "mi_matvec": (ctypes.c_int, [P, ctypes.c_int, P, I64, I32, I32, P, I32, P, I32, P, P, SZ]),
+    "mi_matvec_noalloc": (ctypes.c_int, [P, ctypes.c_int, P, I64, I32, I32, P, I32, P, I32, P]),
     "mi_quantize": (ctypes.c_int, [P, P, I32, I32, P]),
     "mi_matvec_xq": (ctypes.c_int, [P, ctypes.c_int, P, I64, I32, I32, P, I32, P, I32, P]),
     "mi_rms_norm": (ctypes.c_int, [P, P, P, I32, I32, F, P, P]),
