@@ -153,12 +153,21 @@ def main():
         line["batched"] = _batched(L, h, kind, ws, copies, rb, stream)
         line["kinds"] = _kinds(L, h, stream)
         line["head"] = _head(L, h, stream)
+    peak = _stream_peak(stream)
+    line["roofline"]["stream_peak"] = peak
+    line["roofline"]["frac_of_stream_33MB"] = round(achieved / peak["read_33MB"]["GB_s"], 4)
+    del ws
+    torch.cuda.empty_cache()
+    model = None
+    if not args.no_decode or not args.no_cpu:
+        from molla_amd import block
+        model = block.synthetic_model(block.BlockSpec(), 32, 128256, device="cuda")
     if not args.no_cpu:
-        line["cpu_baseline"] = _cpu_baseline(base, kind, rb, x)
+        line["cpu_baseline"] = _cpu_baseline(base, kind, rb, x, model)
     if not args.no_prefill:
         line["prefill"] = _prefill(L, h, stream)
     if not args.no_decode:
-        line["decode"] = _decode(ctx, args)
+        line["decode"] = _decode(ctx, args, model)
     print(json.dumps(line), flush=True)
 
 
@@ -358,30 +367,167 @@ def _traffic_from_profile():
     return None
 
 
-def _cpu_baseline(w_dev, kind, rb, x_dev):
-    """The CPU oracle (serial C restatement of kernel.mojo:316 matvec) on the
-    same bytes, single thread; bounded to ~10 s of work."""
-    import numpy as np
+def _host_facts():
+    """The host the CPU baseline ran on: logical CPUs, the ones this process
+    may use, and the CPU model from /proc/cpuinfo."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    usable = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    return {"nproc": os.cpu_count(), "usable_cpus": usable, "cpu_model": model}
 
-    import oracle
 
-    blob = w_dev.cpu().numpy()
-    x = x_dev.cpu().numpy()
+def _timed(fn, budget_s, max_reps):
     t0 = time.perf_counter()
     reps = 0
     while True:
-        oracle.matvec(kind, blob, ROWS, COLS, x, threads=1)
+        fn()
         reps += 1
         el = time.perf_counter() - t0
-        if el > 10.0 or reps >= 200:
-            break
-    per = el / reps
-    gbs = _algo_bytes(ROWS, COLS, 1, ROWS * rb) / per / 1e9
-    return {"value": round(gbs, 3), "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"{reps} full Q4_K 14336x4096 matvecs (same bytes), {per * 1e3:.1f} ms each"}
+        if el > budget_s or reps >= max_reps:
+            return el / reps, reps
 
 
-def _decode(ctx, args):
+def _cpu_baseline(w_dev, kind, rb, x_dev, model=None):
+    """The CPU oracle (a C restatement of molla's host path) on the GPU box's
+    host, bounded to roughly 15-25 s of work:
+      * the config-2 matvec (kernel.mojo:316, the same bytes as the GPU
+        line), serial as the reference's host path is -- this is `value` --
+        and row-parallel over `threads` cores with OpenMP (the courtesy
+        variant of the reference's own baseline);
+      * one config-4 decoder layer (block.mojo:466: hidden 4096, 32/8 heads
+        of 128, MLP 14336, Q4_K, a cache of 4096 positions, the token at
+        4096), serial and threaded;
+      * one token of the synthetic 8B model (model.mojo:178 forward at
+        position 0 over the decode line's weights), serial and threaded."""
+    import numpy as np
+
+    import oracle
+    from molla_amd import synth
+
+    facts = _host_facts()
+    threads = max(1, min(16, facts["usable_cpus"] or 1))
+    blob = w_dev.cpu().numpy()
+    x = x_dev.cpu().numpy()
+    algo = _algo_bytes(ROWS, COLS, 1, ROWS * rb)
+    per1, reps1 = _timed(lambda: oracle.matvec(kind, blob, ROWS, COLS, x, threads=1), 6.0, 200)
+    pern, repsn = _timed(lambda: oracle.matvec(kind, blob, ROWS, COLS, x, threads=threads), 2.0, 400)
+    out = {"value": round(algo / per1 / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+           "sample": f"{reps1} full Q4_K 14336x4096 matvecs (same bytes), {per1 * 1e3:.1f} ms each, one thread",
+           "host": facts,
+           "matvec_threads": {"threads": threads, "GB_s": round(algo / pern / 1e9, 3), "ms": round(pern * 1e3, 3),
+                              "reps": repsn}}
+
+    # config 4: one layer at position 4096
+    spec = dict(width=4096, hidden=14336, heads=32, kv_heads=8, head_dim=128, rope_dim=128, neox=0, eps=1e-5,
+                rope_base=500000.0, attn_scale=float(np.float32(1 / np.sqrt(128.0))))
+    shapes = {"wq": (4096, 4096), "wk": (1024, 4096), "wv": (1024, 4096), "wo": (4096, 4096),
+              "gate": (14336, 4096), "up": (14336, 4096), "down": (4096, 14336)}
+    host = {n: (kind, r, c, synth.quant_tensor(kind, r, c, 500 + i).numpy()) for i, (n, (r, c)) in
+            enumerate(shapes.items())}
+    host["attn_norm"] = synth.normal(4096, 510, mean=1.0, std=0.1).numpy()
+    host["ffn_norm"] = synth.normal(4096, 511, mean=1.0, std=0.1).numpy()
+    keep = []
+    L = oracle.make_layer(spec, host, keep)
+    pos = 4096
+    keys0 = synth.normal((pos + 1) * 1024, 512).half().float().numpy()
+    vals0 = synth.normal((pos + 1) * 1024, 513).half().float().numpy()
+    xl = synth.normal(4096, 514).numpy()
+
+    def layer(t):
+        oracle.layer_step(L, xl.copy(), keys0.copy(), vals0.copy(), pos, pos, f16_store=True, threads=t)
+    l1, lr1 = _timed(lambda: layer(1), 3.0, 50)
+    ln, lrn = _timed(lambda: layer(threads), 1.5, 100)
+    lbytes = sum(host[n][3].nbytes for n in shapes) + 2 * 2 * (pos + 1) * 1024
+    out["layer_config4"] = {"bytes": lbytes, "ms_1_thread": round(l1 * 1e3, 2), "reps_1": lr1,
+                            f"ms_{threads}_threads": round(ln * 1e3, 2), f"reps_{threads}": lrn}
+    del host, keep, L, keys0, vals0
+
+    if model is not None:
+        s = model.spec
+        ospec = dict(width=s.width, hidden=s.hidden, heads=s.heads, kv_heads=s.kv_heads, head_dim=s.head_dim,
+                     rope_dim=s.rope_dim, neox=int(s.neox), eps=s.eps, rope_base=s.rope_base,
+                     attn_scale=s.attn_scale)
+        keep = []
+        layers = []
+        for lay in model.layers:
+            w = {n: (t.kind, t.rows, t.cols, t.keep.cpu().numpy()) for n, t in lay.weights.items()}
+            w["attn_norm"] = lay.attn_norm.cpu().numpy()
+            w["ffn_norm"] = lay.ffn_norm.cpu().numpy()
+            layers.append(oracle.make_layer(ospec, w, keep))
+        head = (model.output.kind, model.output.rows, model.output.cols, model.output.keep.cpu().numpy())
+        emb = model.embedding.cpu().numpy()
+        onorm = model.output_norm.cpu().numpy()
+        kvw = s.kv_width()
+
+        def token(t):
+            ks = [np.zeros(kvw, np.float32) for _ in layers]
+            vs = [np.zeros(kvw, np.float32) for _ in layers]
+            oracle.forward(layers, emb, onorm, head, 17, 0, 0, ks, vs, f16_store=True, threads=t)
+        t1, _ = _timed(lambda: token(1), 0.0, 1)
+        tn, trn = _timed(lambda: token(threads), 1.0, 5)
+        out["token_8b"] = {"weight_bytes": model.weight_bytes(), "s_1_thread": round(t1, 3),
+                           "tokens_per_s_1_thread": round(1 / t1, 3), f"s_{threads}_threads": round(tn, 3),
+                           f"tokens_per_s_{threads}_threads": round(1 / tn, 2), f"reps_{threads}": trn}
+        del layers, keep, head, emb
+    return out
+
+
+def _stream_peak(stream, reps=200):
+    """The read ceiling measured on this box: a plain streaming read
+    (libmolla_probe.so probe_read) of a 33,030,144-byte buffer rotated over
+    2 GiB so every launch reads cold HBM, timed like the roofline (K
+    back-to-back launches between HIP events), and of a 1 GiB buffer; the
+    best over four grid sizes."""
+    import ctypes
+
+    import torch
+
+    plib = ctypes.CDLL(os.path.join(ROOT, "molla_amd", "libmolla_probe.so"))
+    plib.probe_read.restype = ctypes.c_int
+    plib.probe_read.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_void_p]
+    size = ROWS * (COLS // 256) * 144
+    slot = (size + 4095) // 4096 * 4096
+    n = (2 << 30) // slot
+    big = torch.empty(n * slot + (1 << 30), dtype=torch.uint8, device="cuda")
+    big.view(torch.float32).zero_()
+    sink = torch.zeros(1, device="cuda")
+    h = stream.cuda_stream
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+    def run(nbytes, count, blocks, rotate):
+        for i in range(count):
+            off = (i % n) * slot if rotate else 0
+            if plib.probe_read(h, big.data_ptr() + off, nbytes, blocks, sink.data_ptr()) != 0:
+                raise RuntimeError("probe_read launch failed")
+
+    out = {}
+    for name, nbytes, count in (("read_33MB", size, reps), ("read_1GiB", 1 << 30, 10)):
+        best = None
+        for blocks in (1024, 2048, 4096, 8192):
+            run(nbytes, 5, blocks, name == "read_33MB")
+            torch.cuda.synchronize()
+            e0.record(stream)
+            run(nbytes, count, blocks, name == "read_33MB")
+            e1.record(stream)
+            torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) * 1e3 / count
+            if best is None or us < best[0]:
+                best = (us, blocks)
+        out[name] = {"bytes": nbytes, "us": round(best[0], 3), "GB_s": round(nbytes / best[0] / 1e3, 1),
+                     "blocks": best[1]}
+    del big
+    torch.cuda.empty_cache()
+    return out
+
+
+def _decode(ctx, args, model=None):
     """Config 5: synthetic 8B (32 layers, Q4_K, Q6_K head, f32 embedding);
     a prompt of uniform random ids prefilled in 256-token chunks through the
     prefill layer (gpu_block.mojo:1654 forward over a chunk; each sequence of
@@ -396,7 +542,8 @@ def _decode(ctx, args):
     spec = block.BlockSpec()
     vocab = 128256
     dev = "cuda"
-    model = block.synthetic_model(spec, 32, vocab, device=dev)
+    if model is None:
+        model = block.synthetic_model(spec, 32, vocab, device=dev)
     wb = model.weight_bytes()
     out = {"metric": "8B Q4_K decode tokens/sec", "prompt": args.prompt, "generated": args.decode_tokens,
            "weight_bytes_per_step": wb}
