@@ -815,8 +815,9 @@ __global__ void attend_merge_kernel(const float* __restrict__ part_acc, const fl
 // attend_wide_kernel: the slice half of attention.mojo:144 attend
 // (gpu_ops.mojo:929 attend_split_kernel) for one query token per sequence
 // over an f16 cache, head_dim 64 or 128.  A block takes one (64-key slice,
-// key head, token) as attend_split_kernel does, with 1024 threads instead of
-// 256, so every stage is spread over 16 waves:
+// key head, token) as attend_split_kernel does, with NT = 1024 threads (one
+// token; 512 for a batch, so that two blocks share a CU) instead of 256, so
+// every stage is spread over NT / 64 waves:
 //   * the slice's keys and values go to LDS with one load per thread;
 //   * each (query head, key) score is SPL threads of DPT dimensions each,
 //     added by shuffles;
@@ -825,28 +826,29 @@ __global__ void attend_merge_kernel(const float* __restrict__ part_acc, const fl
 //     interleaved keys, added by shuffles.
 // It writes each slice's (max, sum) and unnormalised values exactly where
 // attend_split_kernel does, and attend_merge_kernel folds them.
-constexpr int kWideThreads = 1024;
 constexpr int kWideKeys = 64;
 
-template <int GROUP, int D>
+template <int GROUP, int D, int NT>
 struct WideShape {
   static constexpr int KS = D + 8;   // K rows in halves (16-byte pad)
   static constexpr int VS = D + 32;  // V rows: 16 dwords of pad, so the KQ lanes
                                      // reading one dim pair hit distinct banks
-  static constexpr int SPL = (16 / GROUP) < (D / 8) ? (16 / GROUP) : (D / 8);  // threads per score
-  static constexpr int DPT = D / SPL;                                         // dims per score thread
-  static constexpr int KQ = 2 * kWideThreads / (GROUP * D);                   // threads per output pair
+  static constexpr int SPL0 = NT / (GROUP * kWideKeys);
+  static constexpr int SPL = SPL0 < (D / 8) ? SPL0 : (D / 8);  // threads per score
+  static constexpr int DPT = D / SPL;                           // dims per score thread
+  static constexpr int KQ = 2 * NT / (GROUP * D);               // threads per output pair
 };
 
-template <int GROUP, int D>
-__global__ __launch_bounds__(kWideThreads) void attend_wide_kernel(
+template <int GROUP, int D, int NT>
+__global__ __launch_bounds__(NT) void attend_wide_kernel(
     const float* __restrict__ q, int64_t q_stride, const __half* __restrict__ kc, const __half* __restrict__ vc,
     int64_t cache_stride, int heads, int kv_heads, float scale, const int32_t* __restrict__ pos_dev,
     int count_host, int max_chunks, float* __restrict__ part_acc, float* __restrict__ part_ml,
     const int32_t* __restrict__ kv_index, int64_t index_stride) {
-  using S = WideShape<GROUP, D>;
+  using S = WideShape<GROUP, D, NT>;
   constexpr int KK = kWideKeys, PIECES = D / 8, TOTAL = KK * PIECES, PAIRS = D / 2;
-  static_assert(TOTAL <= kWideThreads && GROUP * D <= kWideThreads && S::KQ >= 1 && S::KQ <= 64, "shape");
+  constexpr int PER = (TOTAL + NT - 1) / NT;  // 16-byte pieces of K (and of V) per thread
+  static_assert(GROUP * D / 4 <= NT && S::SPL >= 1 && S::KQ >= 1 && S::KQ <= 64, "shape");
   __shared__ __align__(16) __half Ks[KK * S::KS];
   __shared__ __align__(16) __half Vs[KK * S::VS];
   __shared__ __align__(16) float Qs[GROUP * D];
@@ -865,15 +867,25 @@ __global__ __launch_bounds__(kWideThreads) void attend_wide_kernel(
   const bool has_q = tid < GROUP * D / 4;
   const float4 qv = ((const float4*)qg)[has_q ? tid : 0];
   const int64_t seq = kv_index ? 0 : (int64_t)t * cache_stride;
-  const int skey = min(tid / PIECES, KK - 1), pc = tid % PIECES;
-  const int cell = max(kv_cell(kv_index, index_stride, t, start + min(skey, nk - 1)), 0);
-  const int64_t off = seq + (int64_t)cell * kvw + (int64_t)kvh * D + pc * 8;
-  const uint4 kraw = *(const uint4*)(kc + off);
-  const uint4 vraw = *(const uint4*)(vc + off);
+  uint4 kraw[PER], vraw[PER];
+#pragma unroll
+  for (int j = 0; j < PER; j++) {
+    const int i = min(tid + j * NT, TOTAL - 1);
+    const int skey = i / PIECES, pc = i % PIECES;
+    const int cell = max(kv_cell(kv_index, index_stride, t, start + min(skey, nk - 1)), 0);
+    const int64_t off = seq + (int64_t)cell * kvw + (int64_t)kvh * D + pc * 8;
+    kraw[j] = *(const uint4*)(kc + off);
+    vraw[j] = *(const uint4*)(vc + off);
+  }
   if (has_q) ((float4*)Qs)[tid] = qv;
-  if (tid < TOTAL) {
-    *(uint4*)(Ks + skey * S::KS + pc * 8) = kraw;
-    *(uint4*)(Vs + skey * S::VS + pc * 8) = vraw;
+#pragma unroll
+  for (int j = 0; j < PER; j++) {
+    const int i = tid + j * NT;
+    const int skey = i / PIECES, pc = i % PIECES;
+    if (i < TOTAL) {
+      *(uint4*)(Ks + skey * S::KS + pc * 8) = kraw[j];
+      *(uint4*)(Vs + skey * S::VS + pc * 8) = vraw[j];
+    }
   }
   __syncthreads();
 
@@ -1130,11 +1142,16 @@ int launch_attend(hipStream_t s, const float* q, int64_t q_stride, const uint16_
   if (tokens <= kMaxTokens && form != MI_CACHE_Q8 && (head_dim == 64 || head_dim == 128)) {
     dim3 grid(chunks, kv_heads, tokens);
 #define MI_WIDE(G, DD)                                                                                       \
-  hipLaunchKernelGGL((attend_wide_kernel<G, DD>), grid, dim3(kWideThreads), 0, s, q, q_stride,               \
-                     (const __half*)k_cache, (const __half*)v_cache, cache_stride, heads, kv_heads, scale,     \
-                     pos_dev, count_host, chunks, part_acc, part_ml, kv_index, index_stride)
+  if (tokens == 1)                                                                                           \
+    hipLaunchKernelGGL((attend_wide_kernel<G, DD, 1024>), grid, dim3(1024), 0, s, q, q_stride,               \
+                       (const __half*)k_cache, (const __half*)v_cache, cache_stride, heads, kv_heads, scale,   \
+                       pos_dev, count_host, chunks, part_acc, part_ml, kv_index, index_stride);               \
+  else                                                                                                       \
+    hipLaunchKernelGGL((attend_wide_kernel<G, DD, 512>), grid, dim3(512), 0, s, q, q_stride,                 \
+                       (const __half*)k_cache, (const __half*)v_cache, cache_stride, heads, kv_heads, scale,   \
+                       pos_dev, count_host, chunks, part_acc, part_ml, kv_index, index_stride)
 #define MI_WIDE_D(G) \
-  if (head_dim == 64) MI_WIDE(G, 64); else MI_WIDE(G, 128)
+  if (head_dim == 64) { MI_WIDE(G, 64); } else { MI_WIDE(G, 128); }
     switch (group) {
       case 1: MI_WIDE_D(1); break;
       case 2: MI_WIDE_D(2); break;
