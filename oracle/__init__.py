@@ -63,7 +63,13 @@ class Layer(ctypes.Structure):
                [(n, ctypes.c_float) for n in ("eps", "rope_base", "attn_scale")] + \
                [("attn_norm", ctypes.c_void_p), ("ffn_norm", ctypes.c_void_p)] + \
                [(n, Weight) for n in ("wq", "wk", "wv", "wo", "gate", "up", "down")] + \
-               [("rope_factors", ctypes.c_void_p)]
+               [("rope_factors", ctypes.c_void_p)] + \
+               [(n, ctypes.c_void_p) for n in ("q_bias", "k_bias", "v_bias", "q_norm", "k_norm", "attn_post_norm",
+                                               "ffn_post_norm")] + \
+               [("ungated", ctypes.c_int32), ("act", ctypes.c_int32)]
+
+# block.mojo optional layer parts: f32 vectors the layer may carry
+OPTIONAL_VECTORS = ("q_bias", "k_bias", "v_bias", "q_norm", "k_norm", "attn_post_norm", "ffn_post_norm")
 
 
 def _declare(l):
@@ -89,6 +95,7 @@ def _declare(l):
         "or_q8_cache_round": (None, [P, I32]),
         "or_attend": (None, [I32, I32, I32, F, P, P, P, I32, P, P]),
         "or_layer_step": (ctypes.c_int, [ctypes.POINTER(Layer), P, P, P, I32, I32, I32, I32]),
+        "or_layer_part": (ctypes.c_int, [ctypes.POINTER(Layer), P, P, P, I32, I32, I32, I32, I32]),
         "or_forward": (ctypes.c_int, [ctypes.POINTER(Layer), I32, P, I32, P, ctypes.POINTER(Weight),
                                       I32, I32, I32, P, P, I32, P, I32]),
         "or_xorshift_next": (U64, [ctypes.POINTER(U64)]),
@@ -230,9 +237,10 @@ def attend(heads, kv_heads, head_dim, scale, q, keys, values, count) -> np.ndarr
 
 
 def make_layer(spec: dict, weights: dict, keep: list) -> Layer:
-    """spec: width, hidden, heads, kv_heads, head_dim, rope_dim, neox, eps, rope_base, attn_scale.
-    weights: attn_norm, ffn_norm (f32 arrays); wq..down as (kind, rows, cols, bytes);
-    optionally rope_factors (f32, rope_dim / 2)."""
+    """spec: width, hidden, heads, kv_heads, head_dim, rope_dim, neox, eps, rope_base, attn_scale,
+    optionally ungated (1: act(up) MLP) and act (0 silu, 1 gelu).
+    weights: attn_norm, ffn_norm (f32 arrays); wq..down as (kind, rows, cols, bytes) (gate may be
+    absent when ungated); optionally rope_factors (f32, rope_dim / 2) and the OPTIONAL_VECTORS."""
     L = Layer()
     for k in ("width", "hidden", "heads", "kv_heads", "head_dim", "rope_dim", "neox"):
         setattr(L, k, int(spec[k]))
@@ -243,10 +251,20 @@ def make_layer(spec: dict, weights: dict, keep: list) -> Layer:
         keep.append(a)
         setattr(L, k, a.ctypes.data)
     for k in ("wq", "wk", "wv", "wo", "gate", "up", "down"):
+        if k not in weights:
+            continue
         kind, rows, cols, blob = weights[k]
         blob = np.ascontiguousarray(blob, dtype=np.uint8)
         keep.append(blob)
         setattr(L, k, Weight(blob.ctypes.data, kind, rows, cols, row_bytes(kind, cols)))
+    for k in OPTIONAL_VECTORS:
+        v = weights.get(k)
+        if v is not None:
+            v = np.ascontiguousarray(v, dtype=np.float32)
+            keep.append(v)
+            setattr(L, k, v.ctypes.data)
+    L.ungated = int(spec.get("ungated", 0))
+    L.act = int(spec.get("act", 0))
     f = weights.get("rope_factors")  # rope_freqs.weight, one per pair, or absent
     if f is not None:
         f = np.ascontiguousarray(f, dtype=np.float32)
@@ -267,14 +285,15 @@ def _store_form(f16_store, q8_store) -> int:
 
 
 def layer_step(L: Layer, x: np.ndarray, keys: np.ndarray, values: np.ndarray, slot: int, pos: int,
-               f16_store: bool = False, threads: int = 1, q8_store: bool = False) -> None:
+               f16_store: bool = False, threads: int = 1, q8_store: bool = False, parts: int = 3) -> None:
     """In place on x, keys[slot], values[slot] (f32 caches).  f16_store /
     q8_store: the new key and value go through what an f16 / q8_0 device cache
-    holds before they are attended over."""
+    holds before they are attended over.  parts: 1 the attention sublayer
+    only (block.mojo:319), 2 the mlp sublayer only (:429), 3 the layer."""
     for a in (x, keys, values):
         assert a.dtype == np.float32 and a.flags["C_CONTIGUOUS"]
-    rc = lib().or_layer_step(ctypes.byref(L), _p(x), _p(keys), _p(values), slot, pos,
-                             _store_form(f16_store, q8_store), threads)
+    rc = lib().or_layer_part(ctypes.byref(L), _p(x), _p(keys), _p(values), slot, pos,
+                             _store_form(f16_store, q8_store), threads, parts)
     if rc != 0:
         raise ValueError(f"layer refused (rc {rc})")
 

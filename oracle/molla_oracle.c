@@ -627,9 +627,23 @@ void or_q8_cache_round(float* v, int32_t n) {
   }
 }
 
-/* block.mojo:466 layer = attention_layer (:319) then mlp_layer (:429). */
-int or_layer_step(const or_layer* L, float* x, float* keys, float* values,
-                  int32_t slot, int32_t pos, int32_t f16_store, int32_t threads) {
+/* kernel.mojo:400 rms_norm_at: the same norm over a run of n values, in
+ * place (a head of q or k, or a sublayer's whole output). */
+static void rms_norm_at(float* x, const float* gain, int32_t n, float eps) {
+  or_rms_norm(x, x, gain, n, eps);
+}
+
+/* kernel.mojo:526 add_bias_at */
+static void add_bias_at(float* x, const float* bias, int32_t n) {
+  for (int32_t i = 0; i < n; i++) x[i] += bias[i];
+}
+
+static float act_of(int32_t act, float v) { return act ? or_gelu(v) : or_silu(v); }
+
+/* block.mojo:466 layer = attention_layer (:319) then mlp_layer (:429);
+ * parts: 1 the attention sublayer only, 2 the mlp sublayer only, 3 both. */
+int or_layer_part(const or_layer* L, float* x, float* keys, float* values,
+                  int32_t slot, int32_t pos, int32_t f16_store, int32_t threads, int32_t parts) {
   int32_t width = L->width, qw = L->heads * L->head_dim, kvw = L->kv_heads * L->head_dim;
   int32_t hidden = L->hidden;
   float* norm = (float*)malloc(sizeof(float) * width);
@@ -642,6 +656,7 @@ int or_layer_step(const or_layer* L, float* x, float* keys, float* values,
   int rc = 0;
   if (!norm || !q || !heads_out || !projected || !gate || !up || !scores) { rc = -9; goto done; }
 
+  if (!(parts & 1)) goto mlp;
   /* attention_layer */
   or_rms_norm(norm, x, L->attn_norm, width, L->eps);
   if ((rc = mv(&L->wq, norm, q, threads))) goto done;
@@ -649,6 +664,16 @@ int or_layer_step(const or_layer* L, float* x, float* keys, float* values,
   float* vslot = values + (int64_t)slot * kvw;
   if ((rc = mv(&L->wk, norm, kslot, threads))) goto done;
   if ((rc = mv(&L->wv, norm, vslot, threads))) goto done;
+  /* block.mojo:363-366: the bias is part of the projection */
+  if (L->q_bias) add_bias_at(q, L->q_bias, qw);
+  if (L->k_bias) add_bias_at(kslot, L->k_bias, kvw);
+  if (L->v_bias) add_bias_at(vslot, L->v_bias, kvw);
+  /* block.mojo:367-384: each head of q and k normed before rope */
+  if (L->q_norm) {
+    for (int32_t h = 0; h < L->heads; h++) rms_norm_at(q + (int64_t)h * L->head_dim, L->q_norm, L->head_dim, L->eps);
+    for (int32_t h = 0; h < L->kv_heads; h++)
+      rms_norm_at(kslot + (int64_t)h * L->head_dim, L->k_norm, L->head_dim, L->eps);
+  }
   or_rotate_run_scaled(q, L->heads, L->head_dim, L->rope_dim, L->rope_base, L->neox, pos, L->rope_factors);
   or_rotate_run_scaled(kslot, L->kv_heads, L->head_dim, L->rope_dim, L->rope_base, L->neox, pos,
                        L->rope_factors);
@@ -664,19 +689,37 @@ int or_layer_step(const or_layer* L, float* x, float* keys, float* values,
   or_attend(L->heads, L->kv_heads, L->head_dim, L->attn_scale, q, keys, values,
             slot + 1, heads_out, scores);
   if ((rc = mv(&L->wo, heads_out, projected, threads))) goto done;
+  /* block.mojo:405-406: a sublayer's output normed on its way in */
+  if (L->attn_post_norm) rms_norm_at(projected, L->attn_post_norm, width, L->eps);
   for (int32_t i = 0; i < width; i++) x[i] += projected[i];
 
-  /* mlp_layer, gated silu */
+mlp:
+  if (!(parts & 2)) goto done;
+  /* mlp_layer (:429-463) */
   or_rms_norm(norm, x, L->ffn_norm, width, L->eps);
   if ((rc = mv(&L->up, norm, up, threads))) goto done;
-  if ((rc = mv(&L->gate, norm, gate, threads))) goto done;
-  or_swiglu(gate, up, hidden);
-  if ((rc = mv(&L->down, gate, projected, threads))) goto done;
+  if (!L->ungated) {
+    if ((rc = mv(&L->gate, norm, gate, threads))) goto done;
+    if (L->act)
+      for (int32_t i = 0; i < hidden; i++) gate[i] = or_gelu(gate[i]) * up[i];
+    else
+      or_swiglu(gate, up, hidden);
+    if ((rc = mv(&L->down, gate, projected, threads))) goto done;
+  } else {
+    for (int32_t i = 0; i < hidden; i++) up[i] = act_of(L->act, up[i]);
+    if ((rc = mv(&L->down, up, projected, threads))) goto done;
+  }
+  if (L->ffn_post_norm) rms_norm_at(projected, L->ffn_post_norm, width, L->eps);
   for (int32_t i = 0; i < width; i++) x[i] += projected[i];
 
 done:
   free(norm); free(q); free(heads_out); free(projected); free(gate); free(up); free(scores);
   return rc;
+}
+
+int or_layer_step(const or_layer* L, float* x, float* keys, float* values,
+                  int32_t slot, int32_t pos, int32_t f16_store, int32_t threads) {
+  return or_layer_part(L, x, keys, values, slot, pos, f16_store, threads, 3);
 }
 
 /* model.mojo:178 forward: embed (:102, an f32 row copy), the layers, head (:136). */

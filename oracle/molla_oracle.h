@@ -80,6 +80,17 @@ typedef struct {
   const float* ffn_norm;
   or_weight wq, wk, wv, wo, gate, up, down;
   const float* rope_factors; /* rope_dim/2 per-pair factors (rope_freqs.weight) or NULL */
+  /* Optional parts of other families (block.mojo:61 BlockSpec, :116
+   * LayerWeights); NULL / 0 is the Llama layer. */
+  const float* q_bias;          /* q_width values (Qwen 2) */
+  const float* k_bias;          /* kv_width */
+  const float* v_bias;          /* kv_width */
+  const float* q_norm;          /* head_dim gains, every query head (Qwen 3) */
+  const float* k_norm;          /* head_dim gains, every key head */
+  const float* attn_post_norm;  /* width gains on wo's output (Gemma 2) */
+  const float* ffn_post_norm;   /* width gains on down's output */
+  int32_t ungated;              /* 1: act(up(x)) instead of act(gate(x)) * up(x) */
+  int32_t act;                  /* 0 silu, 1 gelu (tanh form, kernel.mojo:499) */
 } or_layer;
 
 /* block.mojo:466 layer (attention_layer :319 + mlp_layer :429), in place on x.
@@ -93,6 +104,10 @@ typedef struct {
 void or_q8_cache_round(float* v, int32_t n);
 int or_layer_step(const or_layer* L, float* x, float* keys, float* values,
                   int32_t slot, int32_t pos, int32_t f16_store, int32_t threads);
+/* One sublayer of it: parts 1 = attention_layer (block.mojo:319), 2 =
+ * mlp_layer (:429), 3 = both (the same as or_layer_step). */
+int or_layer_part(const or_layer* L, float* x, float* keys, float* values,
+                  int32_t slot, int32_t pos, int32_t f16_store, int32_t threads, int32_t parts);
 
 /* model.mojo:178 forward for a Llama stack with an f32 embedding:
  * embed (:102) -> layers -> head (:136).  keys[i]/values[i] per layer. */

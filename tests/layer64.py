@@ -53,6 +53,16 @@ def attend64(q, keys, values, count, heads, kv_heads, head_dim, scale, interleav
     return out.reshape(-1)
 
 
+def silu64(v):
+    with np.errstate(over="ignore"):
+        return v / (1 + np.exp(-v))
+
+
+def gelu64(v):
+    """kernel.mojo:499 gelu, the tanh approximation."""
+    return 0.5 * v * (1 + np.tanh(0.7978845608028654 * (v + 0.044715 * v ** 3)))
+
+
 def dq(w):
     kind, rows, cols, blob = w
     if kind == oracle.F32:
@@ -65,24 +75,43 @@ def layer64(spec, weights, x, keys, values, slot, pos, interleave=False, parts=F
     slot.  parts: also return {"W": the dequantized matrices, "attn": the
     attention output wo reads, "act": the gated activation down reads}."""
     H, KV, HD = spec["heads"], spec["kv_heads"], spec["head_dim"]
-    W = {k: dq(weights[k]) for k in ("wq", "wk", "wv", "wo", "gate", "up", "down")}
+    W = {k: dq(weights[k]) for k in ("wq", "wk", "wv", "wo", "gate", "up", "down") if k in weights}
     fac = weights.get("rope_factors")
     x = x.astype(np.float64)
-    n = rms64(x, weights["attn_norm"].astype(np.float64), spec["eps"])
+    opt = {k: (None if weights.get(k) is None else np.asarray(weights[k], np.float64)) for k in
+           ("q_bias", "k_bias", "v_bias", "q_norm", "k_norm", "attn_post_norm", "ffn_post_norm")}
+    eps = spec["eps"]
+    n = rms64(x, weights["attn_norm"].astype(np.float64), eps)
     q = W["wq"] @ n
     keys[slot] = W["wk"] @ n
     values[slot] = W["wv"] @ n
+    # block.mojo:363-384: biases, then each head of q and k normed, then rope
+    if opt["q_bias"] is not None:
+        q = q + opt["q_bias"]
+        keys[slot] = keys[slot] + opt["k_bias"]
+        values[slot] = values[slot] + opt["v_bias"]
+    if opt["q_norm"] is not None:
+        q = np.concatenate([rms64(h, opt["q_norm"], eps) for h in q.reshape(H, HD)])
+        keys[slot] = np.concatenate([rms64(h, opt["k_norm"], eps) for h in keys[slot].reshape(KV, HD)])
     q = rope64(q, H, HD, spec["rope_dim"], spec["rope_base"], spec["neox"], pos, fac)
     keys[slot] = rope64(keys[slot], KV, HD, spec["rope_dim"], spec["rope_base"], spec["neox"], pos, fac)
     heads_out = attend64(q, keys.reshape(-1), values.reshape(-1), slot + 1, H, KV, HD, spec["attn_scale"],
                          interleave)
-    x = x + W["wo"] @ heads_out
-    n = rms64(x, weights["ffn_norm"].astype(np.float64), spec["eps"])
-    g = W["gate"] @ n
+    proj = W["wo"] @ heads_out
+    if opt["attn_post_norm"] is not None:
+        proj = rms64(proj, opt["attn_post_norm"], eps)
+    x = x + proj
+    n = rms64(x, weights["ffn_norm"].astype(np.float64), eps)
     u = W["up"] @ n
-    with np.errstate(over="ignore"):
-        act = g / (1 + np.exp(-g)) * u
-    out = x + W["down"] @ act
+    fn = gelu64 if spec.get("act", 0) else silu64
+    if spec.get("ungated", 0):
+        act = fn(u)
+    else:
+        act = fn(W["gate"] @ n) * u
+    proj = W["down"] @ act
+    if opt["ffn_post_norm"] is not None:
+        proj = rms64(proj, opt["ffn_post_norm"], eps)
+    out = x + proj
     if parts:
         return out, {"W": W, "attn": heads_out, "act": act}
     return out
