@@ -225,6 +225,21 @@ typedef struct {
                                 its factor, rope.mojo:253), or NULL for none */
   int32_t cache_form;        /* MI_CACHE_F16 (0, the default) or MI_CACHE_Q8; the
                                 caches' cache_stride counts halves either way */
+  /* The optional parts of other families (block.mojo:61 BlockSpec, :116
+   * LayerWeights; on the device gpu_block.mojo:678-896).  NULL / 0 in every
+   * one of them is the Llama layer above. */
+  const float* q_bias;         /* device f32[heads*head_dim], with k_bias and v_bias
+                                  (f32[kv_heads*head_dim]): Qwen 2's projection biases */
+  const float* k_bias;
+  const float* v_bias;
+  const float* q_norm;         /* device f32[head_dim], with k_norm: each head of q and
+                                  k RMS-normed before rope (Qwen 3) */
+  const float* k_norm;
+  const float* attn_post_norm; /* device f32[width]: wo's output normed before the
+                                  residual add (Gemma 2); likewise ffn_post_norm on down's */
+  const float* ffn_post_norm;
+  int32_t ungated;             /* 1: the MLP is down(act(up(x))), gate unused */
+  int32_t act;                 /* 0 silu, MI_ACT_GELU gelu (tanh form, kernel.mojo:499) */
 } mi_layer_desc;
 
 /* One Llama layer for `tokens` independent sequences (batch decode, one token

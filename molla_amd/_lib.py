@@ -25,7 +25,10 @@ class MiLayerDesc(ctypes.Structure):
                 ("rope_dim", I32), ("neox", I32), ("eps", F), ("attn_scale", F), ("attn_norm", P),
                 ("ffn_norm", P), ("rope_steps", P)] + \
                [(n, MiWeight) for n in ("wq", "wk", "wv", "wo", "gate", "up", "down")] + \
-               [("rope_factors", P), ("cache_form", I32)]
+               [("rope_factors", P), ("cache_form", I32)] + \
+               [(n, P) for n in ("q_bias", "k_bias", "v_bias", "q_norm", "k_norm", "attn_post_norm",
+                                 "ffn_post_norm")] + \
+               [("ungated", I32), ("act", I32)]
 
 
 # Every symbol include/molla_mi.h declares, with its C signature.

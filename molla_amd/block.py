@@ -32,6 +32,8 @@ class BlockSpec:
     rope_base: float = 500000.0
     neox: bool = False  # Llama pairs adjacent elements (arch.mojo:146-152)
     eps: float = 1e-5
+    ungated: bool = False  # block.mojo:80 gated: False computes act(up(x))
+    act: int = 0  # block.mojo:83: 0 silu, gpu.ACT_BIT (8) gelu
 
     @property
     def attn_scale(self) -> float:
@@ -50,8 +52,10 @@ class DeviceLayer:
 
     NAMES = ("wq", "wk", "wv", "wo", "gate", "up", "down")
 
+    OPTIONAL = ("q_bias", "k_bias", "v_bias", "q_norm", "k_norm", "attn_post_norm", "ffn_post_norm")
+
     def __init__(self, spec: BlockSpec, attn_norm: torch.Tensor, ffn_norm: torch.Tensor, weights: dict,
-                 rope_steps: torch.Tensor, rope_factors: torch.Tensor | None = None):
+                 rope_steps: torch.Tensor, rope_factors: torch.Tensor | None = None, extras: dict | None = None):
         self.spec = spec
         self.attn_norm = attn_norm
         self.ffn_norm = ffn_norm
@@ -66,7 +70,18 @@ class DeviceLayer:
         d.eps, d.attn_scale = spec.eps, spec.attn_scale
         d.attn_norm, d.ffn_norm, d.rope_steps = attn_norm.data_ptr(), ffn_norm.data_ptr(), rope_steps.data_ptr()
         for n in self.NAMES:
+            if n == "gate" and spec.ungated and n not in weights:
+                continue
             setattr(d, n, weights[n].weight())
+        # block.mojo:116 LayerWeights' optional parts (device f32 vectors)
+        self.extras = dict(extras or {})
+        for n, t in self.extras.items():
+            if n not in self.OPTIONAL:
+                raise ValueError(f"unknown optional layer part {n!r}")
+            if t.dtype != torch.float32 or not t.is_cuda:
+                raise ValueError(f"{n} must be a device float32 tensor")
+            setattr(d, n, t.data_ptr())
+        d.ungated, d.act = int(spec.ungated), int(spec.act)
         if rope_factors is not None:
             if rope_factors.dtype != torch.float32 or rope_factors.numel() < spec.rope_dim // 2:
                 raise ValueError(f"rope wants {spec.rope_dim // 2} f32 frequency factors")

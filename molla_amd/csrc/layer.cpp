@@ -118,6 +118,12 @@ int check_desc(const mi_layer_desc* d) {
   if (!(d->eps > 0.0f)) return fail(MI_ERR_ARG, "layer: a norm epsilon has to be positive");
   if (!d->attn_norm || !d->ffn_norm || !d->rope_steps) return fail(MI_ERR_ARG, "layer: null norm or rope table");
   const int32_t qw = d->heads * d->head_dim, kvw = d->kv_heads * d->head_dim;
+  // block.mojo:116 LayerWeights.check: the optional parts come whole or not at all
+  const int biases = !!d->q_bias + !!d->k_bias + !!d->v_bias;
+  if (biases != 0 && biases != 3) return fail(MI_ERR_ARG, "layer: q, k and v biases come together (%d of 3)", biases);
+  if (!d->q_norm != !d->k_norm) return fail(MI_ERR_ARG, "layer: q and k norms come together");
+  if (d->ungated != 0 && d->ungated != 1) return fail(MI_ERR_ARG, "layer: ungated is 0 or 1, not %d", d->ungated);
+  if (d->act != 0 && d->act != MI_ACT_GELU) return fail(MI_ERR_ARG, "layer: act %d is neither silu (0) nor gelu", d->act);
   struct {
     const char* name;
     const mi_weight& w;
@@ -127,6 +133,7 @@ int check_desc(const mi_layer_desc* d) {
               {"gate", d->gate, d->hidden, d->width}, {"up", d->up, d->hidden, d->width},
               {"down", d->down, d->width, d->hidden}};
   for (auto& e : want) {
+    if (d->ungated && &e.w == &d->gate) continue;  // act(up(x)): no gate
     // block.mojo:230-247 _shape: a projection of the wrong size is refused.
     if (e.w.rows != e.rows || e.w.cols != e.cols)
       return fail(MI_ERR_SHAPE, "layer: %s is %d x %d where the layer wants %d x %d", e.name, e.w.rows,
@@ -137,7 +144,93 @@ int check_desc(const mi_layer_desc* d) {
   return MI_OK;
 }
 
+// Whether the layer uses any part beyond the Llama layer (q|k|v biases,
+// q/k norms, post norms, a non-gated or gelu MLP).
+bool extended(const mi_layer_desc* d) {
+  return d->q_bias || d->q_norm || d->attn_post_norm || d->ffn_post_norm || d->ungated || d->act;
+}
+
 }  // namespace
+
+// The layer with the optional parts of other families at 1..8 tokens, as
+// gpu_block.mojo:678 device_attention and :846 device_mlp run it: norm,
+// q/k/v (bias epilogue), per-head q/k norms, rope and the cache store,
+// attention, wo (then the post norm and the residual add, or the add
+// epilogue), norm, up and gate (GLU epilogue, silu or gelu) or up and the
+// activation, down (likewise).  Each part is its own launch; the fused
+// Llama kernels stay for the Llama layer.
+static int extended_layer(hipStream_t s, const mi_layer_desc* d, float* resid, uint16_t* k_cache,
+                          uint16_t* v_cache, int64_t cache_stride, const int32_t* kv_index, int64_t index_stride,
+                          const int32_t* pos, int32_t max_count, int32_t tokens, char* base, const Carve& c) {
+  void* xq = base + c.xq;
+  void* xq2 = base + c.xq2;
+  float* qkv = (float*)(base + c.qkv);
+  float* up = (float*)(base + c.up);
+  float* gate = (float*)(base + c.gate);
+  void* attn = base + c.attn;
+  const int32_t qw = d->heads * d->head_dim, kvw = d->kv_heads * d->head_dim;
+  const int64_t qkv_stride = qw + 2 * (int64_t)kvw;
+  const int32_t bias = d->q_bias ? MI_EPI_BIAS : MI_EPI_NONE;
+  int rc;
+  // attention_layer (block.mojo:319)
+  if ((rc = launch_rms_norm(s, resid, d->attn_norm, d->width, tokens, d->eps, nullptr, xq))) return rc;
+  if ((rc = launch_matvec(s, d->wq.kind, d->wq.data, d->wq.row_bytes, qw, d->width, xq, tokens, qkv, qkv_stride,
+                          bias, d->q_bias)))
+    return rc;
+  if ((rc = launch_matvec(s, d->wk.kind, d->wk.data, d->wk.row_bytes, kvw, d->width, xq, tokens, qkv + qw,
+                          qkv_stride, bias, d->k_bias)))
+    return rc;
+  if ((rc = launch_matvec(s, d->wv.kind, d->wv.data, d->wv.row_bytes, kvw, d->width, xq, tokens, qkv + qw + kvw,
+                          qkv_stride, bias, d->v_bias)))
+    return rc;
+  if (d->q_norm) {
+    if ((rc = launch_head_norm(s, qkv, d->heads, d->head_dim, tokens, qkv_stride, d->q_norm, d->eps))) return rc;
+    if ((rc = launch_head_norm(s, qkv + qw, d->kv_heads, d->head_dim, tokens, qkv_stride, d->k_norm, d->eps)))
+      return rc;
+  }
+  if ((rc = launch_rope_store(s, qkv, d->heads, d->kv_heads, d->head_dim, d->rope_dim, d->neox, d->rope_steps, pos,
+                              tokens, qkv_stride, k_cache, v_cache, cache_stride, d->rope_factors, d->cache_form,
+                              kv_index, index_stride)))
+    return rc;
+  if ((rc = launch_attend(s, qkv, qkv_stride, k_cache, v_cache, cache_stride, d->heads, d->kv_heads, d->head_dim,
+                          d->attn_scale, pos, -1, max_count, tokens, nullptr, xq, attn, d->cache_form, kv_index,
+                          index_stride)))
+    return rc;
+  if (d->attn_post_norm) {
+    // wo into a scratch row (the up buffer is free until the MLP), normed into the stream
+    if ((rc = launch_matvec(s, d->wo.kind, d->wo.data, d->wo.row_bytes, d->width, qw, xq, tokens, up, d->width,
+                            MI_EPI_NONE, nullptr)))
+      return rc;
+    if ((rc = launch_norm_add(s, resid, up, d->width, tokens, d->attn_post_norm, d->eps))) return rc;
+  } else if ((rc = launch_matvec(s, d->wo.kind, d->wo.data, d->wo.row_bytes, d->width, qw, xq, tokens, resid,
+                                 d->width, MI_EPI_ADD, nullptr))) {
+    return rc;
+  }
+  // mlp_layer (block.mojo:429)
+  if ((rc = launch_rms_norm(s, resid, d->ffn_norm, d->width, tokens, d->eps, nullptr, xq))) return rc;
+  if ((rc = launch_matvec(s, d->up.kind, d->up.data, d->up.row_bytes, d->hidden, d->width, xq, tokens, up,
+                          d->hidden, MI_EPI_NONE, nullptr)))
+    return rc;
+  float* h = up;
+  if (d->ungated) {
+    if ((rc = launch_act(s, up, (int64_t)d->hidden * tokens, d->act))) return rc;
+  } else {
+    if ((rc = launch_matvec(s, d->gate.kind, d->gate.data, d->gate.row_bytes, d->hidden, d->width, xq, tokens, gate,
+                            d->hidden, MI_EPI_GLU | d->act, up)))
+      return rc;
+    h = gate;
+  }
+  if ((rc = launch_quantize(s, h, d->hidden, tokens, xq2))) return rc;
+  if (d->ffn_post_norm) {
+    float* tmp = h == up ? gate : up;  // whichever of the two the activation is not in
+    if ((rc = launch_matvec(s, d->down.kind, d->down.data, d->down.row_bytes, d->width, d->hidden, xq2, tokens, tmp,
+                            d->width, MI_EPI_NONE, nullptr)))
+      return rc;
+    return launch_norm_add(s, resid, tmp, d->width, tokens, d->ffn_post_norm, d->eps);
+  }
+  return launch_matvec(s, d->down.kind, d->down.data, d->down.row_bytes, d->width, d->hidden, xq2, tokens, resid,
+                       d->width, MI_EPI_ADD, nullptr);
+}
 
 // The layer over a chunk of more than 8 tokens (a prompt chunk, cache stride
 // or index stride 0, or that many sequences): the same chain on f32
@@ -170,7 +263,12 @@ static int prefill_layer(hipStream_t s, const mi_layer_desc* d, float* resid, ui
   // attention_layer (block.mojo:319)
   auto tile = [&](const mi_weight& w) { return prefill_fits(w.kind, w.cols, w.row_bytes, w.data); };
   if ((rc = launch_rms_norm(s, resid, d->attn_norm, d->width, tokens, d->eps, xn, nullptr))) return rc;
-  if (tile(d->wq) && tile(d->wk) && tile(d->wv)) {
+  if (d->q_bias) {
+    // each projection with its bias in the epilogue (block.mojo:363-366)
+    if ((rc = mat(d->wq, qw, d->width, xn, qkv, qkv_stride, MI_EPI_BIAS, d->q_bias))) return rc;
+    if ((rc = mat(d->wk, kvw, d->width, xn, qkv + qw, qkv_stride, MI_EPI_BIAS, d->k_bias))) return rc;
+    if ((rc = mat(d->wv, kvw, d->width, xn, qkv + qw + kvw, qkv_stride, MI_EPI_BIAS, d->v_bias))) return rc;
+  } else if (tile(d->wq) && tile(d->wk) && tile(d->wv)) {
     // one activation prep for q, k and v; consecutive projections of one
     // kind as one launch over their rows end to end (q|k|v, or q|k and v
     // when v is of another kind, as in Q4_K_M files)
@@ -198,6 +296,11 @@ static int prefill_layer(hipStream_t s, const mi_layer_desc* d, float* resid, ui
     if ((rc = mat(d->wk, kvw, d->width, xn, qkv + qw, qkv_stride, MI_EPI_NONE, nullptr))) return rc;
     if ((rc = mat(d->wv, kvw, d->width, xn, qkv + qw + kvw, qkv_stride, MI_EPI_NONE, nullptr))) return rc;
   }
+  if (d->q_norm) {  // each head of q and k normed before rope (block.mojo:367-384)
+    if ((rc = launch_head_norm(s, qkv, d->heads, d->head_dim, tokens, qkv_stride, d->q_norm, d->eps))) return rc;
+    if ((rc = launch_head_norm(s, qkv + qw, d->kv_heads, d->head_dim, tokens, qkv_stride, d->k_norm, d->eps)))
+      return rc;
+  }
   if ((rc = launch_rope_store(s, qkv, d->heads, d->kv_heads, d->head_dim, d->rope_dim, d->neox, d->rope_steps, pos,
                               tokens, qkv_stride, k_cache, v_cache, cache_stride, d->rope_factors, d->cache_form,
                               kv_index, index_stride)))
@@ -206,9 +309,27 @@ static int prefill_layer(hipStream_t s, const mi_layer_desc* d, float* resid, ui
                           d->attn_scale, pos, -1, max_count, tokens, attn_out, nullptr, attn, d->cache_form,
                           kv_index, index_stride)))
     return rc;
-  if ((rc = mat(d->wo, d->width, qw, attn_out, resid, d->width, MI_EPI_ADD, nullptr))) return rc;
-  // mlp_layer (block.mojo:429), gated silu
+  if (d->attn_post_norm) {  // wo into xn (free once q, k, v are made), normed into the stream
+    if ((rc = mat(d->wo, d->width, qw, attn_out, xn, d->width, MI_EPI_NONE, nullptr))) return rc;
+    if ((rc = launch_norm_add(s, resid, xn, d->width, tokens, d->attn_post_norm, d->eps))) return rc;
+  } else if ((rc = mat(d->wo, d->width, qw, attn_out, resid, d->width, MI_EPI_ADD, nullptr))) {
+    return rc;
+  }
+  // mlp_layer (block.mojo:429)
   if ((rc = launch_rms_norm(s, resid, d->ffn_norm, d->width, tokens, d->eps, xn, nullptr))) return rc;
+  if (d->ungated || d->act || d->ffn_post_norm) {
+    if ((rc = mat(d->up, d->hidden, d->width, xn, up, d->hidden, MI_EPI_NONE, nullptr))) return rc;
+    float* act = up;
+    if (d->ungated) {
+      if ((rc = launch_act(s, up, (int64_t)d->hidden * tokens, d->act))) return rc;
+    } else {
+      if ((rc = mat(d->gate, d->hidden, d->width, xn, h, d->hidden, MI_EPI_GLU | d->act, up))) return rc;
+      act = h;
+    }
+    if (!d->ffn_post_norm) return mat(d->down, d->width, d->hidden, act, resid, d->width, MI_EPI_ADD, nullptr);
+    if ((rc = mat(d->down, d->width, d->hidden, act, xn, d->width, MI_EPI_NONE, nullptr))) return rc;
+    return launch_norm_add(s, resid, xn, d->width, tokens, d->ffn_post_norm, d->eps);
+  }
   if (tile(d->up) && tile(d->gate)) {  // one activation prep for both
     if ((rc = prefill_prepare(s, xn, d->width, tokens, mm))) return rc;
     if ((rc = launch_prefill_segs(s, d->up.kind, rows::one_matrix(d->up.data, d->up.row_bytes, d->hidden),
@@ -256,6 +377,9 @@ static int decoder_layer(mi_stream stream, const mi_layer_desc* d, float* resid,
 
   hipStream_t s = (hipStream_t)stream;
   char* base = (char*)work;
+  if (extended(d))
+    return extended_layer(s, d, resid, k_cache, v_cache, cache_stride, kv_index, index_stride, pos, max_count,
+                          tokens, base, c);
   void* xq = base + c.xq;
   float* qkv = (float*)(base + c.qkv);
   float* up = (float*)(base + c.up);

@@ -195,6 +195,14 @@ int launch_attend(hipStream_t s, const float* q, int64_t q_stride, const uint16_
                   int32_t max_count, int32_t tokens, float* out, void* xq_out, void* work,
                   int32_t form = MI_CACHE_F16, const int32_t* kv_index = nullptr, int64_t index_stride = 0);
 int launch_argmax(hipStream_t s, const float* x, int32_t n, int32_t tokens, int32_t* out);
+// The optional layer parts (ops.hip): per-head RMS norm of `heads` runs of n
+// in each of `tokens` rows row_stride apart, in place; resid[t] +=
+// rms_norm(y[t]) * gain; x = act(x) (silu, or gelu with MI_ACT_GELU).
+int launch_head_norm(hipStream_t s, float* x, int32_t heads, int32_t n, int32_t tokens, int64_t row_stride,
+                     const float* gain, float eps);
+int launch_norm_add(hipStream_t s, float* resid, const float* y, int32_t n, int32_t tokens, const float* gain,
+                    float eps);
+int launch_act(hipStream_t s, float* x, int64_t n, int32_t act);
 int launch_embed(hipStream_t s, const float* emb, int32_t vocab, int32_t width, const int32_t* ids,
                  int32_t tokens, float* out);
 

@@ -8,8 +8,11 @@
 // next projection needs no separate quantize launch.
 #include <math.h>
 
+#include <algorithm>
+
 #include "mi_internal.h"
 #include "xq_device.h"
+#include "matvec_units.h"
 
 namespace mi {
 namespace {
@@ -960,6 +963,50 @@ __global__ __launch_bounds__(NT) void attend_wide_kernel(
     *(float2*)(part_acc + (slot0 + (int64_t)g * max_chunks + c) * D + 2 * e) = make_float2(a0, a1);
 }
 
+// ---- the optional layer parts of other families ----------------------------
+// kernel.mojo:400 rms_norm_at over runs: every head of q (or k) in a row of
+// the fused q|k|v, in place (gpu_block.mojo device_rms_norm_run, Qwen 3's
+// per-head norms).  Block = one (head, token), 64 threads; float64 sum of
+// squares, f32 scale, x * scale * gain as rms_norm_kernel.
+__global__ __launch_bounds__(64) void head_norm_kernel(float* __restrict__ x, int64_t row_stride, int n,
+                                                       const float* __restrict__ gain, float eps) {
+#pragma clang fp contract(off)
+  float* run = x + (int64_t)blockIdx.y * row_stride + (int64_t)blockIdx.x * n;
+  double acc = 0.0;
+  for (int i = threadIdx.x; i < n; i += 64) acc += (double)run[i] * (double)run[i];
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) acc += __shfl_xor(acc, m);
+  const float scale = (float)(1.0 / sqrt(acc / (double)n + (double)eps));
+  for (int i = threadIdx.x; i < n; i += 64) run[i] = run[i] * scale * gain[i];
+}
+
+// A sublayer's output normed on its way into the residual stream
+// (gpu_block.mojo device_rms_norm_inplace then device_add_run, Gemma 2's post
+// norms): resid[t] += rms_norm(y[t]) * gain.  Block = one token, 256 threads.
+__global__ __launch_bounds__(256) void norm_add_kernel(float* __restrict__ resid, const float* __restrict__ y, int n,
+                                                       const float* __restrict__ gain, float eps) {
+#pragma clang fp contract(off)
+  const float* yr = y + (int64_t)blockIdx.x * n;
+  float* rr = resid + (int64_t)blockIdx.x * n;
+  double acc = 0.0;
+  for (int i = threadIdx.x; i < n; i += 256) acc += (double)yr[i] * (double)yr[i];
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) acc += __shfl_xor(acc, m);
+  __shared__ double part[4];
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = acc;
+  __syncthreads();
+  const double sum = part[0] + part[1] + part[2] + part[3];
+  const float scale = (float)(1.0 / sqrt(sum / (double)n + (double)eps));
+  for (int i = threadIdx.x; i < n; i += 256) rr[i] += yr[i] * scale * gain[i];
+}
+
+// The non-gated MLP's activation in place (gpu_block.mojo device_silu /
+// device_gelu): x = act(x) over n values.
+__global__ void act_kernel(float* __restrict__ x, int64_t n, int gelu_act) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+    x[i] = gelu_act ? mv::gelu(x[i]) : mv::silu(x[i]);
+}
+
 // ---- argmax ----------------------------------------------------------------
 // kernel.mojo:571: index of the maximum, ties to the lower index.
 __device__ __forceinline__ void better(float& v, int& i, float ov, int oi) {
@@ -1257,6 +1304,24 @@ int launch_embed(hipStream_t s, const float* emb, int32_t vocab, int32_t width, 
   dim3 grid((width / 4 + 255) / 256, tokens);
   hipLaunchKernelGGL(embed_kernel, grid, dim3(256), 0, s, emb, vocab, width, ids, out);
   return hip_check(hipGetLastError(), "embed launch");
+}
+
+int launch_head_norm(hipStream_t s, float* x, int32_t heads, int32_t n, int32_t tokens, int64_t row_stride,
+                     const float* gain, float eps) {
+  hipLaunchKernelGGL(head_norm_kernel, dim3(heads, tokens), dim3(64), 0, s, x, row_stride, n, gain, eps);
+  return hip_check(hipGetLastError(), "head_norm launch");
+}
+
+int launch_norm_add(hipStream_t s, float* resid, const float* y, int32_t n, int32_t tokens, const float* gain,
+                    float eps) {
+  hipLaunchKernelGGL(norm_add_kernel, dim3(tokens), dim3(256), 0, s, resid, y, n, gain, eps);
+  return hip_check(hipGetLastError(), "norm_add launch");
+}
+
+int launch_act(hipStream_t s, float* x, int64_t n, int32_t act) {
+  const int blocks = (int)std::min<int64_t>((n + 255) / 256, 2048);
+  hipLaunchKernelGGL(act_kernel, dim3(blocks), dim3(256), 0, s, x, n, (act & MI_ACT_GELU) ? 1 : 0);
+  return hip_check(hipGetLastError(), "act launch");
 }
 
 }  // namespace mi

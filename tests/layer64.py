@@ -98,7 +98,9 @@ def layer64(spec, weights, x, keys, values, slot, pos, interleave=False, parts=F
     heads_out = attend64(q, keys.reshape(-1), values.reshape(-1), slot + 1, H, KV, HD, spec["attn_scale"],
                          interleave)
     proj = W["wo"] @ heads_out
+    post = {}
     if opt["attn_post_norm"] is not None:
+        post["attn"] = (proj.copy(), opt["attn_post_norm"])
         proj = rms64(proj, opt["attn_post_norm"], eps)
     x = x + proj
     n = rms64(x, weights["ffn_norm"].astype(np.float64), eps)
@@ -110,10 +112,11 @@ def layer64(spec, weights, x, keys, values, slot, pos, interleave=False, parts=F
         act = fn(W["gate"] @ n) * u
     proj = W["down"] @ act
     if opt["ffn_post_norm"] is not None:
+        post["ffn"] = (proj.copy(), opt["ffn_post_norm"])
         proj = rms64(proj, opt["ffn_post_norm"], eps)
     out = x + proj
     if parts:
-        return out, {"W": W, "attn": heads_out, "act": act}
+        return out, {"W": W, "attn": heads_out, "act": act, "post": post, "eps": eps}
     return out
 
 
@@ -125,7 +128,18 @@ def layer_bound(parts, rel=1e-4):
     covers what the rounding upstream of them (norm, q|k|v, attention)
     moves their inputs by."""
     W = parts["W"]
-    return rel * (np.abs(W["wo"]) @ np.abs(parts["attn"]) + np.abs(W["down"]) @ np.abs(parts["act"]))
+    e_attn = np.abs(W["wo"]) @ np.abs(parts["attn"])
+    e_ffn = np.abs(W["down"]) @ np.abs(parts["act"])
+
+    def through_post(e, key):
+        # a post norm y * s * g (s = 1 / rms(y)) moves an error e in y by at
+        # most s |g| (e_i + |y_i| ||e|| / ||y||) per element
+        if key not in parts.get("post", {}):
+            return e
+        y, g = parts["post"][key]
+        s = 1.0 / np.sqrt(np.mean(y * y) + parts["eps"])
+        return s * np.abs(g) * (e + np.abs(y) * np.linalg.norm(e) / np.linalg.norm(y))
+    return rel * (through_post(e_attn, "attn") + through_post(e_ffn, "ffn"))
 
 
 def envelope_close(got, want, rel):
