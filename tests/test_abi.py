@@ -116,3 +116,25 @@ def test_layer_refuses_wrong_projection_shape():
     rc = lib.mi_decoder_layer(None, ctypes.byref(d), 0x100000, 0x100000, 0x100000, 0, 0x100000, 8, 1,
                               0x100000, 1 << 24)
     assert rc == -3 and "wk" in lib.mi_last_error().decode()
+
+
+def test_mojo_binding_covers_the_header():
+    """mojo/molla_mi.mojo binds every symbol include/molla_mi.h declares
+    (one external_call each) and lays out mi_layer_desc at the C offsets."""
+    import ctypes
+    import re
+    with open(os.path.join(ROOT, "mojo", "molla_mi.mojo")) as f:
+        text = f.read()
+    bound = set(re.findall(r'external_call\["(mi_[a-z0-9_]+)"', text))
+    missing = [n for n in declared_symbols() if n not in bound]
+    assert not missing, missing
+    D = _lib.MiLayerDesc
+    offsets = {"WEIGHTS": D.wq.offset, "ROPE_FACTORS": D.rope_factors.offset, "CACHE_FORM": D.cache_form.offset,
+               "Q_BIAS": D.q_bias.offset, "K_BIAS": D.k_bias.offset, "V_BIAS": D.v_bias.offset,
+               "Q_NORM": D.q_norm.offset, "K_NORM": D.k_norm.offset, "ATTN_POST_NORM": D.attn_post_norm.offset,
+               "FFN_POST_NORM": D.ffn_post_norm.offset, "UNGATED": D.ungated.offset, "ACT": D.act.offset,
+               "SIZE": ctypes.sizeof(D)}
+    for name, want in offsets.items():
+        m = re.search(rf"comptime {name} = (\d+)", text)
+        assert m and int(m.group(1)) == want, (name, want)
+    assert ctypes.sizeof(_lib.MiWeight) == 32
