@@ -94,7 +94,9 @@ int mi_dequant(mi_stream stream, int kind, const void* w, int64_t count, float* 
  * head of the configs).  Activations are carried as 23-bit block fixed point
  * per 32 values (three int8 limbs), so every product is an exact integer dot;
  * the result agrees with the fp32 host path to ~1e-7 relative.
- * Workspace: mi_matvec_workspace(cols, tokens) bytes, 256-byte aligned.
+ * Workspace: mi_matvec_workspace(cols, tokens) bytes, 256-byte aligned (at
+ * 2..8 tokens the activations twice over: the int8-limb form and, for the
+ * f16 matrix-core tile, the same integers as pairs of halves).
  *
  * tokens 9..65536 is the prefill matmul (device_matmul_into at a prompt
  * chunk, gpu.mojo:1695 PREFILL_CHUNK; the tile of gpu.mojo:2665): matrix
@@ -133,7 +135,8 @@ int mi_matvec_xq(mi_stream stream, int kind, const void* w, int64_t row_bytes,
 /* ---- block ops (src/molla/nn/gpu_ops.mojo) --------------------------------
  * rms_norm: out[t] = x[t] * rsqrt(mean(x[t]^2) + eps) * gain, sum of squares in
  * float64 as the host does (kernel.mojo:432-467).  If xq is non-NULL the
- * normalised row is also quantized for a following mi_matvec_xq. */
+ * normalised row is also quantized for a following mi_matvec_xq (xq holds
+ * mi_matvec_workspace(n, tokens) bytes). */
 int mi_rms_norm(mi_stream stream, const float* x, const float* gain, int32_t n,
                 int32_t tokens, float eps, float* out, void* xq);
 

@@ -1,0 +1,357 @@
+// matvec_htile.hip -- the batched (2..8 tokens) Q4_K matvec on the f16
+// matrix cores (v_mfma_f32_16x16x32_f16), gfx950.
+//
+// The int8 tile (matvec_tile.hip) multiplies exactly but has to recombine
+// three activation limbs per (row, token, group) on the VALU afterwards.
+// This tile feeds the matrix core half-precision numbers that are exact, so
+// everything after the MFMA is one scale per superblock:
+//
+//  * Activations ("hx" form, written next to the xq form by its producers,
+//    xq_device.h quantize_group32): the xq integers X of a group split into
+//    two halves hi + lo = X * 2^-8 exactly (X has at most 22 significant
+//    bits; hi carries the top 11, lo the rest).  The tile rescales each
+//    group to its superblock's largest group scale (a power of two, so exact
+//    while the group is within 2^16 of the largest).
+//  * Weights enter as the integer codes sc * q (at most 63 * 15), exact in
+//    half precision, so every product is exact and d scales the superblock's
+//    sum once.
+//  * The min term dmin * sum_g m_g * sum(x in group g) is one more MFMA per
+//    superblock: the 8 mins of a row against the 8 group sums of each column
+//    (each sum divided by 256 and split into two halves, hi and lo, so 16 of
+//    the 32 k slots).
+//
+// MFMA fragments (16x16x32): lane l holds row / column l % 16 and values
+// 8 (l / 16) .. +8 of the 32; result element i of lane l is row 4 (l / 16) +
+// i, column l % 16.  Here M = 16 rows of the tile, N = 16 columns: token t
+// hi (2t) and lo (2t + 1), K = the 32 values of one Q4_K group (group 2h + e
+// of a superblock is the low (e = 0) or high nibbles of bytes 32h..32h+31;
+// lane l supplies bytes 32h + 8 (l / 16) .. +8).
+//
+// Work decomposition: a block is cols / 512 waves, wave w owning superblocks
+// 2w, 2w + 1 (512 values) of every row: it builds its activation fragments
+// once and keeps them in registers for every tile the block takes.  Blocks
+// loop over 16-row tiles (tile, tile + gridDim.x, ...).  A tile's 16 rows are
+// one run of memory: the block reads it with contiguous loads into LDS (a
+// fragment read straight from memory touches 16 rows per instruction, a
+// part of a cache line each, at about half the speed), keeping the next
+// tile's weights in flight while it computes the current one.  The waves'
+// partial sums meet in LDS, where 16 * tokens (row, token) sums add them in
+// a fixed order and apply the epilogue.
+//
+// Replaces the batched planar_matmul_kernel (src/molla/nn/gpu.mojo:1809) for
+// Q4_K; output y[t * ldy + r] and epilogues as gpu.mojo:1005.
+#include "matvec_rows.h"
+
+namespace mi {
+namespace {
+using namespace mv;
+
+typedef _Float16 hh8 __attribute__((ext_vector_type(8)));
+typedef _Float16 hh2 __attribute__((ext_vector_type(2)));
+typedef float ff4 __attribute__((ext_vector_type(4)));
+typedef uint32_t uu4 __attribute__((ext_vector_type(4)));
+
+constexpr int kSBW = 2;                                  // superblocks per wave
+constexpr int kMaxHWaves = 8;                            // cols <= 8 * 512
+constexpr int kRowPad = 32;                              // LDS rows 8 banks apart
+constexpr int kMaxRowBytes = kMaxHWaves * kSBW * 144;    // cols = 4096
+constexpr int kLdsRow = kMaxRowBytes + kRowPad;
+constexpr int kLoads = kSBW * 144 * 16 / (64 * 8);       // 8-byte loads per lane per tile
+
+__device__ __forceinline__ ff4 mfma16(hh8 a, hh8 b, ff4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ hh8 as_hh8(uint4 u) { return __builtin_bit_cast(hh8, u); }
+__device__ __forceinline__ hh2 as_hh2(uint32_t u) { return __builtin_bit_cast(hh2, u); }
+__device__ __forceinline__ uint32_t as_u32(hh2 h) { return __builtin_bit_cast(uint32_t, h); }
+
+// Two bytes of x (picked by the perm selector) as the halves 1024 + byte:
+// 0x64 above a byte is the exponent of 1024, the byte the mantissa.
+__device__ __forceinline__ uint32_t magic2(uint32_t x, uint32_t sel) {
+  return __builtin_amdgcn_perm(0x64646464u, x, sel);
+}
+constexpr uint32_t kSel01 = 0x04010400u, kSel23 = 0x04030402u;
+__device__ __forceinline__ uint32_t sel_splat(int k) { return 0x04000400u | ((uint32_t)k << 16) | (uint32_t)k; }
+
+// sc * u for the eight nibble codes u in the bytes of t0, t1: (1024 + u) *
+// sc - 1024 * sc, one rounding of an exact small integer.
+__device__ __forceinline__ hh8 codes8(uint32_t t0, uint32_t t1, hh2 sc, hh2 nsc) {
+  uint4 o;
+  o.x = as_u32(__builtin_elementwise_fma(as_hh2(magic2(t0, kSel01)), sc, nsc));
+  o.y = as_u32(__builtin_elementwise_fma(as_hh2(magic2(t0, kSel23)), sc, nsc));
+  o.z = as_u32(__builtin_elementwise_fma(as_hh2(magic2(t1, kSel01)), sc, nsc));
+  o.w = as_u32(__builtin_elementwise_fma(as_hh2(magic2(t1, kSel23)), sc, nsc));
+  return as_hh8(o);
+}
+
+// The 6-bit scales and mins of groups 0..7 from scales[0..11] held in y, z,
+// w (quant.mojo:161 _k_scale), four to a dword: sc0..3, sc4..7, m0..3, m4..7.
+__device__ __forceinline__ void kscales(uint32_t y, uint32_t z, uint32_t w, uint32_t& sc_lo, uint32_t& sc_hi,
+                                        uint32_t& m_lo, uint32_t& m_hi) {
+  sc_lo = y & 0x3F3F3F3Fu;
+  m_lo = z & 0x3F3F3F3Fu;
+  sc_hi = (w & 0x0F0F0F0Fu) | ((y >> 2) & 0x30303030u);
+  m_hi = ((w >> 4) & 0x0F0F0F0Fu) | ((z >> 2) & 0x30303030u);
+}
+
+// The partial product of superblock `sb` of the 16 rows in LDS (lrows: row
+// 0 of the tile) for this lane's result rows 4 kq + i, column lm:
+// esc * (d * C - dmin * Cmin).  bm is this lane's fragment of the group sums
+// (the min MFMA's B), which are held divided by 256.
+__device__ __forceinline__ void sb_product(const uint8_t* lrows, int sb, const hh8 (&b)[8], hh8 bm, float esc,
+                                           int lm, int kq, ff4& acc) {
+  const uint8_t* lrow = lrows + lm * kLdsRow + sb * 144;
+  const uint4 h = *(const uint4*)lrow;
+  uint2 q[4];
+#pragma unroll
+  for (int k = 0; k < 4; k++) q[k] = *(const uint2*)(lrow + 16 + 32 * k + 8 * kq);
+  uint32_t dd[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) dd[i] = *(const uint32_t*)(lrows + (4 * kq + i) * kLdsRow + sb * 144);
+
+  uint32_t sc_lo, sc_hi, m_lo, m_hi;
+  kscales(h.y, h.z, h.w, sc_lo, sc_hi, m_lo, m_hi);
+  const hh2 k1024 = {(_Float16)-1024.0f, (_Float16)-1024.0f};
+  ff4 c = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int j = 0; j < 8; j++) {
+    const hh2 sc = as_hh2(magic2(j < 4 ? sc_lo : sc_hi, sel_splat(j & 3))) + k1024;
+    const hh2 nsc = sc * k1024;
+    const uint32_t t0 = q[j >> 1].x, t1 = q[j >> 1].y;
+    const uint32_t u0 = (j & 1) ? (t0 >> 4) & 0x0F0F0F0Fu : t0 & 0x0F0F0F0Fu;
+    const uint32_t u1 = (j & 1) ? (t1 >> 4) & 0x0F0F0F0Fu : t1 & 0x0F0F0F0Fu;
+    c = mfma16(codes8(u0, u1, sc, nsc), b[j], c);
+  }
+  // the mins of groups 0..7 as this lane's A fragment: k 0..7 and 8..15
+  // (the hi and lo group sums) both take m0..m7; k 16..31 are zero
+  const uint4 am = make_uint4(magic2(m_lo, kSel01), magic2(m_lo, kSel23), magic2(m_hi, kSel01),
+                              magic2(m_hi, kSel23));
+  const _Float16 n = (_Float16)-1024.0f;
+  hh8 a_m = as_hh8(am) + hh8{n, n, n, n, n, n, n, n};
+  if (kq >= 2) a_m = hh8{0, 0, 0, 0, 0, 0, 0, 0};
+  const ff4 cm = mfma16(a_m, bm, ff4{0.0f, 0.0f, 0.0f, 0.0f});
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const float di = half_bits_to_float(dd[i]), mi_ = half_bits_to_float(dd[i] >> 16);
+    acc[i] = fmaf(esc, fmaf(di, c[i], -256.0f * mi_ * cm[i]), acc[i]);
+  }
+}
+
+template <int TN>
+__global__ __launch_bounds__(kMaxHWaves * 64) void q4k_htile_kernel(const RowSegs sg, int cols,
+                                                                     const uint8_t* __restrict__ xq,
+                                                                     const uint8_t* __restrict__ hx,
+                                                                     float* __restrict__ y, int64_t ldy, int epi,
+                                                                     const float* __restrict__ aux) {
+  __shared__ __align__(16) uint8_t wl[2][16 * kLdsRow];
+  __shared__ float part[2][kMaxHWaves][16][17];
+  __shared__ __align__(16) uint8_t sink[16];  // target of the copies' idle lanes
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  const int lm = lane & 15, kq = lane >> 4;
+  const int rows = sg.end[sg.nseg - 1];
+  const int tiles = (rows + 15) >> 4;
+  const int G = cols >> 5;
+  const int rb = (cols >> 8) * 144;  // bytes per row; the tile is 16 rows in a run
+  const int64_t tok_bytes = xq_token_bytes(cols);
+  const int step = gridDim.x;
+
+  // This lane's share of a tile: 8-byte words threadIdx.x + blockDim.x * j,
+  // and where each lands in the padded LDS rows.
+  int ldso[kLoads];
+#pragma unroll
+  for (int j = 0; j < kLoads; j++) {
+    // o / rb through a float reciprocal (o < 2^16: exact after one
+    // correction), not the long integer division sequence
+    const int o = 8 * ((int)threadIdx.x + (int)blockDim.x * j);
+    int row = (int)((float)o * (1.0f / (float)rb));
+    row -= row * rb > o;
+    row += (row + 1) * rb <= o;
+    ldso[j] = row * kLdsRow + (o - row * rb);
+  }
+  // A last tile of fewer than 16 rows reads its last word again in place of
+  // the missing rows (whose sums are never stored): loads stay unconditional.
+  auto load_tile = [&](uint2 (&r)[kLoads], int tl) __attribute__((always_inline)) {
+    const uint2* src = (const uint2*)rows::seg_row(sg, tl * 16);
+    const int words = min(16, rows - tl * 16) * (rb >> 3);
+#pragma unroll
+    for (int j = 0; j < kLoads; j++) r[j] = src[min((int)threadIdx.x + (int)blockDim.x * j, words - 1)];
+  };
+  auto store_tile = [&](const uint2 (&r)[kLoads], int buf) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < kLoads; j++) *(uint2*)(wl[buf] + ldso[j]) = r[j];
+  };
+
+  // Activation fragments: token t = lm / 2, hi (lm even) or lo, groups of
+  // the wave's superblocks; columns of absent tokens are zero.  The block
+  // copies the group scales and the whole hx form into registers with
+  // contiguous loads, all issued before tile 0's weights (loads queue in
+  // order, and these are the ones the first tile waits for), then passes
+  // them through LDS in chunks of `cw` waves' superblocks that fit the
+  // weight buffers' space; each lane reads its fragments there.  (Per-lane
+  // gathers of the fragments straight from memory, or a copy loop that
+  // waits on each load, cost several times longer.)
+  const int t = lm >> 1, part_hl = lm & 1;
+  const bool live_col = t < TN;
+  const int wave_bytes = kSBW * 8 * 128;  // one token's hx for one wave
+  // 16-byte word tid + j * blockDim.x of the block's hx is word tid +
+  // (j & 1) * blockDim.x of token j / 2 (a token is 2 * blockDim.x words)
+  uu4 v[2 * TN];
+#pragma unroll
+  for (int j = 0; j < 2 * TN; j++) {
+    const int u = j >> 1, w = (int)threadIdx.x + (j & 1) * (int)blockDim.x;
+    v[j] = *(const uu4*)(hx + u * tok_bytes + w * 16);
+  }
+  const float* scale_src = &((const XMeta*)(xq + 6 * (int64_t)G * 16))->scale;
+  float scl[TN];  // thread g < G: group g's scale of every token
+  const int sg_g = min((int)threadIdx.x, G - 1);
+#pragma unroll
+  for (int u = 0; u < TN; u++) scl[u] = scale_src[u * (tok_bytes / 4) + sg_g * 4];
+  uint2 ra[kLoads], rb_[kLoads];
+  load_tile(ra, blockIdx.x);  // the grid is at most `tiles` blocks
+  if (blockIdx.x + step < tiles) load_tile(rb_, blockIdx.x + step);
+
+  hh8 b[kSBW][8];
+  float sc8[kSBW][8];
+  {
+    float* lsc = (float*)part;  // TN * G scales; part is free until the first tile
+#pragma unroll
+    for (int u = 0; u < TN; u++) *((int)threadIdx.x < G ? &lsc[u * G + threadIdx.x] : (float*)sink) = scl[u];
+    const int cw = min(nw, (int)sizeof(wl) / (TN * (wave_bytes + 128)));
+    for (int w0 = 0; w0 < nw; w0 += cw) {
+      const int nwc = min(cw, nw - w0);
+      const int tstride = nwc * wave_bytes + 128;  // 128 extra: tokens 32 banks apart
+      uint8_t* lhx = &wl[0][0];
+      if (w0) __syncthreads();  // the previous chunk has been read
+#pragma unroll
+      for (int j = 0; j < 2 * TN; j++) {
+        const int u = j >> 1;
+        const int o = ((int)threadIdx.x + (j & 1) * (int)blockDim.x) * 16 - w0 * wave_bytes;  // inside the chunk
+        *(uu4*)(o >= 0 && o < nwc * wave_bytes ? lhx + u * tstride + o : sink) = v[j];
+      }
+      __syncthreads();
+      if (wave >= w0 && wave < w0 + nwc) {
+#pragma unroll
+        for (int s = 0; s < kSBW; s++)
+#pragma unroll
+          for (int g = 0; g < 8; g++) {
+            sc8[s][g] = live_col ? lsc[t * G + (wave * kSBW + s) * 8 + g] : 0.0f;
+            b[s][g] = live_col ? as_hh8(*(const uint4*)(lhx + t * tstride + (wave - w0) * wave_bytes +
+                                                        (s * 8 + g) * 128 + (kq * 2 + part_hl) * 16))
+                               : hh8{0, 0, 0, 0, 0, 0, 0, 0};
+          }
+      }
+    }
+    __syncthreads();  // every fragment read before the buffers take weights
+  }
+  // Rescale each group to its superblock's largest scale (2^(e_g - e_sb),
+  // exact) and form the min MFMA's B: column lm's group sums (divided by
+  // 256: a sum reaches 2^19, past the largest half), hi in k 0..7 (lanes
+  // kq = 0), lo in k 8..15 (kq = 1), zero above.  A group's column sums come
+  // from the matrix core too: a block of ones times the group's fragment.
+  float esc[kSBW];
+  hh8 bm[kSBW];
+  const hh8 ones = {1, 1, 1, 1, 1, 1, 1, 1};
+#pragma unroll
+  for (int s = 0; s < kSBW; s++) {
+    float emax = 0.0f;
+#pragma unroll
+    for (int g = 0; g < 8; g++) emax = fmaxf(emax, sc8[s][g]);
+    esc[s] = 256.0f * emax;
+    const float inv = emax > 0.0f ? __builtin_amdgcn_rcpf(emax) : 0.0f;  // exact: a power of two
+    hh8 hv, lv;
+#pragma unroll
+    for (int g = 0; g < 8; g++) {
+      const _Float16 f = (_Float16)(sc8[s][g] * inv);
+      b[s][g] = b[s][g] * hh8{f, f, f, f, f, f, f, f};
+      const float gs = mfma16(ones, b[s][g], ff4{0.0f, 0.0f, 0.0f, 0.0f})[0] * (1.0f / 256.0f);
+      hv[g] = (_Float16)gs;
+      lv[g] = (_Float16)(gs - (float)hv[g]);
+    }
+    bm[s] = kq == 0 ? hv : (kq == 1 ? lv : hh8{0, 0, 0, 0, 0, 0, 0, 0});
+  }
+
+  // (row r, token u) sums of tile tl over the waves, in wave order, hi + lo,
+  // and the epilogue; the 16 * TN sums are dealt round the waves, so that
+  // no wave comes late to the next barrier.
+  auto finish = [&](int tl, int buf) __attribute__((always_inline)) {
+    for (int ix = lane * nw + wave; ix < 16 * TN; ix += 64 * nw) {
+      const int rr = ix & 15, u = ix >> 4;
+      float v = 0.0f;
+#pragma unroll
+      for (int w = 0; w < kMaxHWaves; w++)
+        if (w < nw) v += part[buf][w][rr][2 * u] + part[buf][w][rr][2 * u + 1];
+      const int row = tl * 16 + rr;
+      if (row < rows) epilogue(y, aux, epi, (int64_t)u * ldy + row, row, v);
+    }
+  };
+
+  // Tile k of this block is computed from LDS buffer k & 1 while tiles
+  // k + 1 and k + 2 are in flight in the two register sets; then tile k + 1
+  // goes into the other buffer and its registers send for tile k + 3.  With
+  // buffers alternating, one barrier per tile keeps every buffer from being
+  // overwritten before it has been read.
+  int tl = blockIdx.x, k = 0;
+  store_tile(ra, 0);
+  if (tl + 2 * step < tiles) load_tile(ra, tl + 2 * step);
+  auto step_tile = [&](uint2 (&rn)[kLoads]) __attribute__((always_inline)) {
+    __syncthreads();
+    if (k > 0) finish(tl - step, (k - 1) & 1);
+    ff4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int s = 0; s < kSBW; s++) sb_product(wl[k & 1], wave * kSBW + s, b[s], bm[s], esc[s], lm, kq, acc);
+#pragma unroll
+    for (int i = 0; i < 4; i++) part[k & 1][wave][4 * kq + i][lm] = acc[i];
+    if (tl + step >= tiles) return false;
+    store_tile(rn, (k + 1) & 1);  // tile k + 1
+    if (tl + 3 * step < tiles) load_tile(rn, tl + 3 * step);
+    tl += step;
+    k++;
+    return true;
+  };
+  while (step_tile(rb_) && step_tile(ra)) {
+  }
+  __syncthreads();
+  finish(tl, k & 1);
+}
+
+int cu_count_h() {
+  static int cus[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cus[dev]) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cus[dev] = n;
+  }
+  return cus[dev];
+}
+
+}  // namespace
+
+bool q4k_htile_fits(int32_t rows, int32_t cols, int32_t tokens) {
+  return tokens >= 2 && tokens <= kMaxTokens && cols % (256 * kSBW) == 0 && cols / (256 * kSBW) <= kMaxHWaves &&
+         rows > 0;
+}
+
+int launch_q4k_htile(hipStream_t s, const RowSegs& sg, int32_t rows, int32_t cols, const void* xq, const void* hx,
+                     int32_t tokens, float* y, int64_t ldy, int32_t epi, const float* aux) {
+  for (int i = 0; i < sg.nseg; i++)
+    if ((i < sg.nseg - 1 && sg.end[i] % 16) || sg.rb[i] != (int64_t)(cols / 256) * 144)
+      return fail(MI_ERR_SHAPE, "htile: segments must be whole 16-row tiles of %d-column rows", cols);
+  const int waves = cols / (256 * kSBW);
+  const int grid = std::min((rows + 15) / 16, cu_count_h());
+#define MI_HT(T)                                                                                         \
+  case T:                                                                                                \
+    hipLaunchKernelGGL(q4k_htile_kernel<T>, dim3(grid), dim3(waves * 64), 0, s, sg, cols, (const uint8_t*)xq, \
+                       (const uint8_t*)hx, y, ldy, epi, aux);                                            \
+    break;
+  switch (tokens) {
+    MI_HT(2) MI_HT(3) MI_HT(4) MI_HT(5) MI_HT(6) MI_HT(7) MI_HT(8)
+    default: return fail(MI_ERR_ARG, "htile: %d tokens", tokens);
+  }
+#undef MI_HT
+  return hip_check(hipGetLastError(), "htile launch");
+}
+
+}  // namespace mi

@@ -84,11 +84,16 @@ struct XUnitRegs {
   __device__ __forceinline__ int2 lsum23(int, int g) const { return s23[L23 ? (g & 1) : 0]; }
 };
 
-// Row `row` of the segmented matrix: base address of its blocks.
+// Row `row` of the segmented matrix: base address of its blocks.  The
+// segment fields are picked by constant index: indexing the kernel-argument
+// arrays with a per-lane value would fetch them with vector loads, whose
+// wait (vmcnt) then also waits for every weight load already in flight.
 __device__ __forceinline__ const uint8_t* seg_row(const RowSegs& sg, int row) {
-  const int s = row < sg.end[0] ? 0 : (row < sg.end[1] ? 1 : 2);
-  const int start = s == 0 ? 0 : sg.end[s - 1];
-  return sg.w[s] + (int64_t)(row - start) * sg.rb[s];
+  const bool s0 = row < sg.end[0], s1 = !s0 && row < sg.end[1];
+  const uint8_t* w = s0 ? sg.w[0] : (s1 ? sg.w[1] : sg.w[2]);
+  const int64_t rb = s0 ? sg.rb[0] : (s1 ? sg.rb[1] : sg.rb[2]);
+  const int start = s0 ? 0 : (s1 ? sg.end[0] : sg.end[1]);
+  return w + (int64_t)(row - start) * rb;
 }
 
 // The activation of unit u (groups 2u, 2u + 1) into a lane's registers.

@@ -52,7 +52,9 @@ int allow_lds(const void* fn, int bytes, bool* done, const char* what);
 // ---- launchers (no validation beyond what the kernel itself assumes; the
 // ---- C-ABI layer in shim.cpp checks shapes before calling these) ----------
 int launch_dequant(hipStream_t s, int kind, const void* w, int64_t count, float* out);
-int launch_quantize(hipStream_t s, const float* x, int32_t cols, int32_t tokens, void* xq);
+// hx: when not null, also the hx form of the same tokens (xq_device.h
+// hx_group32), which the f16 matrix-core tile reads.
+int launch_quantize(hipStream_t s, const float* x, int32_t cols, int32_t tokens, void* xq, void* hx = nullptr);
 // Batch-1 Q4_K / Q4_0 / Q8_0 matvec (matvec_rows.hip); launch_matvec routes
 // there itself.  _segs: rows of up to three Q4_K matrices of width cols
 // numbered end to end (a layer's q, k, v into one fused row).  _glu:
@@ -152,7 +154,13 @@ int matmul_tokens(hipStream_t s, int kind, const void* w, int64_t row_bytes, int
 // matvec_kernel.h.
 int launch_matvec(hipStream_t s, int kind, const void* w, int64_t row_bytes, int32_t rows,
                   int32_t cols, const void* xq, int32_t tokens, float* y, int64_t ldy, int32_t epi,
-                  const float* aux);
+                  const float* aux, const void* hx = nullptr);
+// The f16 matrix-core tile for 2..8 tokens (matvec_htile.hip): Q4_K rows of
+// up to three matrices whose ends (but the last) are whole 16-row tiles,
+// reading the xq form (group scales) and the hx form of the same tokens.
+bool q4k_htile_fits(int32_t rows, int32_t cols, int32_t tokens);
+int launch_q4k_htile(hipStream_t s, const RowSegs& sg, int32_t rows, int32_t cols, const void* xq, const void* hx,
+                     int32_t tokens, float* y, int64_t ldy, int32_t epi, const float* aux);
 // rms_norm_trig: also writes trig[p] = (cos, sin) of f32(pos[0]) * steps[p]
 // (divided by factors[p] when factors is given) for p < pairs (float64 trig,
 // as rope.mojo:253-285), for the fused q|k|v epilogue of the same layer.
@@ -160,7 +168,7 @@ int launch_rms_norm_trig(hipStream_t s, const float* x, const float* gain, int32
                          const int32_t* pos, const float* steps, const float* factors, int32_t pairs,
                          float* trig);
 int launch_rms_norm(hipStream_t s, const float* x, const float* gain, int32_t n, int32_t tokens,
-                    float eps, float* out, void* xq);
+                    float eps, float* out, void* xq, void* hx = nullptr);
 // factors: rope_freqs.weight (one per pair), or null for none.
 int launch_rope(hipStream_t s, float* x, int32_t heads, int32_t head_dim, int32_t dim, int32_t neox,
                 const float* steps, const int32_t* pos, int32_t tokens, int64_t row_stride,

@@ -36,6 +36,7 @@ __global__ __launch_bounds__(kNormThreads) void rms_norm_kernel(const float* __r
                                                                 const float* __restrict__ gain, int n,
                                                                 float eps, float* __restrict__ out,
                                                                 uint8_t* __restrict__ xq,
+                                                                uint8_t* __restrict__ hx,
                                                                 const int32_t* __restrict__ pos,
                                                                 const float* __restrict__ steps,
                                                                 const float* __restrict__ factors, int pairs,
@@ -80,7 +81,9 @@ __global__ __launch_bounds__(kNormThreads) void rms_norm_kernel(const float* __r
   if (out && live) out[(int64_t)t * n + mine] = v;
   // A half-wave is one 32-value group; n is a multiple of 32 whenever xq
   // is asked for, so a group is either entirely live or entirely past the end.
-  if (xq) quantize_group32(v, threadIdx.x & 31, mine >> 5, n >> 5, xq + (int64_t)t * xq_token_bytes(n), live);
+  if (xq)
+    quantize_group32(v, threadIdx.x & 31, mine >> 5, n >> 5, xq + (int64_t)t * xq_token_bytes(n), live,
+                     hx ? hx + (int64_t)t * xq_token_bytes(n) : nullptr);
 }
 
 // One q8_0 block of a cache row: the 32 lanes of a half-wave each bring one
@@ -1094,13 +1097,13 @@ __global__ void embed_kernel(const float* __restrict__ emb, int vocab, int width
 }  // namespace
 
 static int norm_launch(hipStream_t s, const float* x, const float* gain, int32_t n, int32_t tokens, float eps,
-                       float* out, void* xq, const int32_t* pos, const float* steps, const float* factors,
+                       float* out, void* xq, void* hx, const int32_t* pos, const float* steps, const float* factors,
                        int32_t pairs, float* trig) {
   const int per = (n + kNormThreads - 1) / kNormThreads;
   dim3 grid(per, tokens);
 #define MI_NORM(P)                                                                                      \
   hipLaunchKernelGGL(rms_norm_kernel<P>, grid, dim3(kNormThreads), 0, s, x, gain, n, eps, out, (uint8_t*)xq, \
-                     pos, steps, factors, pairs, (float2*)trig)
+                     (uint8_t*)hx, pos, steps, factors, pairs, (float2*)trig)
   if (per <= 4) MI_NORM(4);
   else if (per <= 8) MI_NORM(8);
   else if (per <= 16) MI_NORM(16);
@@ -1112,14 +1115,14 @@ static int norm_launch(hipStream_t s, const float* x, const float* gain, int32_t
 }
 
 int launch_rms_norm(hipStream_t s, const float* x, const float* gain, int32_t n, int32_t tokens, float eps,
-                    float* out, void* xq) {
-  return norm_launch(s, x, gain, n, tokens, eps, out, xq, nullptr, nullptr, nullptr, 0, nullptr);
+                    float* out, void* xq, void* hx) {
+  return norm_launch(s, x, gain, n, tokens, eps, out, xq, hx, nullptr, nullptr, nullptr, 0, nullptr);
 }
 
 int launch_rms_norm_trig(hipStream_t s, const float* x, const float* gain, int32_t n, float eps, void* xq,
                          const int32_t* pos, const float* steps, const float* factors, int32_t pairs,
                          float* trig) {
-  return norm_launch(s, x, gain, n, 1, eps, nullptr, xq, pos, steps, factors, pairs, trig);
+  return norm_launch(s, x, gain, n, 1, eps, nullptr, xq, nullptr, pos, steps, factors, pairs, trig);
 }
 
 int launch_rope(hipStream_t s, float* x, int32_t heads, int32_t head_dim, int32_t dim, int32_t neox,

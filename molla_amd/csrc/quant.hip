@@ -127,7 +127,7 @@ __global__ void dequant_kernel(int kind, const uint8_t* __restrict__ w, int64_t 
 // Quantize x (tokens rows of cols floats) into the xq layout.  Each 32-lane
 // half of a wave owns one group.
 __global__ void quantize_kernel(const float* __restrict__ x, int32_t cols, int32_t tokens,
-                                uint8_t* __restrict__ xq) {
+                                uint8_t* __restrict__ xq, uint8_t* __restrict__ hx) {
   const int G = cols >> 5;
   const int64_t gg = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 5;  // global group
   const int lane32 = threadIdx.x & 31;
@@ -135,7 +135,8 @@ __global__ void quantize_kernel(const float* __restrict__ x, int32_t cols, int32
   const int64_t t = live ? gg / G : 0;
   const int g = live ? (int)(gg - t * G) : 0;
   float v = live ? x[t * cols + (int64_t)g * 32 + lane32] : 0.0f;
-  quantize_group32(v, lane32, g, G, xq + t * xq_token_bytes(cols), live);
+  quantize_group32(v, lane32, g, G, xq + t * xq_token_bytes(cols), live,
+                   hx ? hx + t * xq_token_bytes(cols) : nullptr);
 }
 
 }  // namespace
@@ -150,12 +151,12 @@ int launch_dequant(hipStream_t s, int kind, const void* w, int64_t count, float*
   return hip_check(hipGetLastError(), "dequant launch");
 }
 
-int launch_quantize(hipStream_t s, const float* x, int32_t cols, int32_t tokens, void* xq) {
+int launch_quantize(hipStream_t s, const float* x, int32_t cols, int32_t tokens, void* xq, void* hx) {
   int64_t lanes = (int64_t)(cols / 32) * tokens * 32;
   int threads = 256;
   int64_t blocks = (lanes + threads - 1) / threads;
   hipLaunchKernelGGL(quantize_kernel, dim3((unsigned)blocks), dim3(threads), 0, s, x, cols, tokens,
-                     (uint8_t*)xq);
+                     (uint8_t*)xq, (uint8_t*)hx);
   return hip_check(hipGetLastError(), "quantize launch");
 }
 

@@ -144,7 +144,13 @@ int mi_dequant(mi_stream stream, int kind, const void* w, int64_t count, float* 
 size_t mi_matvec_workspace(int32_t cols, int32_t tokens) {
   if (cols <= 0 || tokens <= 0 || tokens > kMaxPrefill) return 0;
   if (tokens > kMaxTokens) return prefill_prep_bytes(cols, tokens);
-  return (size_t)xq_token_bytes(cols) * (size_t)tokens;
+  // 2..8 tokens: the xq form, then the hx form the f16 matrix-core tile reads
+  return (size_t)xq_token_bytes(cols) * (size_t)tokens * (tokens > 1 ? 2 : 1);
+}
+
+// The hx form inside an activation workspace of 2..8 tokens, or null.
+static void* hx_of(const void* xq, int32_t cols, int32_t tokens) {
+  return tokens > 1 ? (uint8_t*)xq + xq_token_bytes(cols) * tokens : nullptr;
 }
 
 size_t mi_matmul_workspace(int32_t rows, int32_t cols, int32_t tokens) {
@@ -165,7 +171,7 @@ int mi_quantize(mi_stream stream, const float* x, int32_t cols, int32_t tokens, 
   if (!x) return fail(MI_ERR_ARG, "quantize: null input");
   int rc = check_xq("quantize", xq, cols, tokens);
   if (rc) return rc;
-  return launch_quantize((hipStream_t)stream, x, cols, tokens, xq);
+  return launch_quantize((hipStream_t)stream, x, cols, tokens, xq, hx_of(xq, cols, tokens));
 }
 
 int mi_matvec_xq(mi_stream stream, int kind, const void* w, int64_t row_bytes, int32_t rows,
@@ -178,7 +184,8 @@ int mi_matvec_xq(mi_stream stream, int kind, const void* w, int64_t row_bytes, i
     return fail(MI_ERR_ARG, "matvec: unknown epilogue bits 0x%x", epi);
   if ((epi & MI_EPI_BIAS) && (epi & MI_EPI_GLU)) return fail(MI_ERR_ARG, "matvec: BIAS and GLU together");
   if ((epi & (MI_EPI_BIAS | MI_EPI_GLU)) && !aux) return fail(MI_ERR_ARG, "matvec: epilogue needs aux");
-  return launch_matvec((hipStream_t)stream, kind, w, row_bytes, rows, cols, xq, tokens, y, rows, epi, aux);
+  return launch_matvec((hipStream_t)stream, kind, w, row_bytes, rows, cols, xq, tokens, y, rows, epi, aux,
+                       hx_of(xq, cols, tokens));
 }
 
 static int matmul_many(mi_stream stream, int kind, const void* w, int64_t row_bytes, int32_t rows, int32_t cols,
@@ -225,7 +232,7 @@ int mi_rms_norm(mi_stream stream, const float* x, const float* gain, int32_t n, 
     int rc = check_xq("rms_norm", xq, n, tokens);
     if (rc) return rc;
   }
-  return launch_rms_norm((hipStream_t)stream, x, gain, n, tokens, eps, out, xq);
+  return launch_rms_norm((hipStream_t)stream, x, gain, n, tokens, eps, out, xq, xq ? hx_of(xq, n, tokens) : nullptr);
 }
 
 // rope.mojo:230 step_table: f32(exp(f64(y) * log(f64(base)))), y = f32(-2p) / f32(dim).

@@ -8,11 +8,33 @@
 
 namespace mi {
 
+// The "hx" form of a token (read by the f16 matrix-core tile,
+// matvec_htile.hip), 4 cols bytes like the xq form: group g at g * 128 is
+// [kq 0..3][hi, lo][8 halves], value 8 kq + u of the group being X * 2^-8 =
+// hi + lo exactly (hi = f16(X / 256), lo = f16(X / 256 - hi)), X the group's
+// xq integer.  The group's scale stays in the xq form's plane 6.
+__device__ __forceinline__ void hx_group32(int X, int lane32, int g, uint8_t* __restrict__ hxtok, bool live) {
+  const float xs = (float)X * (1.0f / 256.0f);  // exact: |X| < 2^22
+  const _Float16 hi = (_Float16)xs;
+  const _Float16 lo = (_Float16)(xs - (float)hi);
+  const uint32_t pair = (uint32_t)__builtin_bit_cast(uint16_t, hi) |
+                        ((uint32_t)__builtin_bit_cast(uint16_t, lo) << 16);
+  // lanes 2j and 2j + 1: (hi, hi') and (lo, lo') as two dwords
+  const uint32_t other = (uint32_t)__shfl_down((int)pair, 1, 32);
+  if (!live || (lane32 & 1)) return;
+  const int kq = lane32 >> 3, u = lane32 & 7;
+  uint8_t* e = hxtok + (int64_t)g * 128 + kq * 32 + u * 2;
+  *(uint32_t*)e = (pair & 0xFFFFu) | (other << 16);
+  *(uint32_t*)(e + 16) = (pair >> 16) | (other & 0xFFFF0000u);
+}
+
 // All 32 lanes of one half-wave call this together, lane32 = value index in
 // the group.  `live` is false for padding lanes, which still take part in the
-// shuffles but write nothing.  xtok points at the token's 4*cols bytes.
+// shuffles but write nothing.  xtok points at the token's 4*cols bytes; hxtok,
+// when not null, at the token's hx form (hx_group32).
 __device__ __forceinline__ void quantize_group32(float v, int lane32, int g, int G,
-                                                 uint8_t* __restrict__ xtok, bool live) {
+                                                 uint8_t* __restrict__ xtok, bool live,
+                                                 uint8_t* __restrict__ hxtok = nullptr) {
   float a = fabsf(v);
 #pragma unroll
   for (int m = 16; m >= 1; m >>= 1) a = fmaxf(a, __shfl_xor(a, m));
@@ -34,6 +56,7 @@ __device__ __forceinline__ void quantize_group32(float v, int lane32, int g, int
   for (int m = 16; m >= 1; m >>= 1) sx += __shfl_xor(sx, m);
   const int other1 = __shfl_xor(s1, 16);
   const int other23 = __shfl_xor(s23, 16);
+  if (hxtok) hx_group32(X, lane32, g, hxtok, live);
   // Gather each limb's bytes four lanes to a dword: byte stores from every
   // lane cost the memory system far more than a quarter as many dword stores.
   uint32_t w[3] = {(uint32_t)L1 & 0xFFu, (uint32_t)L2 & 0xFFu, (uint32_t)L3 & 0xFFu};

@@ -251,6 +251,32 @@ def test_rms_norm(ctx):
     assert np.abs(got - want).max() <= 2e-6 * np.abs(want).max()
 
 
+@pytest.mark.parametrize("tokens", [2, 5, 8])
+def test_rms_norm_xq_feeds_matvec_xq(ctx, tokens):
+    """mi_rms_norm with an xq target, then mi_matvec_xq on it: at 2..8 tokens
+    the norm also writes the activations' half-precision (hx) form, which the
+    Q4_K matrix-core tile reads (cols a multiple of 512, here with a last
+    partial tile of rows), against the oracle's norm then matvec."""
+    from molla_amd import gpu
+    from molla_amd._lib import lib, check
+    kind, rows, cols = oracle.Q4_K, 1000, 2048
+    x = synth.normal(tokens * cols, 41 + tokens).numpy()
+    g = synth.normal(cols, 42, mean=1.0, std=0.1).numpy()
+    blob = synth.quant_tensor(kind, rows, cols, 43).numpy()
+    w = upload(blob, kind, cols, rows)
+    L = lib()
+    xq = torch.empty(L.mi_matvec_workspace(cols, tokens), dtype=torch.uint8, device="cuda")
+    dx, dg = torch.from_numpy(x).cuda(), torch.from_numpy(g).cuda()
+    out = torch.zeros(tokens * rows, device="cuda")
+    check(L.mi_rms_norm(ctx.handle, dx.data_ptr(), dg.data_ptr(), cols, tokens, 1e-5, None, xq.data_ptr()))
+    check(L.mi_matvec_xq(ctx.handle, kind, w.address, w.row_bytes(), rows, cols, xq.data_ptr(), tokens,
+                         out.data_ptr(), 0, None))
+    normed = np.stack([oracle.rms_norm(x[t * cols:(t + 1) * cols], g, 1e-5) for t in range(tokens)])
+    want = oracle.matvec(kind, blob, rows, cols, normed, threads=8)
+    assert_matvec_close(out.cpu().numpy(), want.reshape(tokens, rows), dequant_abs(kind, blob, rows, cols),
+                        normed.reshape(-1))
+
+
 @pytest.mark.parametrize("pos", [0, 3, 4096, 70000])
 @pytest.mark.parametrize("neox", [False, True])
 def test_rope(ctx, pos, neox):
