@@ -47,8 +47,8 @@ Carve carve(const mi_layer_desc* d, int32_t max_count, int32_t tokens) {
   const int64_t widest = std::max<int64_t>({d->width, qw, d->hidden});
   Carve c;
   size_t at = 0;
-  c.xq = at;
-  at += up256((size_t)xq_token_bytes((int32_t)widest) * tokens);
+  c.xq = at;  // at 2..8 tokens followed by the hx form (for wo's f16 matrix-core tile)
+  at += up256((size_t)xq_token_bytes((int32_t)widest) * tokens * (tokens > 1 ? 2 : 1));
   c.qkv = at;
   at += up256(sizeof(float) * (size_t)(qw + 2 * kvw) * tokens);
   c.up = at;
@@ -387,6 +387,8 @@ static int decoder_layer(mi_stream stream, const mi_layer_desc* d, float* resid,
   void* attn = base + c.attn;
   const int32_t qw = d->heads * d->head_dim;
   const int64_t qkv_stride = qw + 2 * kvw;
+  // a batch's attention output also in the hx form, right after its xq form
+  void* hx = tokens > 1 ? (uint8_t*)xq + (size_t)xq_token_bytes(qw) * tokens : nullptr;
 
   // attention_layer (block.mojo:319)
   const bool fused_qkv = tokens == 1 && d->wq.kind == MI_Q4_K && d->wk.kind == MI_Q4_K &&
@@ -492,10 +494,10 @@ static int decoder_layer(mi_stream stream, const mi_layer_desc* d, float* resid,
   // count = pos + 1 per sequence: the attention kernels read pos and add one.
   if ((rc = launch_attend(s, qkv, qkv_stride, k_cache, v_cache, cache_stride, d->heads, d->kv_heads,
                           d->head_dim, d->attn_scale, pos, -1, max_count, tokens, nullptr, xq, attn,
-                          d->cache_form, kv_index, index_stride)))
+                          d->cache_form, kv_index, index_stride, hx)))
     return rc;
   if ((rc = launch_matvec(s, d->wo.kind, d->wo.data, d->wo.row_bytes, d->width, qw, xq, tokens, resid,
-                          d->width, MI_EPI_ADD, nullptr)))
+                          d->width, MI_EPI_ADD, nullptr, hx)))
     return rc;
 
   // mlp_layer (block.mojo:429), gated silu

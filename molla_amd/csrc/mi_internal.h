@@ -201,7 +201,8 @@ int launch_attend(hipStream_t s, const float* q, int64_t q_stride, const uint16_
                   const uint16_t* v_cache, int64_t cache_stride, int32_t heads, int32_t kv_heads,
                   int32_t head_dim, float scale, const int32_t* pos_dev, int32_t count_host,
                   int32_t max_count, int32_t tokens, float* out, void* xq_out, void* work,
-                  int32_t form = MI_CACHE_F16, const int32_t* kv_index = nullptr, int64_t index_stride = 0);
+                  int32_t form = MI_CACHE_F16, const int32_t* kv_index = nullptr, int64_t index_stride = 0,
+                  void* hx_out = nullptr);
 int launch_argmax(hipStream_t s, const float* x, int32_t n, int32_t tokens, int32_t* out);
 // The optional layer parts (ops.hip): per-head RMS norm of `heads` runs of n
 // in each of `tokens` rows row_stride apart, in place; resid[t] +=

@@ -771,7 +771,7 @@ constexpr int kMergeBatch = 64;
 __global__ void attend_merge_kernel(const float* __restrict__ part_acc, const float* __restrict__ part_ml,
                                     int heads, int head_dim, const int32_t* __restrict__ pos_dev,
                                     int count_host, int max_chunks, float* __restrict__ out,
-                                    uint8_t* __restrict__ xq) {
+                                    uint8_t* __restrict__ xq, uint8_t* __restrict__ hx) {
   extern __shared__ float mls[];  // [max_chunks][2], then the weights [ceil32(max_chunks)]
   const int h = blockIdx.x, t = blockIdx.y;
   const int count = pos_dev ? pos_dev[t] + 1 : count_host;  // a position p attends over p + 1 slots
@@ -814,7 +814,8 @@ __global__ void attend_merge_kernel(const float* __restrict__ part_acc, const fl
   if (live && out) out[(int64_t)t * width + (int64_t)h * head_dim + d] = o;
   if (xq)
     quantize_group32(o, threadIdx.x & 31, (h * head_dim + d) >> 5, width >> 5,
-                     xq + (int64_t)t * xq_token_bytes(width), live);
+                     xq + (int64_t)t * xq_token_bytes(width), live,
+                     hx ? hx + (int64_t)t * xq_token_bytes(width) : nullptr);
 }
 
 // ---- decode attention slices ------------------------------------------------
@@ -1177,7 +1178,7 @@ int launch_attend(hipStream_t s, const float* q, int64_t q_stride, const uint16_
                   const uint16_t* v_cache, int64_t cache_stride, int32_t heads, int32_t kv_heads,
                   int32_t head_dim, float scale, const int32_t* pos_dev, int32_t count_host,
                   int32_t max_count, int32_t tokens, float* out, void* xq_out, void* work, int32_t form,
-                  const int32_t* kv_index, int64_t index_stride) {
+                  const int32_t* kv_index, int64_t index_stride, void* hx_out) {
   const int kk = attn_slice(head_dim);
   const int chunks = (max_count + kk - 1) / kk;
   const int64_t slots = (int64_t)tokens * heads * chunks;
@@ -1214,7 +1215,8 @@ int launch_attend(hipStream_t s, const float* q, int64_t q_stride, const uint16_
     int rc = hip_check(hipGetLastError(), "attend_wide launch");
     if (rc) return rc;
     hipLaunchKernelGGL(attend_merge_kernel, dim3(heads, tokens), dim3(head_dim < 64 ? 64 : head_dim), merge_lds, s,
-                       part_acc, part_ml, heads, head_dim, pos_dev, count_host, chunks, out, (uint8_t*)xq_out);
+                       part_acc, part_ml, heads, head_dim, pos_dev, count_host, chunks, out, (uint8_t*)xq_out,
+                       (uint8_t*)hx_out);
     return hip_check(hipGetLastError(), "attend_merge launch");
   }
   // one sequence's chunk (its tokens share one cache): 16 tokens per block
@@ -1251,7 +1253,8 @@ int launch_attend(hipStream_t s, const float* q, int64_t q_stride, const uint16_
     if (rc) return rc;
     const size_t mlds = ((size_t)chunks * 2 + (chunks + kMergeBatch - 1) / kMergeBatch * kMergeBatch) * sizeof(float);
     hipLaunchKernelGGL(attend_merge_kernel, dim3(heads, tokens), dim3(head_dim < 64 ? 64 : head_dim), mlds, s,
-                       part_acc, part_ml, heads, head_dim, pos_dev, count_host, chunks, out, (uint8_t*)xq_out);
+                       part_acc, part_ml, heads, head_dim, pos_dev, count_host, chunks, out, (uint8_t*)xq_out,
+                       (uint8_t*)hx_out);
     return hip_check(hipGetLastError(), "attend_merge launch");
   }
   const int tq = (one_seq && tokens > kMaxTokens && form != MI_CACHE_Q8) ? 16 : 1;
@@ -1282,7 +1285,7 @@ int launch_attend(hipStream_t s, const float* q, int64_t q_stride, const uint16_
   if (rc) return rc;
   hipLaunchKernelGGL(attend_merge_kernel, dim3(heads, tokens), dim3(head_dim < 64 ? 64 : head_dim), merge_lds, s,
                      part_acc, part_ml, heads, head_dim, pos_dev,
-                     count_host, chunks, out, (uint8_t*)xq_out);
+                     count_host, chunks, out, (uint8_t*)xq_out, (uint8_t*)hx_out);
   return hip_check(hipGetLastError(), "attend_merge launch");
 }
 
