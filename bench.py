@@ -231,10 +231,11 @@ def _prefill(L, h, stream, tokens=256, reps=20):
 
 def _batched(L, h, kind, ws, copies, rb, stream, reps=100):
     """Batch 4 and 8: the same weights against 4 / 8
-    tokens on the matrix-core tile (matvec_tile.hip).  Weights are still read
-    once per launch, so GB/s is over the same algorithmic bytes (plus the
-    larger x and y); MFMA utilisation = useful int8 ops (2 rows cols tokens,
-    times the three activation limbs) over the 5.0 POP/s dense int8 peak."""
+    tokens on the f16 matrix-core tile (matvec_htile.hip; mi_quantize writes
+    the activations' hx form it reads).  Weights are still read once per
+    launch, so GB/s is over the same algorithmic bytes (plus the larger x and
+    y); MFMA utilisation = useful f16 flops (2 rows cols tokens, times the
+    two halves of each activation) over the 2.5 PFLOP/s dense f16 peak."""
     import torch
 
     from molla_amd import synth
@@ -260,12 +261,13 @@ def _batched(L, h, kind, ws, copies, rb, stream, reps=100):
         torch.cuda.synchronize()
         us = e0.elapsed_time(e1) * 1e3 / reps
         algo = _algo_bytes(ROWS, COLS, tokens, ROWS * rb)
-        ops = 2.0 * ROWS * COLS * tokens * 3
-        out[f"tokens_{tokens}"] = {"kernel": "q4k_tile_kernel (v_mfma_i32_32x32x32_i8)", "us_per_launch": round(us, 3),
+        flops = 2.0 * ROWS * COLS * tokens * 2
+        out[f"tokens_{tokens}"] = {"kernel": "q4k_htile_kernel (v_mfma_f32_16x16x32_f16)",
+                                   "us_per_launch": round(us, 3),
                                    "GB_s": round(algo / us / 1e3, 1),
                                    "frac_hbm_peak": round(algo / us / 1e3 / PEAK_GBS, 4),
-                                   "mfma_int8_TOPs": round(ops / us / 1e6, 2),
-                                   "mfma_util_of_5POPs": round(ops / us / 1e6 / 5000.0, 5)}
+                                   "mfma_f16_TFLOPs": round(flops / us / 1e6, 2),
+                                   "mfma_util_of_2500TFLOPs": round(flops / us / 1e6 / 2500.0, 5)}
     return out
 
 

@@ -3,6 +3,9 @@
 
     python -m molla_amd.trace_summary DB            # every kernel of the run
     python -m molla_amd.trace_summary DB --steps N  # the last N decode steps
+    python -m molla_amd.trace_summary DB --calls prefill_x_kernel --per 23
+        # calls that start at each dispatch of the named kernel, in runs of
+        # 23 calls (one bench shape each): median duration per kernel
 
 A decode step starts at an embed_kernel dispatch (DeviceSession.step), so
 --steps N keeps the dispatches from the N-th last embed_kernel on and reports
@@ -28,8 +31,30 @@ def main() -> None:
     ap.add_argument("db")
     ap.add_argument("--steps", type=int, default=0)
     ap.add_argument("--top", type=int, default=20)
+    ap.add_argument("--calls", default="")
+    ap.add_argument("--per", type=int, default=1)
     a = ap.parse_args()
     rows = sqlite3.connect(a.db).execute("select name, start, end from kernels order by start").fetchall()
+    if a.calls:
+        calls = []
+        for name, st, en in rows:
+            if a.calls in name:
+                calls.append([])
+            if calls:
+                calls[-1].append((short(name), (en - st) / 1e3))
+        # the calls of one run share the kernels of the first; stop a call at
+        # any kernel the run's first call does not have
+        for r0 in range(0, len(calls) - a.per + 1, a.per):
+            run = calls[r0:r0 + a.per]
+            names = list(dict.fromkeys(n for n, _ in run[0]))
+            per = collections.defaultdict(list)
+            for c in run:
+                for n, d in c:
+                    if n in names:
+                        per[n].append(d)
+            cells = "; ".join(f"`{n}` {sorted(per[n])[len(per[n]) // 2]:.1f}" for n in names)
+            print(f"| run {r0 // a.per} | {cells} |")
+        return
     n = 1
     if a.steps:
         emb = [r[1] for r in rows if "embed_kernel" in r[0]]
