@@ -1,9 +1,9 @@
 // matvec.cpp -- routes mi_matvec / mi_matvec_xq to the kernel for its kind
 // and batch: the batch-1 row kernel of matvec_rows.hip (Q4_K, Q4_0, Q8_0)
 // and matvec_rows_more.hip (Q4_1, Q5_0, Q5_1, Q5_K), the batch-1 Q6_K
-// kernel of matvec_q6k_rows.hip, the batched Q4_K f16 matrix-core tile of
-// matvec_htile.hip (when the caller's activations carry the hx form) or the
-// int8 one of matvec_tile.hip and its Q6_K and Q4_0 / Q8_0 siblings
+// kernel of matvec_q6k_rows.hip, the batched Q4_K / Q6_K f16 matrix-core
+// tile of matvec_htile.hip (when the caller's activations carry the hx form)
+// or the int8 one of matvec_tile.hip and its Q6_K and Q4_0 / Q8_0 siblings
 // (matvec_tile_q6k.hip, matvec_tile_b32.hip), else the general
 // kernel of matvec_kernel.h, instantiated per kind in matvec_<kind>.hip.
 #include "matvec_rows.h"
@@ -32,8 +32,8 @@ int launch_matvec(hipStream_t s, int kind, const void* w, int64_t row_bytes, int
                   const float* aux, const void* hx) {
   if (tokens == 1 && rows_fits(kind, cols))
     return launch_rows(s, kind, w, row_bytes, rows, cols, xq, y, epi, aux);
-  if (hx && kind == MI_Q4_K && q4k_htile_fits(rows, cols, tokens) && ((uintptr_t)w & 15) == 0)
-    return launch_q4k_htile(s, rows::one_matrix(w, row_bytes, rows), rows, cols, xq, hx, tokens, y, ldy, epi, aux);
+  if (hx && htile_fits(kind, rows, cols, tokens) && ((uintptr_t)w & 7) == 0)
+    return launch_htile(s, kind, rows::one_matrix(w, row_bytes, rows), rows, cols, xq, hx, tokens, y, ldy, epi, aux);
   if (kind == MI_Q4_K && q4k_tile_fits(cols, tokens))
     return launch_q4k_tile(s, w, row_bytes, rows, cols, xq, tokens, y, ldy, epi, aux);
   if (b32_tile_fits(kind, cols, row_bytes, tokens) && ((uintptr_t)w & 15) == 0)

@@ -1,5 +1,5 @@
-// matvec_htile.hip -- the batched (2..8 tokens) Q4_K matvec on the f16
-// matrix cores (v_mfma_f32_16x16x32_f16), gfx950.
+// matvec_htile.hip -- the batched (2..8 tokens) Q4_K and Q6_K matvec on the
+// f16 matrix cores (v_mfma_f32_16x16x32_f16), gfx950.
 //
 // The int8 tile (matvec_tile.hip) multiplies exactly but has to recombine
 // three activation limbs per (row, token, group) on the VALU afterwards.
@@ -38,8 +38,10 @@
 // partial sums meet in LDS, where 16 * tokens (row, token) sums add them in
 // a fixed order and apply the epilogue.
 //
+// Q6_K (sb_product_q6k) has no min term; its codes need two MFMAs a group.
+//
 // Replaces the batched planar_matmul_kernel (src/molla/nn/gpu.mojo:1809) for
-// Q4_K; output y[t * ldy + r] and epilogues as gpu.mojo:1005.
+// Q4_K and Q6_K; output y[t * ldy + r] and epilogues as gpu.mojo:1005.
 #include "matvec_rows.h"
 
 namespace mi {
@@ -53,10 +55,26 @@ typedef uint32_t uu4 __attribute__((ext_vector_type(4)));
 
 constexpr int kSBW = 2;                                  // superblocks per wave
 constexpr int kMaxHWaves = 8;                            // cols <= 8 * 512
-constexpr int kRowPad = 32;                              // LDS rows 8 banks apart
-constexpr int kMaxRowBytes = kMaxHWaves * kSBW * 144;    // cols = 4096
-constexpr int kLdsRow = kMaxRowBytes + kRowPad;
-constexpr int kLoads = kSBW * 144 * 16 / (64 * 8);       // 8-byte loads per lane per tile
+
+// Per kind: superblock bytes, and the LDS row stride of a tile (the row at
+// 4096 columns, so that a fragment read's 16 rows start 8 banks apart: Q4_K
+// rows of 2304 bytes take 32 bytes of padding, Q6_K rows of 3360 bytes are
+// 8 banks apart already).
+template <int KIND>
+struct HGeo;
+template <>
+struct HGeo<MI_Q4_K> {
+  static constexpr int SB = 144, ROW = kMaxHWaves * kSBW * 144 + 32;
+};
+template <>
+struct HGeo<MI_Q6_K> {
+  static constexpr int SB = 210, ROW = kMaxHWaves * kSBW * 210;
+};
+constexpr int kTileBuf = 16 * HGeo<MI_Q6_K>::ROW;  // one tile buffer, the larger kind
+// 8-byte loads per lane per tile: a tile is 16 rows of cols / 256
+// superblocks, a block cols / 8 lanes, so SB / 16 words a lane
+template <int KIND>
+constexpr int kLoadsOf = (HGeo<KIND>::SB + 15) / 16;
 
 __device__ __forceinline__ ff4 mfma16(hh8 a, hh8 b, ff4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
@@ -101,6 +119,7 @@ __device__ __forceinline__ void kscales(uint32_t y, uint32_t z, uint32_t w, uint
 // (the min MFMA's B), which are held divided by 256.
 __device__ __forceinline__ void sb_product(const uint8_t* lrows, int sb, const hh8 (&b)[8], hh8 bm, float esc,
                                            int lm, int kq, ff4& acc) {
+  constexpr int kLdsRow = HGeo<MI_Q4_K>::ROW;
   const uint8_t* lrow = lrows + lm * kLdsRow + sb * 144;
   const uint4 h = *(const uint4*)lrow;
   uint2 q[4];
@@ -138,13 +157,72 @@ __device__ __forceinline__ void sb_product(const uint8_t* lrows, int sb, const h
   }
 }
 
-template <int TN>
-__global__ __launch_bounds__(kMaxHWaves * 64) void q4k_htile_kernel(const RowSegs sg, int cols,
+// The same for a Q6_K superblock (ql[128], qh[64], int8 scales[16], f16 d:
+// quant.mojo Q6_K; value 32 g + l of a group g of half h = g / 4 takes the low
+// (g & 2 = 0) or high nibble of ql[64 h + 32 (g & 1) + l] and bits 2 (g & 3)
+// of qh[32 h + l], minus 32, times scale 2 g + l / 16).  sc * (q - 32)
+// reaches 4096, past exact halves, so the scale splits into 16 s_hi + s_lo
+// and each group is two MFMAs of exact codes (b - 32) s_hi and (b - 32) s_lo.
+// Superblocks of 210 bytes sit packed in LDS: one of odd index S starts 2
+// bytes past a dword, so its fields are read as dwords and realigned.
+template <int S>
+__device__ __forceinline__ void sb_product_q6k(const uint8_t* lrows, int sb, const hh8 (&b)[8], float esc,
+                                               int lm, int kq, ff4& acc) {
+  constexpr int kLdsRow = HGeo<MI_Q6_K>::ROW;
+  const uint8_t* p = lrows + lm * kLdsRow + sb * 210;  // 4-aligned + 2 S
+  auto ld8 = [&](int off) __attribute__((always_inline)) {
+    const uint32_t* a = (const uint32_t*)(p + off - 2 * S);
+    if constexpr (S == 0) return make_uint2(a[0], a[1]);
+    else return make_uint2(__builtin_amdgcn_alignbyte(a[1], a[0], 2), __builtin_amdgcn_alignbyte(a[2], a[1], 2));
+  };
+  uint2 ql[2][2], qh[2];
+#pragma unroll
+  for (int h = 0; h < 2; h++) {
+    ql[h][0] = ld8(64 * h + 8 * kq);
+    ql[h][1] = ld8(64 * h + 32 + 8 * kq);
+    qh[h] = ld8(128 + 32 * h + 8 * kq);
+  }
+  uint32_t scw[4];
+  {
+    const uint32_t* a = (const uint32_t*)(p + 192 - 2 * S);
+#pragma unroll
+    for (int j = 0; j < 4; j++) scw[j] = S == 0 ? a[j] : __builtin_amdgcn_alignbyte(a[j + 1], a[j], 2);
+  }
+  float dd[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const uint32_t w = *(const uint32_t*)(lrows + (4 * kq + i) * kLdsRow + sb * 210 + 208 - 2 * S);
+    dd[i] = half_bits_to_float(S == 0 ? w : w >> 16);
+  }
+  const int kh = kq >> 1;  // which 16-value sub-block of a group this lane's values are in
+  ff4 ch = {0.0f, 0.0f, 0.0f, 0.0f}, cl = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int g = 0; g < 8; g++) {
+    const int h = g >> 2, qq = g & 3;
+    const uint32_t t0 = ql[h][qq & 1].x, t1 = ql[h][qq & 1].y;
+    const uint32_t n0 = (qq >> 1) ? (t0 >> 4) & 0x0F0F0F0Fu : t0 & 0x0F0F0F0Fu;
+    const uint32_t n1 = (qq >> 1) ? (t1 >> 4) & 0x0F0F0F0Fu : t1 & 0x0F0F0F0Fu;
+    const uint32_t b0 = n0 | (((qh[h].x >> (2 * qq)) & 0x03030303u) << 4);
+    const uint32_t b1 = n1 | (((qh[h].y >> (2 * qq)) & 0x03030303u) << 4);
+    const int sc = __builtin_amdgcn_sbfe((int)scw[g >> 1], 8 * (2 * (g & 1) + kh), 8);
+    const _Float16 fh = (_Float16)(float)(sc >> 4), fl = (_Float16)(float)(sc & 15);
+    const hh2 shi = {fh, fh}, slo = {fl, fl};
+    const hh2 k1056 = {(_Float16)-1056.0f, (_Float16)-1056.0f};
+    ch = mfma16(codes8(b0, b1, shi, shi * k1056), b[g], ch);
+    cl = mfma16(codes8(b0, b1, slo, slo * k1056), b[g], cl);
+  }
+#pragma unroll
+  for (int i = 0; i < 4; i++) acc[i] = fmaf(esc * dd[i], fmaf(16.0f, ch[i], cl[i]), acc[i]);
+}
+
+template <int TN, int KIND>
+__global__ __launch_bounds__(kMaxHWaves * 64) void htile_kernel(const RowSegs sg, int cols,
                                                                      const uint8_t* __restrict__ xq,
                                                                      const uint8_t* __restrict__ hx,
                                                                      float* __restrict__ y, int64_t ldy, int epi,
                                                                      const float* __restrict__ aux) {
-  __shared__ __align__(16) uint8_t wl[2][16 * kLdsRow];
+  constexpr int SB = HGeo<KIND>::SB, kLdsRow = HGeo<KIND>::ROW, kLoads = kLoadsOf<KIND>;
+  __shared__ __align__(16) uint8_t wl[2][kTileBuf];
   __shared__ float part[2][kMaxHWaves][16][17];
   __shared__ __align__(16) uint8_t sink[16];  // target of the copies' idle lanes
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
@@ -152,7 +230,7 @@ __global__ __launch_bounds__(kMaxHWaves * 64) void q4k_htile_kernel(const RowSeg
   const int rows = sg.end[sg.nseg - 1];
   const int tiles = (rows + 15) >> 4;
   const int G = cols >> 5;
-  const int rb = (cols >> 8) * 144;  // bytes per row; the tile is 16 rows in a run
+  const int rb = (cols >> 8) * SB;  // bytes per row; the tile is 16 rows in a run
   const int64_t tok_bytes = xq_token_bytes(cols);
   const int step = gridDim.x;
 
@@ -162,8 +240,10 @@ __global__ __launch_bounds__(kMaxHWaves * 64) void q4k_htile_kernel(const RowSeg
 #pragma unroll
   for (int j = 0; j < kLoads; j++) {
     // o / rb through a float reciprocal (o < 2^16: exact after one
-    // correction), not the long integer division sequence
-    const int o = 8 * ((int)threadIdx.x + (int)blockDim.x * j);
+    // correction), not the long integer division sequence.  A lane past the
+    // tile's last word (Q6_K's ragged last round) stores that word again
+    // where it belongs.
+    const int o = 8 * min((int)threadIdx.x + (int)blockDim.x * j, 2 * rb - 1);
     int row = (int)((float)o * (1.0f / (float)rb));
     row -= row * rb > o;
     row += (row + 1) * rb <= o;
@@ -259,16 +339,19 @@ __global__ __launch_bounds__(kMaxHWaves * 64) void q4k_htile_kernel(const RowSeg
     for (int g = 0; g < 8; g++) emax = fmaxf(emax, sc8[s][g]);
     esc[s] = 256.0f * emax;
     const float inv = emax > 0.0f ? __builtin_amdgcn_rcpf(emax) : 0.0f;  // exact: a power of two
-    hh8 hv, lv;
+    hh8 hv = {}, lv = {};
 #pragma unroll
     for (int g = 0; g < 8; g++) {
       const _Float16 f = (_Float16)(sc8[s][g] * inv);
       b[s][g] = b[s][g] * hh8{f, f, f, f, f, f, f, f};
-      const float gs = mfma16(ones, b[s][g], ff4{0.0f, 0.0f, 0.0f, 0.0f})[0] * (1.0f / 256.0f);
-      hv[g] = (_Float16)gs;
-      lv[g] = (_Float16)(gs - (float)hv[g]);
+      if constexpr (KIND == MI_Q4_K) {
+        const float gs = mfma16(ones, b[s][g], ff4{0.0f, 0.0f, 0.0f, 0.0f})[0] * (1.0f / 256.0f);
+        hv[g] = (_Float16)gs;
+        lv[g] = (_Float16)(gs - (float)hv[g]);
+      }
     }
-    bm[s] = kq == 0 ? hv : (kq == 1 ? lv : hh8{0, 0, 0, 0, 0, 0, 0, 0});
+    if constexpr (KIND == MI_Q4_K) bm[s] = kq == 0 ? hv : (kq == 1 ? lv : hh8{0, 0, 0, 0, 0, 0, 0, 0});
+    else bm[s] = hh8{0, 0, 0, 0, 0, 0, 0, 0};
   }
 
   // (row r, token u) sums of tile tl over the waves, in wave order, hi + lo,
@@ -299,7 +382,15 @@ __global__ __launch_bounds__(kMaxHWaves * 64) void q4k_htile_kernel(const RowSeg
     if (k > 0) finish(tl - step, (k - 1) & 1);
     ff4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int s = 0; s < kSBW; s++) sb_product(wl[k & 1], wave * kSBW + s, b[s], bm[s], esc[s], lm, kq, acc);
+    for (int s = 0; s < kSBW; s++) {
+      if constexpr (KIND == MI_Q4_K) {
+        sb_product(wl[k & 1], wave * kSBW + s, b[s], bm[s], esc[s], lm, kq, acc);
+      } else if (s == 0) {
+        sb_product_q6k<0>(wl[k & 1], wave * kSBW, b[0], esc[0], lm, kq, acc);
+      } else {
+        sb_product_q6k<1>(wl[k & 1], wave * kSBW + 1, b[1], esc[1], lm, kq, acc);
+      }
+    }
 #pragma unroll
     for (int i = 0; i < 4; i++) part[k & 1][wave][4 * kq + i][lm] = acc[i];
     if (tl + step >= tiles) return false;
@@ -329,22 +420,27 @@ int cu_count_h() {
 
 }  // namespace
 
-bool q4k_htile_fits(int32_t rows, int32_t cols, int32_t tokens) {
-  return tokens >= 2 && tokens <= kMaxTokens && cols % (256 * kSBW) == 0 && cols / (256 * kSBW) <= kMaxHWaves &&
-         rows > 0;
+bool htile_fits(int kind, int32_t rows, int32_t cols, int32_t tokens) {
+  return (kind == MI_Q4_K || kind == MI_Q6_K) && tokens >= 2 && tokens <= kMaxTokens &&
+         cols % (256 * kSBW) == 0 && cols / (256 * kSBW) <= kMaxHWaves && rows > 0;
 }
 
-int launch_q4k_htile(hipStream_t s, const RowSegs& sg, int32_t rows, int32_t cols, const void* xq, const void* hx,
-                     int32_t tokens, float* y, int64_t ldy, int32_t epi, const float* aux) {
+int launch_htile(hipStream_t s, int kind, const RowSegs& sg, int32_t rows, int32_t cols, const void* xq,
+                 const void* hx, int32_t tokens, float* y, int64_t ldy, int32_t epi, const float* aux) {
+  const int sbb = kind == MI_Q6_K ? HGeo<MI_Q6_K>::SB : HGeo<MI_Q4_K>::SB;
   for (int i = 0; i < sg.nseg; i++)
-    if ((i < sg.nseg - 1 && sg.end[i] % 16) || sg.rb[i] != (int64_t)(cols / 256) * 144)
-      return fail(MI_ERR_SHAPE, "htile: segments must be whole 16-row tiles of %d-column rows", cols);
+    if ((i < sg.nseg - 1 && sg.end[i] % 16) || sg.rb[i] != (int64_t)(cols / 256) * sbb || ((uintptr_t)sg.w[i] & 7))
+      return fail(MI_ERR_SHAPE, "htile: segments must be whole 16-row tiles of %d-column rows, 8-byte aligned", cols);
   const int waves = cols / (256 * kSBW);
   const int grid = std::min((rows + 15) / 16, cu_count_h());
-#define MI_HT(T)                                                                                         \
-  case T:                                                                                                \
-    hipLaunchKernelGGL(q4k_htile_kernel<T>, dim3(grid), dim3(waves * 64), 0, s, sg, cols, (const uint8_t*)xq, \
-                       (const uint8_t*)hx, y, ldy, epi, aux);                                            \
+#define MI_HT(T)                                                                                              \
+  case T:                                                                                                     \
+    if (kind == MI_Q6_K)                                                                                      \
+      hipLaunchKernelGGL((htile_kernel<T, MI_Q6_K>), dim3(grid), dim3(waves * 64), 0, s, sg, cols,            \
+                         (const uint8_t*)xq, (const uint8_t*)hx, y, ldy, epi, aux);                          \
+    else                                                                                                      \
+      hipLaunchKernelGGL((htile_kernel<T, MI_Q4_K>), dim3(grid), dim3(waves * 64), 0, s, sg, cols,            \
+                         (const uint8_t*)xq, (const uint8_t*)hx, y, ldy, epi, aux);                          \
     break;
   switch (tokens) {
     MI_HT(2) MI_HT(3) MI_HT(4) MI_HT(5) MI_HT(6) MI_HT(7) MI_HT(8)

@@ -314,10 +314,6 @@ int launch_q6k_tile(hipStream_t s, const void* w, int64_t row_bytes, int32_t row
     case 2: return launch_t<2>(s, w, row_bytes, rows, cols, xq, y, ldy, epi, aux);
     case 3: return launch_t<3>(s, w, row_bytes, rows, cols, xq, y, ldy, epi, aux);
     case 4: return launch_t<4>(s, w, row_bytes, rows, cols, xq, y, ldy, epi, aux);
-    case 5: return launch_t<5>(s, w, row_bytes, rows, cols, xq, y, ldy, epi, aux);
-    case 6: return launch_t<6>(s, w, row_bytes, rows, cols, xq, y, ldy, epi, aux);
-    case 7: return launch_t<7>(s, w, row_bytes, rows, cols, xq, y, ldy, epi, aux);
-    case 8: return launch_t<8>(s, w, row_bytes, rows, cols, xq, y, ldy, epi, aux);
   }
   return fail(MI_ERR_ARG, "matvec: tokens %d outside 2..8 for the batched tile", tokens);
 }

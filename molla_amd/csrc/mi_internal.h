@@ -155,12 +155,13 @@ int matmul_tokens(hipStream_t s, int kind, const void* w, int64_t row_bytes, int
 int launch_matvec(hipStream_t s, int kind, const void* w, int64_t row_bytes, int32_t rows,
                   int32_t cols, const void* xq, int32_t tokens, float* y, int64_t ldy, int32_t epi,
                   const float* aux, const void* hx = nullptr);
-// The f16 matrix-core tile for 2..8 tokens (matvec_htile.hip): Q4_K rows of
-// up to three matrices whose ends (but the last) are whole 16-row tiles,
-// reading the xq form (group scales) and the hx form of the same tokens.
-bool q4k_htile_fits(int32_t rows, int32_t cols, int32_t tokens);
-int launch_q4k_htile(hipStream_t s, const RowSegs& sg, int32_t rows, int32_t cols, const void* xq, const void* hx,
-                     int32_t tokens, float* y, int64_t ldy, int32_t epi, const float* aux);
+// The f16 matrix-core tile for 2..8 tokens (matvec_htile.hip): Q4_K or Q6_K
+// rows of up to three matrices whose ends (but the last) are whole 16-row
+// tiles, 8-byte aligned, reading the xq form (group scales) and the hx form
+// of the same tokens.
+bool htile_fits(int kind, int32_t rows, int32_t cols, int32_t tokens);
+int launch_htile(hipStream_t s, int kind, const RowSegs& sg, int32_t rows, int32_t cols, const void* xq,
+                 const void* hx, int32_t tokens, float* y, int64_t ldy, int32_t epi, const float* aux);
 // rms_norm_trig: also writes trig[p] = (cos, sin) of f32(pos[0]) * steps[p]
 // (divided by factors[p] when factors is given) for p < pairs (float64 trig,
 // as rope.mojo:253-285), for the fused q|k|v epilogue of the same layer.
