@@ -215,12 +215,18 @@ __device__ __forceinline__ void sb_product_q6k(const uint8_t* lrows, int sb, con
   for (int i = 0; i < 4; i++) acc[i] = fmaf(esc * dd[i], fmaf(16.0f, ch[i], cl[i]), acc[i]);
 }
 
-template <int TN, int KIND>
+// GLU (Q4_K): sg holds gate (rows 0 .. end[0]) and up (end[0] .. end[1]);
+// a block takes 32-row groups, each as four tiles (gate rows 0-15, up rows
+// 0-15, gate rows 16-31, up rows 16-31), and writes act(gate) * up of each
+// group only in matvec form, into xq_out (the down projection's input;
+// gpu_block.mojo device_swiglu then the quantize), one half-wave a token.
+template <int TN, int KIND, bool GLU>
 __global__ __launch_bounds__(kMaxHWaves * 64) void htile_kernel(const RowSegs sg, int cols,
                                                                      const uint8_t* __restrict__ xq,
                                                                      const uint8_t* __restrict__ hx,
                                                                      float* __restrict__ y, int64_t ldy, int epi,
-                                                                     const float* __restrict__ aux) {
+                                                                     const float* __restrict__ aux,
+                                                                     uint8_t* __restrict__ xq_out) {
   constexpr int SB = HGeo<KIND>::SB, kLdsRow = HGeo<KIND>::ROW, kLoads = kLoadsOf<KIND>;
   __shared__ __align__(16) uint8_t wl[2][kTileBuf];
   __shared__ float part[2][kMaxHWaves][16][17];
@@ -233,6 +239,21 @@ __global__ __launch_bounds__(kMaxHWaves * 64) void htile_kernel(const RowSegs sg
   const int rb = (cols >> 8) * SB;  // bytes per row; the tile is 16 rows in a run
   const int64_t tok_bytes = xq_token_bytes(cols);
   const int step = gridDim.x;
+  // the k-th tile of this block: tile blockIdx.x + k step, or under GLU tile
+  // k % 4 of 32-row group blockIdx.x + (k / 4) step
+  const int gl_rows = GLU ? sg.end[0] : 0, jobs = gl_rows >> 5;
+  auto tile_of = [&](int kk) __attribute__((always_inline)) {
+    if constexpr (GLU) {
+      const int j = blockIdx.x + (kk >> 2) * step, q = kk & 3;
+      return (q & 1) * (gl_rows >> 4) + 2 * j + (q >> 1);
+    } else {
+      return (int)blockIdx.x + kk * step;
+    }
+  };
+  auto valid = [&](int kk) __attribute__((always_inline)) {
+    if constexpr (GLU) return (int)blockIdx.x + (kk >> 2) * step < jobs;
+    else return (int)blockIdx.x + kk * step < tiles;
+  };
 
   // This lane's share of a tile: 8-byte words threadIdx.x + blockDim.x * j,
   // and where each lands in the padded LDS rows.
@@ -288,8 +309,8 @@ __global__ __launch_bounds__(kMaxHWaves * 64) void htile_kernel(const RowSegs sg
 #pragma unroll
   for (int u = 0; u < TN; u++) scl[u] = scale_src[u * (tok_bytes / 4) + sg_g * 4];
   uint2 ra[kLoads], rb_[kLoads];
-  load_tile(ra, blockIdx.x);  // the grid is at most `tiles` blocks
-  if (blockIdx.x + step < tiles) load_tile(rb_, blockIdx.x + step);
+  load_tile(ra, tile_of(0));  // the grid is at most `tiles` (GLU: groups) blocks
+  if (valid(1)) load_tile(rb_, tile_of(1));
 
   hh8 b[kSBW][8];
   float sc8[kSBW][8];
@@ -354,18 +375,45 @@ __global__ __launch_bounds__(kMaxHWaves * 64) void htile_kernel(const RowSegs sg
     else bm[s] = hh8{0, 0, 0, 0, 0, 0, 0, 0};
   }
 
-  // (row r, token u) sums of tile tl over the waves, in wave order, hi + lo,
+  // (row r, token u) sums of tile kk over the waves, in wave order, hi + lo,
   // and the epilogue; the 16 * TN sums are dealt round the waves, so that
-  // no wave comes late to the next barrier.
-  auto finish = [&](int tl, int buf) __attribute__((always_inline)) {
+  // no wave comes late to the next barrier.  GLU: a gate tile's sums wait in
+  // gsum for the up tile of the same rows (the same thread takes the same
+  // (row, token) every tile), whose act(gate) * up go to hbuf.
+  __shared__ float gsum[GLU ? 2 : 1][16][TN], hbuf[GLU ? 32 : 1][TN];
+  auto finish = [&](int kk, int buf) __attribute__((always_inline)) {
+    const int tl = tile_of(kk);
     for (int ix = lane * nw + wave; ix < 16 * TN; ix += 64 * nw) {
       const int rr = ix & 15, u = ix >> 4;
       float v = 0.0f;
 #pragma unroll
       for (int w = 0; w < kMaxHWaves; w++)
         if (w < nw) v += part[buf][w][rr][2 * u] + part[buf][w][rr][2 * u + 1];
-      const int row = tl * 16 + rr;
-      if (row < rows) epilogue(y, aux, epi, (int64_t)u * ldy + row, row, v);
+      if constexpr (GLU) {
+        const int q = kk & 3;
+        if (!(q & 1)) {
+          gsum[q >> 1][rr][u] = v;
+        } else {
+          const float g = gsum[q >> 1][rr][u];
+          hbuf[16 * (q >> 1) + rr][u] = ((epi & MI_ACT_GELU) ? gelu(g) : silu(g)) * v;
+        }
+      } else {
+        const int row = tl * 16 + rr;
+        if (row < rows) epilogue(y, aux, epi, (int64_t)u * ldy + row, row, v);
+      }
+    }
+  };
+  // GLU: group kk / 4's 32 act(gate) * up per token into xq_out, a half-wave
+  // a token (lane = row); hbuf is complete once a barrier follows its tile's
+  // finish, and the next group's first write to it is two tiles later.
+  auto quantize_group = [&](int kk) __attribute__((always_inline)) {
+    if constexpr (GLU) {
+      const int j = blockIdx.x + (kk >> 2) * step;
+      for (int u0 = 2 * wave; u0 < TN; u0 += 2 * nw) {  // a block of one wave takes every token
+        const int u = u0 + (lane >> 5);
+        quantize_group32(hbuf[lane & 31][u < TN ? u : 0], lane & 31, j, jobs,
+                         xq_out + (int64_t)(u < TN ? u : 0) * xq_token_bytes(gl_rows), u < TN);
+      }
     }
   };
 
@@ -374,12 +422,13 @@ __global__ __launch_bounds__(kMaxHWaves * 64) void htile_kernel(const RowSegs sg
   // goes into the other buffer and its registers send for tile k + 3.  With
   // buffers alternating, one barrier per tile keeps every buffer from being
   // overwritten before it has been read.
-  int tl = blockIdx.x, k = 0;
+  int k = 0;
   store_tile(ra, 0);
-  if (tl + 2 * step < tiles) load_tile(ra, tl + 2 * step);
+  if (valid(2)) load_tile(ra, tile_of(2));
   auto step_tile = [&](uint2 (&rn)[kLoads]) __attribute__((always_inline)) {
     __syncthreads();
-    if (k > 0) finish(tl - step, (k - 1) & 1);
+    if (GLU && k >= 2 && ((k - 2) & 3) == 3) quantize_group(k - 2);
+    if (k > 0) finish(k - 1, (k - 1) & 1);
     ff4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int s = 0; s < kSBW; s++) {
@@ -393,17 +442,20 @@ __global__ __launch_bounds__(kMaxHWaves * 64) void htile_kernel(const RowSegs sg
     }
 #pragma unroll
     for (int i = 0; i < 4; i++) part[k & 1][wave][4 * kq + i][lm] = acc[i];
-    if (tl + step >= tiles) return false;
+    if (!valid(k + 1)) return false;
     store_tile(rn, (k + 1) & 1);  // tile k + 1
-    if (tl + 3 * step < tiles) load_tile(rn, tl + 3 * step);
-    tl += step;
+    if (valid(k + 3)) load_tile(rn, tile_of(k + 3));
     k++;
     return true;
   };
   while (step_tile(rb_) && step_tile(ra)) {
   }
   __syncthreads();
-  finish(tl, k & 1);
+  finish(k, k & 1);
+  if constexpr (GLU) {
+    __syncthreads();
+    quantize_group(k);
+  }
 }
 
 int cu_count_h() {
@@ -436,17 +488,49 @@ int launch_htile(hipStream_t s, int kind, const RowSegs& sg, int32_t rows, int32
 #define MI_HT(T)                                                                                              \
   case T:                                                                                                     \
     if (kind == MI_Q6_K)                                                                                      \
-      hipLaunchKernelGGL((htile_kernel<T, MI_Q6_K>), dim3(grid), dim3(waves * 64), 0, s, sg, cols,            \
-                         (const uint8_t*)xq, (const uint8_t*)hx, y, ldy, epi, aux);                          \
+      hipLaunchKernelGGL((htile_kernel<T, MI_Q6_K, false>), dim3(grid), dim3(waves * 64), 0, s, sg, cols,     \
+                         (const uint8_t*)xq, (const uint8_t*)hx, y, ldy, epi, aux, nullptr);                 \
     else                                                                                                      \
-      hipLaunchKernelGGL((htile_kernel<T, MI_Q4_K>), dim3(grid), dim3(waves * 64), 0, s, sg, cols,            \
-                         (const uint8_t*)xq, (const uint8_t*)hx, y, ldy, epi, aux);                          \
+      hipLaunchKernelGGL((htile_kernel<T, MI_Q4_K, false>), dim3(grid), dim3(waves * 64), 0, s, sg, cols,     \
+                         (const uint8_t*)xq, (const uint8_t*)hx, y, ldy, epi, aux, nullptr);                 \
     break;
   switch (tokens) {
     MI_HT(2) MI_HT(3) MI_HT(4) MI_HT(5) MI_HT(6) MI_HT(7) MI_HT(8)
     default: return fail(MI_ERR_ARG, "htile: %d tokens", tokens);
   }
 #undef MI_HT
+  return hip_check(hipGetLastError(), "htile launch");
+}
+
+bool htile_glu_fits(int32_t rows, int32_t cols, int32_t tokens) {
+  return htile_fits(MI_Q4_K, 2 * rows, cols, tokens) && rows % 32 == 0;
+}
+
+int launch_htile_glu(hipStream_t s, const void* gate, const void* up, int64_t row_bytes, int32_t rows, int32_t cols,
+                     const void* xq, const void* hx, int32_t tokens, int32_t act, void* xq_out) {
+  if (!htile_glu_fits(rows, cols, tokens) || row_bytes != (int64_t)(cols / 256) * HGeo<MI_Q4_K>::SB ||
+      (((uintptr_t)gate | (uintptr_t)up) & 7))
+    return fail(MI_ERR_SHAPE, "htile: no GLU tile for %d x %d at %d tokens", rows, cols, tokens);
+  RowSegs sg{};
+  sg.w[0] = (const uint8_t*)gate;
+  sg.w[1] = sg.w[2] = (const uint8_t*)up;
+  sg.rb[0] = sg.rb[1] = sg.rb[2] = row_bytes;
+  sg.end[0] = rows;
+  sg.end[1] = sg.end[2] = 2 * rows;
+  sg.nseg = 2;
+  const int waves = cols / (256 * kSBW);
+  const int grid = std::min(rows / 32, cu_count_h());
+#define MI_HTG(T)                                                                                             \
+  case T:                                                                                                     \
+    hipLaunchKernelGGL((htile_kernel<T, MI_Q4_K, true>), dim3(grid), dim3(waves * 64), 0, s, sg, cols,        \
+                       (const uint8_t*)xq, (const uint8_t*)hx, nullptr, 0, act & MI_ACT_GELU, nullptr,        \
+                       (uint8_t*)xq_out);                                                                     \
+    break;
+  switch (tokens) {
+    MI_HTG(2) MI_HTG(3) MI_HTG(4) MI_HTG(5) MI_HTG(6) MI_HTG(7) MI_HTG(8)
+    default: return fail(MI_ERR_ARG, "htile: %d tokens", tokens);
+  }
+#undef MI_HTG
   return hip_check(hipGetLastError(), "htile launch");
 }
 

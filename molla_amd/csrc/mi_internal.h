@@ -162,6 +162,12 @@ int launch_matvec(hipStream_t s, int kind, const void* w, int64_t row_bytes, int
 bool htile_fits(int kind, int32_t rows, int32_t cols, int32_t tokens);
 int launch_htile(hipStream_t s, int kind, const RowSegs& sg, int32_t rows, int32_t cols, const void* xq,
                  const void* hx, int32_t tokens, float* y, int64_t ldy, int32_t epi, const float* aux);
+// The gated MLP's input side on the same tile (Q4_K gate and up of `rows` x
+// `cols`, rows a multiple of 32): act(gate) * up written only in matvec form
+// into xq_out (`rows` values a token), for the down projection.
+bool htile_glu_fits(int32_t rows, int32_t cols, int32_t tokens);
+int launch_htile_glu(hipStream_t s, const void* gate, const void* up, int64_t row_bytes, int32_t rows, int32_t cols,
+                     const void* xq, const void* hx, int32_t tokens, int32_t act, void* xq_out);
 // rms_norm_trig: also writes trig[p] = (cos, sin) of f32(pos[0]) * steps[p]
 // (divided by factors[p] when factors is given) for p < pairs (float64 trig,
 // as rope.mojo:253-285), for the fused q|k|v epilogue of the same layer.

@@ -92,6 +92,9 @@ def llama31_factors(pairs):
     ((256, 512, 4, 2, 64), 37, 1, True),
     ((512, 1024, 8, 2, 64), 300, 3, False),
     ((512, 1024, 8, 2, 64), 300, 3, True),
+    # 5 tokens: gate|up on the f16 tile (one-wave blocks at 512 columns, an
+    # odd token count for its per-token quantize)
+    ((512, 1024, 8, 2, 64), 300, 5, False),
     ((4096, 14336, 32, 8, 128), 4096, 1, False),   # config 4
     # an MLP of 8192: the batched down projection splits K over two blocks
     ((1024, 8192, 8, 2, 128), 200, 4, False),
