@@ -18,10 +18,10 @@ using namespace mv;
 // in (Q4_K, cols <= 4096).  A block is 8 waves, each owning four rows of
 // gate and of up in a 32-row group, as rows_kernel<Q4_K, 4, 1, GLU, -, GQ>;
 // the grid is at most one block per CU and a block loops over groups
-// blockIdx.x, blockIdx.x + gridDim.x, ...  The block issues the row's loads,
-// then its first group's weight loads, then normalises the row into LDS in
-// matvec form (norm_row_to_lds) while those weights stream in, and keeps the
-// activation in registers for every group it takes: the norm costs no launch
+// blockIdx.x, blockIdx.x + gridDim.x, ...  The block normalises the row
+// into LDS in matvec form (norm_row_to_lds), then issues its first group's
+// weight loads, and keeps the activation in registers for every group it
+// takes: the norm costs no launch
 // and is computed once per CU, not once per group.  After each group, wave 0
 // writes its act(gate) * up in matvec form for the down projection.
 __global__ __launch_bounds__(8 * 64) void glu_norm_kernel(const RowSegs sg, int cols, float* __restrict__ y,
@@ -40,7 +40,12 @@ __global__ __launch_bounds__(8 * 64) void glu_norm_kernel(const RowSegs sg, int 
 
   rows::XUnitRegs<false> xr;
   UnitOf<MI_Q4_K, 1>::type un[NR];
+  // The norm first, then the weight loads.  Issued behind the weights, the
+  // norm finished about 2 us later (its row loads and code wait behind the
+  // whole chip's weight requests), and the block computes nothing before it.
   const NormRow nr = norm_row_load(nm.x, nm.gain, cols);
+  norm_row_to_lds<kNT>(nr, cols, nm.eps, xs, red);
+  rows::load_x(xr, XLds{xs, 0, (cols >> 5) * 16}, u);
   __builtin_amdgcn_sched_barrier(0);
   int g = blockIdx.x;
 #pragma unroll
@@ -48,9 +53,6 @@ __global__ __launch_bounds__(8 * 64) void glu_norm_kernel(const RowSegs sg, int 
     const int row = (g * 8 + wave) * RPW + r % RPW;
     un[r].load(sg.w[r / RPW] + (int64_t)row * sg.rb[r / RPW], 0, 0, 0, u);
   }
-  __builtin_amdgcn_sched_barrier(0);
-  norm_row_to_lds<kNT>(nr, cols, nm.eps, xs, red);
-  rows::load_x(xr, XLds{xs, 0, (cols >> 5) * 16}, u);
   for (int it = 0;; it++) {
     float acc[NR];
 #pragma unroll
@@ -93,9 +95,9 @@ __global__ __launch_bounds__(8 * 64) void glu_norm_kernel(const RowSegs sg, int 
 // folded in (Q4_K, cols <= 4096), and the rope and cache store of
 // rows_kernel<…, ROPE> in its epilogue.  A block is 12 waves of two rows
 // (one rope pair) each; the grid is at most one block per CU, each block
-// looping over 24-row groups.  The block issues the row's loads, then its
-// weight loads, then normalises the row into LDS in matvec form
-// (norm_row_to_lds) while the weights arrive.  A wave's (cos, sin) comes
+// looping over 24-row groups.  The block normalises the row into LDS in
+// matvec form (norm_row_to_lds), then issues its weight loads (the norm
+// first, as in glu_norm_kernel).  A wave's (cos, sin) comes
 // from scalar loads of pos, steps and factors and float64 trig, as
 // rms_norm_kernel computes its table, so it never waits for weights.
 __global__ __launch_bounds__(12 * 64) void qkv_norm_kernel(const RowSegs sg, int cols, float* __restrict__ y,
@@ -139,12 +141,11 @@ __global__ __launch_bounds__(12 * 64) void qkv_norm_kernel(const RowSegs sg, int
   // waits for a weight
   const NormRow nr = norm_row_load(nm.x, nm.gain, cols);
   float step = rp.steps[pr.pair], factor = rp.factors ? rp.factors[pr.pair] : 1.0f;
+  norm_row_to_lds<kNT>(nr, cols, nm.eps, xs, red);
+  rows::load_x(xr, XLds{xs, 0, (cols >> 5) * 16}, u);
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int r = 0; r < RPW; r++) un[r].load(rows::seg_row(sg, min(pr.row0 + r, rows - 1)), 0, 0, 0, u);
-  __builtin_amdgcn_sched_barrier(0);
-  norm_row_to_lds<kNT>(nr, cols, nm.eps, xs, red);
-  rows::load_x(xr, XLds{xs, 0, (cols >> 5) * 16}, u);
   const int64_t slot = (int64_t)(rp.kv_index ? rp.kv_index[pos] : pos) * rp.kvw;
   for (;;) {
     // rope_theta's arithmetic on the preloaded step and factor
