@@ -228,14 +228,54 @@ __device__ __forceinline__ float half_bits_to_float(uint32_t h16) {
   return __half2float(__ushort_as_half((unsigned short)(h16 & 0xFFFFu)));
 }
 
-__device__ __forceinline__ float wave_sum(float v) {
-  v += __shfl_xor(v, 32);
-  v += __shfl_xor(v, 16);
-  v += __shfl_xor(v, 8);
-  v += __shfl_xor(v, 4);
-  v += __shfl_xor(v, 2);
-  v += __shfl_xor(v, 1);
+// ---- lane exchanges without the LDS unit ------------------------------------
+// __shfl_xor is a ds_bpermute: an LDS-unit round trip (about a hundred
+// cycles), and a reduction chains six of them.  These reductions use DPP
+// (quad permutes and the 8- and 16-lane mirrors, which pair every lane with
+// one of the other half once the halves are uniform) and gfx950's
+// v_permlane16_swap / v_permlane32_swap (rows 0 <-> 1 and 2 <-> 3, or the
+// wave's two halves), each a VALU instruction.  Every lane of the wave must
+// be active.  Results are uniform over the reduced lanes; a float sum adds
+// in a fixed order, so every call with the same inputs gives the same bits.
+namespace lanes {
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, CTRL, 0xF, 0xF, false);
+}
+constexpr int kXor1 = 0xB1, kXor2 = 0x4E, kHalfMirror = 0x141, kMirror = 0x140;
+// within each 4 lanes, lane i reads lane i + 1 (kDown1) or i + 2 (kDown2);
+// the last lanes read themselves (as __shfl_down(v, 1 or 2, 4))
+constexpr int kDown1 = 0xF9, kDown2 = 0xEE;
+struct Add {
+  __device__ __forceinline__ float operator()(float a, float b) const { return a + b; }
+  __device__ __forceinline__ int operator()(int a, int b) const { return a + b; }
+};
+struct Max {
+  __device__ __forceinline__ float operator()(float a, float b) const { return fmaxf(a, b); }
+};
+__device__ __forceinline__ uint32_t bits(float v) { return __float_as_uint(v); }
+__device__ __forceinline__ uint32_t bits(int v) { return (uint32_t)v; }
+__device__ __forceinline__ float back(uint32_t b, float) { return __uint_as_float(b); }
+__device__ __forceinline__ int back(uint32_t b, int) { return (int)b; }
+// all-reduce over each group of N = 2, 4, 8, 16, 32 or 64 aligned lanes
+template <int N, class T, class Op>
+__device__ __forceinline__ T reduce(T v, Op op) {
+  if constexpr (N >= 2) v = op(v, back(dpp<kXor1>(bits(v)), v));
+  if constexpr (N >= 4) v = op(v, back(dpp<kXor2>(bits(v)), v));
+  if constexpr (N >= 8) v = op(v, back(dpp<kHalfMirror>(bits(v)), v));
+  if constexpr (N >= 16) v = op(v, back(dpp<kMirror>(bits(v)), v));
+  if constexpr (N >= 32) {
+    const auto p = __builtin_amdgcn_permlane16_swap(bits(v), bits(v), false, false);
+    v = op(back(p[0], v), back(p[1], v));
+  }
+  if constexpr (N >= 64) {
+    const auto p = __builtin_amdgcn_permlane32_swap(bits(v), bits(v), false, false);
+    v = op(back(p[0], v), back(p[1], v));
+  }
   return v;
 }
+}  // namespace lanes
+
+__device__ __forceinline__ float wave_sum(float v) { return lanes::reduce<64>(v, lanes::Add{}); }
 
 }  // namespace mi

@@ -792,14 +792,12 @@ __global__ void attend_merge_kernel(const float* __restrict__ part_acc, const fl
   const int lane = threadIdx.x & 63;
   float M = -INFINITY;
   for (int c = lane; c < chunks; c += kWave) M = fmaxf(M, mls[2 * c]);
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) M = fmaxf(M, __shfl_xor(M, o));
+  M = lanes::reduce<64>(M, lanes::Max{});
   for (int c = threadIdx.x; c < padded; c += blockDim.x) wts[c] = c < chunks ? expf(mls[2 * c] - M) : 0.0f;
   __syncthreads();
   float L = 0.0f;
   for (int c = lane; c < chunks; c += kWave) L += mls[2 * c + 1] * wts[c];
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) L += __shfl_xor(L, o);
+  L = lanes::reduce<64>(L, lanes::Add{});
   float o = 0.0f;
   for (int c0 = 0; c0 < chunks; c0 += kMergeBatch) {
     if (c0 > 0) {
@@ -921,8 +919,7 @@ __global__ __launch_bounds__(NT) void attend_wide_kernel(
         sdot = fmaf(qb.w, k3.y, sdot);
       }
     }
-#pragma unroll
-    for (int o = 1; o < S::SPL; o <<= 1) sdot += __shfl_xor(sdot, o);
+    sdot = lanes::reduce<S::SPL>(sdot, lanes::Add{});
     if (part == 0 && dot < GROUP * KK) {
       const bool live = key < nk && (!kv_index || kv_cell(kv_index, index_stride, t, start + key) >= 0);
       Ss[g * KK + key] = live ? sdot * scale : -INFINITY;
@@ -934,12 +931,10 @@ __global__ __launch_bounds__(NT) void attend_wide_kernel(
   if (wave < GROUP) {
     const float sc = Ss[wave * KK + lane];
     float m = sc;
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    m = lanes::reduce<64>(m, lanes::Max{});
     const float pr = sc == -INFINITY ? 0.0f : expf(sc - m);
     float l = pr;
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) l += __shfl_xor(l, o);
+    l = lanes::reduce<64>(l, lanes::Add{});
     Ss[wave * KK + lane] = pr;
     if (lane == 0) *(float2*)(part_ml + (slot0 + (int64_t)wave * max_chunks + c) * 2) = make_float2(m, l);
   }
@@ -958,11 +953,8 @@ __global__ __launch_bounds__(NT) void attend_wide_kernel(
       a1 = fmaf(p, v.y, a1);
     }
   }
-#pragma unroll
-  for (int o = 1; o < S::KQ; o <<= 1) {
-    a0 += __shfl_xor(a0, o);
-    a1 += __shfl_xor(a1, o);
-  }
+  a0 = lanes::reduce<S::KQ>(a0, lanes::Add{});
+  a1 = lanes::reduce<S::KQ>(a1, lanes::Add{});
   if (kq == 0 && oe < GROUP * PAIRS)
     *(float2*)(part_acc + (slot0 + (int64_t)g * max_chunks + c) * D + 2 * e) = make_float2(a0, a1);
 }

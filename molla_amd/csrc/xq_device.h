@@ -20,7 +20,7 @@ __device__ __forceinline__ void hx_group32(int X, int lane32, int g, uint8_t* __
   const uint32_t pair = (uint32_t)__builtin_bit_cast(uint16_t, hi) |
                         ((uint32_t)__builtin_bit_cast(uint16_t, lo) << 16);
   // lanes 2j and 2j + 1: (hi, hi') and (lo, lo') as two dwords
-  const uint32_t other = (uint32_t)__shfl_down((int)pair, 1, 32);
+  const uint32_t other = lanes::dpp<lanes::kDown1>(pair);
   if (!live || (lane32 & 1)) return;
   const int kq = lane32 >> 3, u = lane32 & 7;
   uint8_t* e = hxtok + (int64_t)g * 128 + kq * 32 + u * 2;
@@ -35,9 +35,7 @@ __device__ __forceinline__ void hx_group32(int X, int lane32, int g, uint8_t* __
 __device__ __forceinline__ void quantize_group32(float v, int lane32, int g, int G,
                                                  uint8_t* __restrict__ xtok, bool live,
                                                  uint8_t* __restrict__ hxtok = nullptr) {
-  float a = fabsf(v);
-#pragma unroll
-  for (int m = 16; m >= 1; m >>= 1) a = fmaxf(a, __shfl_xor(a, m));
+  const float a = lanes::reduce<32>(fabsf(v), lanes::Max{});
   int E;
   (void)frexpf(a, &E);                // a = f * 2^E, f in [0.5, 1)
   const int e = (a > 0.0f) ? E - 22 : 0;  // a * 2^-e in [2^21, 2^22)
@@ -46,24 +44,20 @@ __device__ __forceinline__ void quantize_group32(float v, int lane32, int g, int
   const int X1 = (X - L3) >> 8;
   const int L2 = (int)(int8_t)(X1 & 0xFF);
   const int L1 = (X1 - L2) >> 8;
-  int s1 = L1, s23 = L2 * 256 + L3, sx = X;
-#pragma unroll
-  for (int m = 8; m >= 1; m >>= 1) {
-    s1 += __shfl_xor(s1, m);
-    s23 += __shfl_xor(s23, m);
-  }
-#pragma unroll
-  for (int m = 16; m >= 1; m >>= 1) sx += __shfl_xor(sx, m);
-  const int other1 = __shfl_xor(s1, 16);
-  const int other23 = __shfl_xor(s23, 16);
+  // this half's limb sums (16 values) and the other half's: the group's
+  // sum less this half's (exact integers)
+  const int s1 = lanes::reduce<16>(L1, lanes::Add{}), s23 = lanes::reduce<16>(L2 * 256 + L3, lanes::Add{});
+  const int other1 = lanes::reduce<32>(L1, lanes::Add{}) - s1;
+  const int other23 = lanes::reduce<32>(L2 * 256 + L3, lanes::Add{}) - s23;
+  const int sx = lanes::reduce<32>(X, lanes::Add{});
   if (hxtok) hx_group32(X, lane32, g, hxtok, live);
   // Gather each limb's bytes four lanes to a dword: byte stores from every
   // lane cost the memory system far more than a quarter as many dword stores.
   uint32_t w[3] = {(uint32_t)L1 & 0xFFu, (uint32_t)L2 & 0xFFu, (uint32_t)L3 & 0xFFu};
 #pragma unroll
   for (int j = 0; j < 3; j++) {
-    w[j] |= (uint32_t)__shfl_down((int)w[j], 1, 4) << 8;
-    w[j] |= (uint32_t)__shfl_down((int)w[j], 2, 4) << 16;
+    w[j] |= lanes::dpp<lanes::kDown1>(w[j]) << 8;
+    w[j] |= lanes::dpp<lanes::kDown2>(w[j]) << 16;
   }
   if (!live) return;
   const int hh = lane32 >> 4, b = lane32 & 15;
@@ -128,8 +122,7 @@ __device__ __forceinline__ void quantize8_to_lds(const float (&v)[8], bool live,
   float a = 0.0f;
 #pragma unroll
   for (int k = 0; k < 8; k++) a = fmaxf(a, fabsf(v[k]));
-  a = fmaxf(a, __shfl_xor(a, 1));
-  a = fmaxf(a, __shfl_xor(a, 2));
+  a = lanes::reduce<4>(a, lanes::Max{});
   int E;
   (void)frexpf(a, &E);
   const int e = (a > 0.0f) ? E - 22 : 0;
@@ -151,12 +144,12 @@ __device__ __forceinline__ void quantize8_to_lds(const float (&v)[8], bool live,
     w[2][k >> 2] |= ((uint32_t)L3 & 0xFFu) << sh;
   }
   // lanes 4q, 4q+1 hold half 0 of group q, lanes 4q+2, 4q+3 half 1
-  s1 += __shfl_xor(s1, 1);
-  s23 += __shfl_xor(s23, 1);
-  sx += __shfl_xor(sx, 1);
-  sx += __shfl_xor(sx, 2);
-  const int other1 = __shfl_xor(s1, 2);
-  const int other23 = __shfl_xor(s23, 2);
+  const int h1 = lanes::reduce<2>(s1, lanes::Add{}), h23 = lanes::reduce<2>(s23, lanes::Add{});
+  const int other1 = lanes::reduce<4>(s1, lanes::Add{}) - h1;
+  const int other23 = lanes::reduce<4>(s23, lanes::Add{}) - h23;
+  s1 = h1;
+  s23 = h23;
+  sx = lanes::reduce<4>(sx, lanes::Add{});
   if (live) {
     const int grp = i0 >> 5, k4 = t & 3, hh = k4 >> 1;
     const int plane = (n >> 5) * 16;
