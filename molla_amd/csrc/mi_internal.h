@@ -274,6 +274,36 @@ __device__ __forceinline__ T reduce(T v, Op op) {
   }
   return v;
 }
+// all-reduce of a float64 sum over each group of N aligned lanes, the two
+// dwords moved together
+template <int CTRL>
+__device__ __forceinline__ double dpp_d(double v) {
+  const uint64_t b = __double_as_longlong(v);
+  const uint64_t lo = dpp<CTRL>((uint32_t)b), hi = dpp<CTRL>((uint32_t)(b >> 32));
+  return __longlong_as_double((long long)(lo | (hi << 32)));
+}
+template <int N>
+__device__ __forceinline__ double reduce_sum(double v) {
+  if constexpr (N >= 2) v += dpp_d<kXor1>(v);
+  if constexpr (N >= 4) v += dpp_d<kXor2>(v);
+  if constexpr (N >= 8) v += dpp_d<kHalfMirror>(v);
+  if constexpr (N >= 16) v += dpp_d<kMirror>(v);
+  if constexpr (N >= 32) {
+    const uint64_t b = __double_as_longlong(v);
+    const auto lo = __builtin_amdgcn_permlane16_swap((uint32_t)b, (uint32_t)b, false, false);
+    const auto hi = __builtin_amdgcn_permlane16_swap((uint32_t)(b >> 32), (uint32_t)(b >> 32), false, false);
+    v = __longlong_as_double((long long)(lo[0] | ((uint64_t)hi[0] << 32))) +
+        __longlong_as_double((long long)(lo[1] | ((uint64_t)hi[1] << 32)));
+  }
+  if constexpr (N >= 64) {
+    const uint64_t b = __double_as_longlong(v);
+    const auto lo = __builtin_amdgcn_permlane32_swap((uint32_t)b, (uint32_t)b, false, false);
+    const auto hi = __builtin_amdgcn_permlane32_swap((uint32_t)(b >> 32), (uint32_t)(b >> 32), false, false);
+    v = __longlong_as_double((long long)(lo[0] | ((uint64_t)hi[0] << 32))) +
+        __longlong_as_double((long long)(lo[1] | ((uint64_t)hi[1] << 32)));
+  }
+  return v;
+}
 }  // namespace lanes
 
 __device__ __forceinline__ float wave_sum(float v) { return lanes::reduce<64>(v, lanes::Add{}); }

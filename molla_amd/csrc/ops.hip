@@ -68,8 +68,7 @@ __global__ __launch_bounds__(kNormThreads) void rms_norm_kernel(const float* __r
   double acc = 0.0;
 #pragma unroll
   for (int k = 0; k < PER; k++) acc += (double)xv[k] * (double)xv[k];
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) acc += __shfl_xor(acc, m);
+  acc = lanes::reduce_sum<64>(acc);
   __shared__ double part[kNormThreads / kWave];
   if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = acc;
   __syncthreads();
@@ -970,8 +969,7 @@ __global__ __launch_bounds__(64) void head_norm_kernel(float* __restrict__ x, in
   float* run = x + (int64_t)blockIdx.y * row_stride + (int64_t)blockIdx.x * n;
   double acc = 0.0;
   for (int i = threadIdx.x; i < n; i += 64) acc += (double)run[i] * (double)run[i];
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) acc += __shfl_xor(acc, m);
+  acc = lanes::reduce_sum<64>(acc);
   const float scale = (float)(1.0 / sqrt(acc / (double)n + (double)eps));
   for (int i = threadIdx.x; i < n; i += 64) run[i] = run[i] * scale * gain[i];
 }
@@ -986,8 +984,7 @@ __global__ __launch_bounds__(256) void norm_add_kernel(float* __restrict__ resid
   float* rr = resid + (int64_t)blockIdx.x * n;
   double acc = 0.0;
   for (int i = threadIdx.x; i < n; i += 256) acc += (double)yr[i] * (double)yr[i];
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) acc += __shfl_xor(acc, m);
+  acc = lanes::reduce_sum<64>(acc);
   __shared__ double part[4];
   if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = acc;
   __syncthreads();

@@ -181,8 +181,7 @@ __device__ __forceinline__ void norm_row_to_lds(const NormRow& nr, int n, float 
   double acc = 0.0;
 #pragma unroll
   for (int k = 0; k < 8; k++) acc += live ? (double)v[k] * (double)v[k] : 0.0;
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) acc += __shfl_xor(acc, m);
+  acc = lanes::reduce_sum<64>(acc);
   if ((t & 63) == 0) red[t >> 6] = acc;
   __syncthreads();
   double sum = 0.0;
