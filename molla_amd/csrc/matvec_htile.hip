@@ -226,7 +226,8 @@ __global__ __launch_bounds__(kMaxHWaves * 64) void htile_kernel(const RowSegs sg
                                                                      const uint8_t* __restrict__ hx,
                                                                      float* __restrict__ y, int64_t ldy, int epi,
                                                                      const float* __restrict__ aux,
-                                                                     uint8_t* __restrict__ xq_out) {
+                                                                     uint8_t* __restrict__ xq_out, int gtot,
+                                                                     int64_t ysplit) {
   constexpr int SB = HGeo<KIND>::SB, kLdsRow = HGeo<KIND>::ROW, kLoads = kLoadsOf<KIND>;
   __shared__ __align__(16) uint8_t wl[2][kTileBuf];
   __shared__ float part[2][kMaxHWaves][16][17];
@@ -235,9 +236,13 @@ __global__ __launch_bounds__(kMaxHWaves * 64) void htile_kernel(const RowSegs sg
   const int lm = lane & 15, kq = lane >> 4;
   const int rows = sg.end[sg.nseg - 1];
   const int tiles = (rows + 15) >> 4;
-  const int G = cols >> 5;
-  const int rb = (cols >> 8) * SB;  // bytes per row; the tile is 16 rows in a run
-  const int64_t tok_bytes = xq_token_bytes(cols);
+  // Split K: block row blockIdx.y takes columns [y cols, (y + 1) cols) of
+  // rows gtot * 32 long and writes its partial sums ysplit floats further on.
+  const int G = cols >> 5, g0 = (int)blockIdx.y * G;
+  const int rb = (cols >> 8) * SB;  // bytes of a row this block reads
+  const int64_t rstride = sg.rb[0];  // bytes between rows (every segment's)
+  const int64_t tok_bytes = xq_token_bytes(gtot * 32);
+  y += (int64_t)blockIdx.y * ysplit;
   const int step = gridDim.x;
   // the k-th tile of this block: tile blockIdx.x + k step, or under GLU tile
   // k % 4 of 32-row group blockIdx.x + (k / 4) step
@@ -257,7 +262,7 @@ __global__ __launch_bounds__(kMaxHWaves * 64) void htile_kernel(const RowSegs sg
 
   // This lane's share of a tile: 8-byte words threadIdx.x + blockDim.x * j,
   // and where each lands in the padded LDS rows.
-  int ldso[kLoads];
+  int ldso[kLoads], wrow[kLoads], woff[kLoads];
 #pragma unroll
   for (int j = 0; j < kLoads; j++) {
     // o / rb through a float reciprocal (o < 2^16: exact after one
@@ -269,14 +274,16 @@ __global__ __launch_bounds__(kMaxHWaves * 64) void htile_kernel(const RowSegs sg
     row -= row * rb > o;
     row += (row + 1) * rb <= o;
     ldso[j] = row * kLdsRow + (o - row * rb);
+    wrow[j] = row;
+    woff[j] = o - row * rb;
   }
   // A last tile of fewer than 16 rows reads its last word again in place of
   // the missing rows (whose sums are never stored): loads stay unconditional.
   auto load_tile = [&](uint2 (&r)[kLoads], int tl) __attribute__((always_inline)) {
-    const uint2* src = (const uint2*)rows::seg_row(sg, tl * 16);
-    const int words = min(16, rows - tl * 16) * (rb >> 3);
+    const uint8_t* src = rows::seg_row(sg, tl * 16) + (int64_t)blockIdx.y * rb;
+    const int last = min(16, rows - tl * 16) - 1;
 #pragma unroll
-    for (int j = 0; j < kLoads; j++) r[j] = src[min((int)threadIdx.x + (int)blockDim.x * j, words - 1)];
+    for (int j = 0; j < kLoads; j++) r[j] = *(const uint2*)(src + min(wrow[j], last) * rstride + woff[j]);
   };
   auto store_tile = [&](const uint2 (&r)[kLoads], int buf) __attribute__((always_inline)) {
 #pragma unroll
@@ -301,9 +308,9 @@ __global__ __launch_bounds__(kMaxHWaves * 64) void htile_kernel(const RowSegs sg
 #pragma unroll
   for (int j = 0; j < 2 * TN; j++) {
     const int u = j >> 1, w = (int)threadIdx.x + (j & 1) * (int)blockDim.x;
-    v[j] = *(const uu4*)(hx + u * tok_bytes + w * 16);
+    v[j] = *(const uu4*)(hx + u * tok_bytes + g0 * 128 + w * 16);
   }
-  const float* scale_src = &((const XMeta*)(xq + 6 * (int64_t)G * 16))->scale;
+  const float* scale_src = &((const XMeta*)(xq + 6 * (int64_t)gtot * 16 + g0 * 16))->scale;
   float scl[TN];  // thread g < G: group g's scale of every token
   const int sg_g = min((int)threadIdx.x, G - 1);
 #pragma unroll
@@ -411,8 +418,9 @@ __global__ __launch_bounds__(kMaxHWaves * 64) void htile_kernel(const RowSegs sg
       const int j = blockIdx.x + (kk >> 2) * step;
       for (int u0 = 2 * wave; u0 < TN; u0 += 2 * nw) {  // a block of one wave takes every token
         const int u = u0 + (lane >> 5);
-        quantize_group32(hbuf[lane & 31][u < TN ? u : 0], lane & 31, j, jobs,
-                         xq_out + (int64_t)(u < TN ? u : 0) * xq_token_bytes(gl_rows), u < TN);
+        const int uu = u < TN ? u : 0;
+        quantize_group32(hbuf[lane & 31][uu], lane & 31, j, jobs, xq_out + (int64_t)uu * xq_token_bytes(gl_rows),
+                         u < TN, (epi & kEpiHx) ? xq_out + (int64_t)(TN + uu) * xq_token_bytes(gl_rows) : nullptr);
       }
     }
   };
@@ -458,6 +466,19 @@ __global__ __launch_bounds__(kMaxHWaves * 64) void htile_kernel(const RowSegs sg
   }
 }
 
+// The parts of a split-K htile (part[k][t][r], k < nsplit) added in part
+// order, then the epilogue.
+__global__ void htile_split_reduce_kernel(const float* __restrict__ part, int nsplit, int tn, int rows,
+                                          float* __restrict__ y, int64_t ldy, int epi, const float* __restrict__ aux) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= tn * rows) return;
+  const int t = i / rows, r = i - t * rows;
+  const int64_t n = (int64_t)tn * rows;
+  float v = part[i];
+  for (int k = 1; k < nsplit; k++) v += part[k * n + i];
+  epilogue(y, aux, epi, (int64_t)t * ldy + r, r, v);
+}
+
 int cu_count_h() {
   static int cus[64];
   int dev = 0;
@@ -489,10 +510,10 @@ int launch_htile(hipStream_t s, int kind, const RowSegs& sg, int32_t rows, int32
   case T:                                                                                                     \
     if (kind == MI_Q6_K)                                                                                      \
       hipLaunchKernelGGL((htile_kernel<T, MI_Q6_K, false>), dim3(grid), dim3(waves * 64), 0, s, sg, cols,     \
-                         (const uint8_t*)xq, (const uint8_t*)hx, y, ldy, epi, aux, nullptr);                 \
+                         (const uint8_t*)xq, (const uint8_t*)hx, y, ldy, epi, aux, nullptr, cols / 32, 0); \
     else                                                                                                      \
       hipLaunchKernelGGL((htile_kernel<T, MI_Q4_K, false>), dim3(grid), dim3(waves * 64), 0, s, sg, cols,     \
-                         (const uint8_t*)xq, (const uint8_t*)hx, y, ldy, epi, aux, nullptr);                 \
+                         (const uint8_t*)xq, (const uint8_t*)hx, y, ldy, epi, aux, nullptr, cols / 32, 0); \
     break;
   switch (tokens) {
     MI_HT(2) MI_HT(3) MI_HT(4) MI_HT(5) MI_HT(6) MI_HT(7) MI_HT(8)
@@ -502,12 +523,58 @@ int launch_htile(hipStream_t s, int kind, const RowSegs& sg, int32_t rows, int32
   return hip_check(hipGetLastError(), "htile launch");
 }
 
+// Split K for rows longer than one block's 4096 columns (the down
+// projection's 14336 = 4 x 3584): parts of a multiple of 512 columns.
+static int htile_nsplit(int32_t cols) {
+  for (int n = (cols + 4095) / 4096; n <= 8; n++)
+    if (cols % (n * 256 * kSBW) == 0) return n;
+  return 0;
+}
+
+bool htile_split_fits(int32_t rows, int32_t cols, int32_t tokens) {
+  const int n = htile_nsplit(cols);
+  return n > 1 && htile_fits(MI_Q4_K, rows, cols / n, tokens);
+}
+
+size_t htile_split_bytes(int32_t rows, int32_t cols, int32_t tokens) {
+  return sizeof(float) * (size_t)htile_nsplit(cols) * rows * tokens;
+}
+
+int launch_htile_split(hipStream_t s, const void* w, int64_t row_bytes, int32_t rows, int32_t cols, const void* xq,
+                       const void* hx, int32_t tokens, float* y, int64_t ldy, int32_t epi, const float* aux,
+                       float* part) {
+  if (!htile_split_fits(rows, cols, tokens) || row_bytes != (int64_t)(cols / 256) * HGeo<MI_Q4_K>::SB ||
+      ((uintptr_t)w & 7))
+    return fail(MI_ERR_SHAPE, "htile: no split-K tile for %d x %d at %d tokens", rows, cols, tokens);
+  const int n = htile_nsplit(cols), pc = cols / n;
+  const RowSegs sg = rows::one_matrix(w, row_bytes, rows);
+  const int waves = pc / (256 * kSBW);
+  const int grid = std::min((rows + 15) / 16, std::max(1, cu_count_h() / n));
+  const int64_t ysplit = (int64_t)tokens * rows;
+#define MI_HS(T)                                                                                              \
+  case T:                                                                                                     \
+    hipLaunchKernelGGL((htile_kernel<T, MI_Q4_K, false>), dim3(grid, n), dim3(waves * 64), 0, s, sg, pc,      \
+                       (const uint8_t*)xq, (const uint8_t*)hx, part, (int64_t)rows, MI_EPI_NONE, nullptr,     \
+                       nullptr, cols / 32, ysplit);                                                           \
+    break;
+  switch (tokens) {
+    MI_HS(2) MI_HS(3) MI_HS(4) MI_HS(5) MI_HS(6) MI_HS(7) MI_HS(8)
+    default: return fail(MI_ERR_ARG, "htile: %d tokens", tokens);
+  }
+#undef MI_HS
+  int rc = hip_check(hipGetLastError(), "htile launch");
+  if (rc) return rc;
+  hipLaunchKernelGGL(htile_split_reduce_kernel, dim3((tokens * rows + 255) / 256), dim3(256), 0, s, part, n, tokens,
+                     rows, y, ldy, epi, aux);
+  return hip_check(hipGetLastError(), "htile split reduce");
+}
+
 bool htile_glu_fits(int32_t rows, int32_t cols, int32_t tokens) {
   return htile_fits(MI_Q4_K, 2 * rows, cols, tokens) && rows % 32 == 0;
 }
 
 int launch_htile_glu(hipStream_t s, const void* gate, const void* up, int64_t row_bytes, int32_t rows, int32_t cols,
-                     const void* xq, const void* hx, int32_t tokens, int32_t act, void* xq_out) {
+                     const void* xq, const void* hx, int32_t tokens, int32_t act, void* xq_out, bool hx_out) {
   if (!htile_glu_fits(rows, cols, tokens) || row_bytes != (int64_t)(cols / 256) * HGeo<MI_Q4_K>::SB ||
       (((uintptr_t)gate | (uintptr_t)up) & 7))
     return fail(MI_ERR_SHAPE, "htile: no GLU tile for %d x %d at %d tokens", rows, cols, tokens);
@@ -523,8 +590,9 @@ int launch_htile_glu(hipStream_t s, const void* gate, const void* up, int64_t ro
 #define MI_HTG(T)                                                                                             \
   case T:                                                                                                     \
     hipLaunchKernelGGL((htile_kernel<T, MI_Q4_K, true>), dim3(grid), dim3(waves * 64), 0, s, sg, cols,        \
-                       (const uint8_t*)xq, (const uint8_t*)hx, nullptr, 0, act & MI_ACT_GELU, nullptr,        \
-                       (uint8_t*)xq_out);                                                                     \
+                       (const uint8_t*)xq, (const uint8_t*)hx, nullptr, 0,                                  \
+                       (act & MI_ACT_GELU) | (hx_out ? kEpiHx : 0), nullptr,                                  \
+                       (uint8_t*)xq_out, cols / 32, 0);                                                       \
     break;
   switch (tokens) {
     MI_HTG(2) MI_HTG(3) MI_HTG(4) MI_HTG(5) MI_HTG(6) MI_HTG(7) MI_HTG(8)

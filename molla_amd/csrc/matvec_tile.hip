@@ -230,7 +230,9 @@ __global__ __launch_bounds__(KW * 64) void q4k_tile_kernel(const RowSegs sg, int
       else y[at] = o2;
       // a half-wave holds one token's 32 rows of this tile: one xq group
       // (rows % 32 == 0, so every lane of it is live)
-      if (xq_out) quantize_group32(o2, nn, r >> 5, rows >> 5, xq_out + (int64_t)t * xq_token_bytes(rows), true);
+      if (xq_out)
+        quantize_group32(o2, nn, r >> 5, rows >> 5, xq_out + (int64_t)t * xq_token_bytes(rows), true,
+                         (epi & kEpiHx) ? xq_out + (int64_t)(tn + t) * xq_token_bytes(rows) : nullptr);
     } else {
       epilogue(y, aux, epi, (int64_t)t * ldy + r, r, v);
     }

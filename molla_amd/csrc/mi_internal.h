@@ -159,15 +159,28 @@ int launch_matvec(hipStream_t s, int kind, const void* w, int64_t row_bytes, int
 // rows of up to three matrices whose ends (but the last) are whole 16-row
 // tiles, 8-byte aligned, reading the xq form (group scales) and the hx form
 // of the same tokens.
+// Internal epilogue bit of the GLU tiles: the quantized output xq_out is
+// followed, tokens * 4 * rows bytes on, by its hx form (the f16 tile's input).
+constexpr int kEpiHx = 1 << 16;
 bool htile_fits(int kind, int32_t rows, int32_t cols, int32_t tokens);
+// Q4_K rows longer than 4096 columns on the f16 tile: K split over column
+// parts (part: htile_split_bytes of scratch), then one reduce launch that adds
+// the parts in order and applies the epilogue.
+bool htile_split_fits(int32_t rows, int32_t cols, int32_t tokens);
+size_t htile_split_bytes(int32_t rows, int32_t cols, int32_t tokens);
+int launch_htile_split(hipStream_t s, const void* w, int64_t row_bytes, int32_t rows, int32_t cols, const void* xq,
+                       const void* hx, int32_t tokens, float* y, int64_t ldy, int32_t epi, const float* aux,
+                       float* part);
 int launch_htile(hipStream_t s, int kind, const RowSegs& sg, int32_t rows, int32_t cols, const void* xq,
                  const void* hx, int32_t tokens, float* y, int64_t ldy, int32_t epi, const float* aux);
 // The gated MLP's input side on the same tile (Q4_K gate and up of `rows` x
 // `cols`, rows a multiple of 32): act(gate) * up written only in matvec form
-// into xq_out (`rows` values a token), for the down projection.
+// into xq_out (`rows` values a token), for the down projection; with hx_out,
+// also its hx form, tokens * 4 * rows bytes past xq_out.
 bool htile_glu_fits(int32_t rows, int32_t cols, int32_t tokens);
 int launch_htile_glu(hipStream_t s, const void* gate, const void* up, int64_t row_bytes, int32_t rows, int32_t cols,
-                     const void* xq, const void* hx, int32_t tokens, int32_t act, void* xq_out);
+                     const void* xq, const void* hx, int32_t tokens, int32_t act, void* xq_out,
+                     bool hx_out = false);
 // rms_norm_trig: also writes trig[p] = (cos, sin) of f32(pos[0]) * steps[p]
 // (divided by factors[p] when factors is given) for p < pairs (float64 trig,
 // as rope.mojo:253-285), for the fused q|k|v epilogue of the same layer.

@@ -96,9 +96,14 @@ def llama31_factors(pairs):
     # odd token count for its per-token quantize)
     ((512, 1024, 8, 2, 64), 300, 5, False),
     ((4096, 14336, 32, 8, 128), 4096, 1, False),   # config 4
-    # an MLP of 8192: the batched down projection splits K over two blocks
+    # an MLP of 8192: at 4+ tokens the batched down projection runs on the f16
+    # tile split over two 4096-column parts (the GLU tile writes its hx form)
     ((1024, 8192, 8, 2, 128), 200, 4, False),
     ((1024, 8192, 8, 2, 128), 200, 8, False),
+    # an MLP of 14336: four 3584-column parts, from the int8 GLU tile (4
+    # tokens) and the f16 GLU tile (6 tokens)
+    ((1024, 14336, 8, 2, 128), 200, 4, False),
+    ((1024, 14336, 8, 2, 128), 200, 6, False),
     # full multi-head attention: a q|k|v of 12288 rows is more 24-row groups
     # than CUs, so the folded-norm q|k|v kernel loops (rope step and factor
     # reloaded per group)
