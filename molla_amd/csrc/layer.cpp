@@ -459,7 +459,9 @@ static int decoder_layer(mi_stream stream, const mi_layer_desc* d, float* resid,
       if ((rc = launch_q4k_qkv_rope(s, sg, d->width, xq, qkv, rp))) return rc;
     }
   } else {
-    if ((rc = launch_rms_norm(s, resid, d->attn_norm, d->width, tokens, d->eps, nullptr, xq))) return rc;
+    // at 2..8 tokens the norm also writes the hx form (the f16 tile's input)
+    void* hxn = tokens > 1 ? (uint8_t*)xq + (size_t)xq_token_bytes(d->width) * tokens : nullptr;
+    if ((rc = launch_rms_norm(s, resid, d->attn_norm, d->width, tokens, d->eps, nullptr, xq, hxn))) return rc;
     bool roped = false;
     const bool tile_qkv = tokens > 1 && d->wq.kind == MI_Q4_K && d->wk.kind == MI_Q4_K &&
                           d->wv.kind == MI_Q4_K && q4k_tile_fits(d->width, tokens);
@@ -494,7 +496,11 @@ static int decoder_layer(mi_stream stream, const mi_layer_desc* d, float* resid,
         rp.factors = d->rope_factors;
         rp.cache_stride = cache_stride;
         rp.index_stride = index_stride;
-        if ((rc = launch_q4k_tile_qkv_rope(s, tg, d->width, xq, tokens, qkv, qkv_stride, rp))) return rc;
+        if (htile_qkv_rope_fits(tg, d->width, tokens, d->head_dim, d->rope_dim))
+          rc = launch_htile_qkv_rope(s, tg, d->width, xq, hxn, tokens, qkv, qkv_stride, rp);
+        else
+          rc = launch_q4k_tile_qkv_rope(s, tg, d->width, xq, tokens, qkv, qkv_stride, rp);
+        if (rc) return rc;
         roped = true;
       } else if ((rc = launch_q4k_tile_segs(s, tg, d->width, xq, tokens, qkv, qkv_stride))) {
         return rc;

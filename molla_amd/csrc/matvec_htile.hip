@@ -55,6 +55,7 @@ typedef uint32_t uu4 __attribute__((ext_vector_type(4)));
 
 constexpr int kSBW = 2;                                  // superblocks per wave
 constexpr int kMaxHWaves = 8;                            // cols <= 8 * 512
+constexpr int kMaxRopePairs = 128;                       // rope_dim <= 256 for the rope epilogue
 
 // Per kind: superblock bytes, and the LDS row stride of a tile (the row at
 // 4096 columns, so that a fragment read's 16 rows start 8 banks apart: Q4_K
@@ -220,14 +221,17 @@ __device__ __forceinline__ void sb_product_q6k(const uint8_t* lrows, int sb, con
 // 0-15, gate rows 16-31, up rows 16-31), and writes act(gate) * up of each
 // group only in matvec form, into xq_out (the down projection's input;
 // gpu_block.mojo device_swiglu then the quantize), one half-wave a token.
-template <int TN, int KIND, bool GLU>
+// ROPE (Q4_K, q|k|v rows): the epilogue of the batched int8 tile's rope form
+// (matvec_tile.hip): rows of q and k rotated in adjacent pairs at each
+// token's position, q to y, k and v to the f16 caches (rp).
+template <int TN, int KIND, bool GLU, bool ROPE = false>
 __global__ __launch_bounds__(kMaxHWaves * 64) void htile_kernel(const RowSegs sg, int cols,
                                                                      const uint8_t* __restrict__ xq,
                                                                      const uint8_t* __restrict__ hx,
                                                                      float* __restrict__ y, int64_t ldy, int epi,
                                                                      const float* __restrict__ aux,
                                                                      uint8_t* __restrict__ xq_out, int gtot,
-                                                                     int64_t ysplit) {
+                                                                     int64_t ysplit, const QkvRope rp) {
   constexpr int SB = HGeo<KIND>::SB, kLdsRow = HGeo<KIND>::ROW, kLoads = kLoadsOf<KIND>;
   __shared__ __align__(16) uint8_t wl[2][kTileBuf];
   __shared__ float part[2][kMaxHWaves][16][17];
@@ -388,6 +392,18 @@ __global__ __launch_bounds__(kMaxHWaves * 64) void htile_kernel(const RowSegs sg
   // gsum for the up tile of the same rows (the same thread takes the same
   // (row, token) every tile), whose act(gate) * up go to hbuf.
   __shared__ float gsum[GLU ? 2 : 1][16][TN], hbuf[GLU ? 32 : 1][TN];
+  // ROPE: (cos, sin) of every (token, pair), once per block, read by the
+  // finish of every tile (computed as rope_theta then float64 trig)
+  __shared__ float2 trig[ROPE ? TN * kMaxRopePairs : 1];
+  if constexpr (ROPE) {
+#pragma clang fp contract(off)
+    const int np = rp.rope_dim >> 1;
+    for (int i = threadIdx.x; i < TN * np; i += blockDim.x) {
+      const int u = i / np, pr = i - u * np;
+      const float theta = rope_theta(rp.pos[u], rp.steps, rp.factors, pr);
+      trig[u * kMaxRopePairs + pr] = make_float2((float)cos((double)theta), (float)sin((double)theta));
+    }
+  }
   auto finish = [&](int kk, int buf) __attribute__((always_inline)) {
     const int tl = tile_of(kk);
     for (int ix = lane * nw + wave; ix < 16 * TN; ix += 64 * nw) {
@@ -396,7 +412,37 @@ __global__ __launch_bounds__(kMaxHWaves * 64) void htile_kernel(const RowSegs sg
 #pragma unroll
       for (int w = 0; w < kMaxHWaves; w++)
         if (w < nw) v += part[buf][w][rr][2 * u] + part[buf][w][rr][2 * u + 1];
-      if constexpr (GLU) {
+      if constexpr (ROPE) {
+#pragma clang fp contract(off)
+        // the partner row's sum, added in the same order as its own thread's
+        float pv = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kMaxHWaves; w++)
+          if (w < nw) pv += part[buf][w][rr ^ 1][2 * u] + part[buf][w][rr ^ 1][2 * u + 1];
+        const int r = tl * 16 + rr;
+        if (r >= rows) continue;
+        // rope.mojo:294 rotate_scaled, adjacent pairs: (a, b) <- (a c - b s, a s + b c)
+        const int p = rp.pos[u];
+        const bool is_q = r < rp.qw, is_k = !is_q && r < rp.qw + rp.kvw;
+        float out = v;
+        if (is_q || is_k) {
+          const int e = (is_q ? r : r - rp.qw) % rp.head_dim;
+          if (e < rp.rope_dim) {
+            const float2 cs = trig[u * kMaxRopePairs + (e >> 1)];
+            const float c = cs.x, sn = cs.y;
+            const float a = (e & 1) ? pv : v, b = (e & 1) ? v : pv;
+            out = (e & 1) ? a * sn + b * c : a * c - b * sn;
+          }
+        }
+        if (is_q) {
+          y[(int64_t)u * ldy + r] = out;
+        } else {
+          const int64_t at = rp.kv_index ? (int64_t)rp.kv_index[u * rp.index_stride + p] * rp.kvw
+                                         : (int64_t)u * rp.cache_stride + (int64_t)p * rp.kvw;
+          if (is_k) rp.k_cache[at + (r - rp.qw)] = __float2half_rn(out);
+          else rp.v_cache[at + (r - rp.qw - rp.kvw)] = __float2half_rn(out);
+        }
+      } else if constexpr (GLU) {
         const int q = kk & 3;
         if (!(q & 1)) {
           gsum[q >> 1][rr][u] = v;
@@ -510,10 +556,10 @@ int launch_htile(hipStream_t s, int kind, const RowSegs& sg, int32_t rows, int32
   case T:                                                                                                     \
     if (kind == MI_Q6_K)                                                                                      \
       hipLaunchKernelGGL((htile_kernel<T, MI_Q6_K, false>), dim3(grid), dim3(waves * 64), 0, s, sg, cols,     \
-                         (const uint8_t*)xq, (const uint8_t*)hx, y, ldy, epi, aux, nullptr, cols / 32, 0); \
+                         (const uint8_t*)xq, (const uint8_t*)hx, y, ldy, epi, aux, nullptr, cols / 32, 0, QkvRope{}); \
     else                                                                                                      \
       hipLaunchKernelGGL((htile_kernel<T, MI_Q4_K, false>), dim3(grid), dim3(waves * 64), 0, s, sg, cols,     \
-                         (const uint8_t*)xq, (const uint8_t*)hx, y, ldy, epi, aux, nullptr, cols / 32, 0); \
+                         (const uint8_t*)xq, (const uint8_t*)hx, y, ldy, epi, aux, nullptr, cols / 32, 0, QkvRope{}); \
     break;
   switch (tokens) {
     MI_HT(2) MI_HT(3) MI_HT(4) MI_HT(5) MI_HT(6) MI_HT(7) MI_HT(8)
@@ -555,7 +601,7 @@ int launch_htile_split(hipStream_t s, const void* w, int64_t row_bytes, int32_t 
   case T:                                                                                                     \
     hipLaunchKernelGGL((htile_kernel<T, MI_Q4_K, false>), dim3(grid, n), dim3(waves * 64), 0, s, sg, pc,      \
                        (const uint8_t*)xq, (const uint8_t*)hx, part, (int64_t)rows, MI_EPI_NONE, nullptr,     \
-                       nullptr, cols / 32, ysplit);                                                           \
+                       nullptr, cols / 32, ysplit, QkvRope{});                                                \
     break;
   switch (tokens) {
     MI_HS(2) MI_HS(3) MI_HS(4) MI_HS(5) MI_HS(6) MI_HS(7) MI_HS(8)
@@ -567,6 +613,37 @@ int launch_htile_split(hipStream_t s, const void* w, int64_t row_bytes, int32_t 
   hipLaunchKernelGGL(htile_split_reduce_kernel, dim3((tokens * rows + 255) / 256), dim3(256), 0, s, part, n, tokens,
                      rows, y, ldy, epi, aux);
   return hip_check(hipGetLastError(), "htile split reduce");
+}
+
+bool htile_qkv_rope_fits(const RowSegs& sg, int32_t cols, int32_t tokens, int32_t head_dim, int32_t rope_dim) {
+  const int rows = sg.end[sg.nseg - 1];
+  if (!htile_fits(MI_Q4_K, rows, cols, tokens) || head_dim % 2 || rope_dim % 2 || rope_dim > 2 * kMaxRopePairs)
+    return false;
+  for (int i = 0; i < sg.nseg; i++)
+    if (sg.end[i] % 16 || sg.rb[i] != (int64_t)(cols / 256) * HGeo<MI_Q4_K>::SB || ((uintptr_t)sg.w[i] & 7))
+      return false;
+  return true;
+}
+
+int launch_htile_qkv_rope(hipStream_t s, const RowSegs& sg, int32_t cols, const void* xq, const void* hx,
+                          int32_t tokens, float* q, int64_t ldq, const QkvRope& rp) {
+  if (!htile_qkv_rope_fits(sg, cols, tokens, rp.head_dim, rp.rope_dim))
+    return fail(MI_ERR_SHAPE, "htile: no rope tile for %d columns at %d tokens", cols, tokens);
+  const int rows = sg.end[sg.nseg - 1];
+  const int waves = cols / (256 * kSBW);
+  const int grid = std::min((rows + 15) / 16, cu_count_h());
+#define MI_HR(T)                                                                                              \
+  case T:                                                                                                     \
+    hipLaunchKernelGGL((htile_kernel<T, MI_Q4_K, false, true>), dim3(grid), dim3(waves * 64), 0, s, sg, cols, \
+                       (const uint8_t*)xq, (const uint8_t*)hx, q, ldq, MI_EPI_NONE, nullptr, nullptr,         \
+                       cols / 32, 0, rp);                                                                     \
+    break;
+  switch (tokens) {
+    MI_HR(2) MI_HR(3) MI_HR(4) MI_HR(5) MI_HR(6) MI_HR(7) MI_HR(8)
+    default: return fail(MI_ERR_ARG, "htile: %d tokens", tokens);
+  }
+#undef MI_HR
+  return hip_check(hipGetLastError(), "htile launch");
 }
 
 bool htile_glu_fits(int32_t rows, int32_t cols, int32_t tokens) {
@@ -592,7 +669,7 @@ int launch_htile_glu(hipStream_t s, const void* gate, const void* up, int64_t ro
     hipLaunchKernelGGL((htile_kernel<T, MI_Q4_K, true>), dim3(grid), dim3(waves * 64), 0, s, sg, cols,        \
                        (const uint8_t*)xq, (const uint8_t*)hx, nullptr, 0,                                  \
                        (act & MI_ACT_GELU) | (hx_out ? kEpiHx : 0), nullptr,                                  \
-                       (uint8_t*)xq_out, cols / 32, 0);                                                       \
+                       (uint8_t*)xq_out, cols / 32, 0, QkvRope{});                                            \
     break;
   switch (tokens) {
     MI_HTG(2) MI_HTG(3) MI_HTG(4) MI_HTG(5) MI_HTG(6) MI_HTG(7) MI_HTG(8)

@@ -167,6 +167,11 @@ bool htile_fits(int kind, int32_t rows, int32_t cols, int32_t tokens);
 // parts (part: htile_split_bytes of scratch), then one reduce launch that adds
 // the parts in order and applies the epilogue.
 bool htile_split_fits(int32_t rows, int32_t cols, int32_t tokens);
+// q|k|v (whole 16-row segments) with the rope and the f16 cache store in the
+// epilogue, as launch_q4k_tile_qkv_rope.
+bool htile_qkv_rope_fits(const RowSegs& sg, int32_t cols, int32_t tokens, int32_t head_dim, int32_t rope_dim);
+int launch_htile_qkv_rope(hipStream_t s, const RowSegs& sg, int32_t cols, const void* xq, const void* hx,
+                          int32_t tokens, float* q, int64_t ldq, const QkvRope& rp);
 size_t htile_split_bytes(int32_t rows, int32_t cols, int32_t tokens);
 int launch_htile_split(hipStream_t s, const void* w, int64_t row_bytes, int32_t rows, int32_t cols, const void* xq,
                        const void* hx, int32_t tokens, float* y, int64_t ldy, int32_t epi, const float* aux,
