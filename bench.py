@@ -262,7 +262,7 @@ def _batched(L, h, kind, ws, copies, rb, stream, reps=100):
         us = e0.elapsed_time(e1) * 1e3 / reps
         algo = _algo_bytes(ROWS, COLS, tokens, ROWS * rb)
         flops = 2.0 * ROWS * COLS * tokens * 2
-        out[f"tokens_{tokens}"] = {"kernel": "q4k_htile_kernel (v_mfma_f32_16x16x32_f16)",
+        out[f"tokens_{tokens}"] = {"kernel": "htile_kernel<T, Q4_K> (v_mfma_f32_16x16x32_f16)",
                                    "us_per_launch": round(us, 3),
                                    "GB_s": round(algo / us / 1e3, 1),
                                    "frac_hbm_peak": round(algo / us / 1e3 / PEAK_GBS, 4),
