@@ -9,10 +9,10 @@ through the prefill layer in one chunk; then three greedy steps.  Checks
 * batch 1: the logits after the prompt and after each greedy step within
   2e-3 of their peak of oracle.forward (model.mojo:178) run token by token
   over the same weights (copied back to the host), with identical picks;
-* batch 4 (four different prompts): each sequence's logits within the same
+* batch 4 and 8 (different prompts): each sequence's logits within the same
   gate of its own batch-1 run, with identical picks;
 * the step replayed from a captured HIP graph equal to the eager step, bit
-  for bit, at batch 1 and 4.
+  for bit, at batch 1, 4 and 8.
 """
 
 import os
@@ -118,20 +118,23 @@ def test_8b_batch1_matches_oracle(model8b):
                                   threads=THREADS)
 
 
-def test_8b_batch4_matches_batch1(model8b):
-    prompts = _prompts(4)
+@pytest.mark.parametrize("batch", [4, 8])
+def test_8b_batch_matches_batch1(model8b, batch):
+    # batch 4: int8 gate|up tile; batch 8: the f16 GLU tile; both run q|k|v
+    # with rope and down (split over K) on the f16 tile
+    prompts = _prompts(batch)
     logits4, picks4 = _run(model8b, prompts)
-    for b in range(4):
+    for b in range(batch):
         logits1, picks1 = _run(model8b, prompts[b:b + 1])
         for i in range(STEPS + 1):
             err, ok = _close(logits4[i][b], logits1[i][0])
-            print(f"seq {b} step {i}: max |dlogit| batch 4 vs 1 {err:.3e} picks {picks4[i][b]} {picks1[i][0]}",
+            print(f"seq {b} step {i}: max |dlogit| batch {batch} vs 1 {err:.3e} picks {picks4[i][b]} {picks1[i][0]}",
                   flush=True)
             assert ok, (b, i)
             assert picks4[i][b] == picks1[i][0], (b, i)
 
 
-@pytest.mark.parametrize("batch", [1, 4])
+@pytest.mark.parametrize("batch", [1, 4, 8])
 def test_8b_graph_replay_matches_eager(model8b, batch):
     prompts = _prompts(batch)
     eager_logits, eager_picks = _run(model8b, prompts)
