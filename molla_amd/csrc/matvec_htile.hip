@@ -133,11 +133,21 @@ __device__ __forceinline__ void sb_product(const uint8_t* lrows, int sb, const h
   uint32_t sc_lo, sc_hi, m_lo, m_hi;
   kscales(h.y, h.z, h.w, sc_lo, sc_hi, m_lo, m_hi);
   const hh2 k1024 = {(_Float16)-1024.0f, (_Float16)-1024.0f};
+  // the 8 scales as pairs (sc 2i, sc 2i + 1) and their negated 1024 multiples;
+  // a group takes one half of its pair to both halves
+  hh2 scp[4], nscp[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    scp[i] = as_hh2(magic2(i < 2 ? sc_lo : sc_hi, (i & 1) ? kSel23 : kSel01)) + k1024;
+    nscp[i] = scp[i] * k1024;
+  }
   ff4 c = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
   for (int j = 0; j < 8; j++) {
-    const hh2 sc = as_hh2(magic2(j < 4 ? sc_lo : sc_hi, sel_splat(j & 3))) + k1024;
-    const hh2 nsc = sc * k1024;
+    const hh2 sc = (j & 1) ? __builtin_shufflevector(scp[j >> 1], scp[j >> 1], 1, 1)
+                           : __builtin_shufflevector(scp[j >> 1], scp[j >> 1], 0, 0);
+    const hh2 nsc = (j & 1) ? __builtin_shufflevector(nscp[j >> 1], nscp[j >> 1], 1, 1)
+                            : __builtin_shufflevector(nscp[j >> 1], nscp[j >> 1], 0, 0);
     const uint32_t t0 = q[j >> 1].x, t1 = q[j >> 1].y;
     const uint32_t u0 = (j & 1) ? (t0 >> 4) & 0x0F0F0F0Fu : t0 & 0x0F0F0F0Fu;
     const uint32_t u1 = (j & 1) ? (t1 >> 4) & 0x0F0F0F0Fu : t1 & 0x0F0F0F0Fu;
@@ -266,7 +276,8 @@ __global__ __launch_bounds__(kMaxHWaves * 64) void htile_kernel(const RowSegs sg
 
   // This lane's share of a tile: 8-byte words threadIdx.x + blockDim.x * j,
   // and where each lands in the padded LDS rows.
-  int ldso[kLoads], wrow[kLoads], woff[kLoads];
+  int ldso[kLoads];
+  uint32_t woff[kLoads], wfull[kLoads];
 #pragma unroll
   for (int j = 0; j < kLoads; j++) {
     // o / rb through a float reciprocal (o < 2^16: exact after one
@@ -278,16 +289,17 @@ __global__ __launch_bounds__(kMaxHWaves * 64) void htile_kernel(const RowSegs sg
     row -= row * rb > o;
     row += (row + 1) * rb <= o;
     ldso[j] = row * kLdsRow + (o - row * rb);
-    wrow[j] = row;
     woff[j] = o - row * rb;
+    wfull[j] = (uint32_t)row * (uint32_t)rstride + woff[j];  // 16 rows of a row stride < 2^27
   }
   // A last tile of fewer than 16 rows reads its last word again in place of
   // the missing rows (whose sums are never stored): loads stay unconditional.
   auto load_tile = [&](uint2 (&r)[kLoads], int tl) __attribute__((always_inline)) {
     const uint8_t* src = rows::seg_row(sg, tl * 16) + (int64_t)blockIdx.y * rb;
-    const int last = min(16, rows - tl * 16) - 1;
+    // a word of a missing row (past `last`) reads the same word of row last
+    const uint32_t lastoff = (uint32_t)(min(16, rows - tl * 16) - 1) * (uint32_t)rstride;
 #pragma unroll
-    for (int j = 0; j < kLoads; j++) r[j] = *(const uint2*)(src + min(wrow[j], last) * rstride + woff[j]);
+    for (int j = 0; j < kLoads; j++) r[j] = *(const uint2*)(src + min(wfull[j], lastoff + woff[j]));
   };
   auto store_tile = [&](const uint2 (&r)[kLoads], int buf) __attribute__((always_inline)) {
 #pragma unroll
