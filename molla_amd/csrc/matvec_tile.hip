@@ -114,14 +114,27 @@ __global__ __launch_bounds__(KW * 64) void q4k_tile_kernel(const RowSegs sg, int
     for (int win = 0; win < NW; win++)
       av[slot][win] = a_live ? ld16(xq + (uint32_t)(a_off + (sb * 8 + win * GW) * 16)) : make_uint4(0, 0, 0, 0);
   };
+  // every token's (scale, xsum) per group, once per block: loaded first,
+  // since a wave's loads complete in order and the barrier below would
+  // otherwise also wait for the weights issued ahead of them
+  float2 mreg[2];
+  int mi[2];
+#pragma unroll
+  for (int k = 0; k < 2; k++) {
+    mi[k] = (int)threadIdx.x + k * (int)blockDim.x;
+    const int i = min(mi[k], tn * G - 1), t = i / G, g = i - t * G;
+    mreg[k] = *(const float2*)(xq + (uint32_t)(t * tok + 6 * plane + g * 16));
+  }
   load_w(0, 0);
   load_a(0, 0);
   if (SBW * NP > 1) {  // the second step (next superblock, or the up row)
     load_w(1, 1);
     load_a(1, 1);
   }
-  // every token's (scale, xsum) per group, once per block
-  for (int i = threadIdx.x; i < tn * G; i += blockDim.x) {
+#pragma unroll
+  for (int k = 0; k < 2; k++)
+    if (mi[k] < tn * G) meta_lds[mi[k]] = mreg[k];
+  for (int i = (int)threadIdx.x + 2 * (int)blockDim.x; i < tn * G; i += blockDim.x) {
     const int t = i / G, g = i - t * G;
     meta_lds[i] = *(const float2*)(xq + (uint32_t)(t * tok + 6 * plane + g * 16));
   }
