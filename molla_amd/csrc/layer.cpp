@@ -433,7 +433,10 @@ static int decoder_layer(mi_stream stream, const mi_layer_desc* d, float* resid,
     sg.nseg = 3;
   }
   const bool q8 = d->cache_form == MI_CACHE_Q8;
-  if (fused_qkv && !d->neox && !q8 && q4k_qkv_rope_fits(d->width, d->head_dim, d->rope_dim)) {
+  // a q8_0 cache takes the folded-norm kernel's q8 form (32-value blocks)
+  const bool q8_fold = q8 && qw % 32 == 0 && kvw % 32 == 0 &&
+                       q4k_qkv_norm_fits(d->width, d->head_dim, d->rope_dim, resid, d->attn_norm);
+  if (fused_qkv && !d->neox && (!q8 || q8_fold) && q4k_qkv_rope_fits(d->width, d->head_dim, d->rope_dim)) {
     // norm (plus this position's rope table), then q|k|v with the rope and
     // the cache store in its epilogue: no separate rope launch
     float* trig = (float*)(base + c.trig);
@@ -451,7 +454,7 @@ static int decoder_layer(mi_stream stream, const mi_layer_desc* d, float* resid,
     rp.factors = d->rope_factors;
     if (q4k_qkv_norm_fits(d->width, d->head_dim, d->rope_dim, resid, d->attn_norm)) {
       // the norm and the rope angles inside the q|k|v launch
-      if ((rc = launch_q4k_qkv_norm(s, sg, d->width, resid, d->attn_norm, d->eps, qkv, rp))) return rc;
+      if ((rc = launch_q4k_qkv_norm(s, sg, d->width, resid, d->attn_norm, d->eps, qkv, rp, q8))) return rc;
     } else {
       if ((rc = launch_rms_norm_trig(s, resid, d->attn_norm, d->width, d->eps, xq, pos, d->rope_steps,
                                      d->rope_factors, d->rope_dim / 2, trig)))

@@ -113,11 +113,16 @@ __global__ __launch_bounds__(8 * 64) void glu_norm_kernel(const RowSegs sg, int 
 // rows measured best).  A wave's (cos, sin) comes
 // from scalar loads of pos, steps and factors and float64 trig, as
 // rms_norm_kernel computes its table, so it never waits for weights.
-template <int PRE>
-__global__ __launch_bounds__(12 * 64) void qkv_norm_kernel(const RowSegs sg, int cols, float* __restrict__ y,
-                                                           const NormIn nm, const QkvRope rp) {
+// Q8 (a q8_0 cache): 16 waves and 32-row groups, so that a group of k or v
+// rows is one q8_0 block of the cache row (qw and kvw multiples of 32); the
+// block gathers the group's 32 outputs in LDS and one half-wave stores it as
+// rope_store_kernel's q8 branch does (store_kv_q8: repack.mojo:174-218).
+template <int PRE, bool Q8 = false>
+__global__ __launch_bounds__((Q8 ? 16 : 12) * 64) void qkv_norm_kernel(const RowSegs sg, int cols,
+                                                                       float* __restrict__ y, const NormIn nm,
+                                                                       const QkvRope rp) {
 #pragma clang fp contract(off)
-  constexpr int W = 12, RPW = 2, kNT = W * 64;
+  constexpr int W = Q8 ? 16 : 12, RPW = 2, kNT = W * 64;
   __shared__ __align__(16) uint8_t xs[4 * 4096];
   __shared__ double red[kNT / 64];
   const int lane = threadIdx.x & 63;
@@ -164,8 +169,13 @@ __global__ __launch_bounds__(12 * 64) void qkv_norm_kernel(const RowSegs sg, int
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int r = PRE; r < RPW; r++) un[r].load(rows::seg_row(sg, min(pr.row0 + r, rows - 1)), 0, 0, 0, u);
-  const int64_t slot = (int64_t)(rp.kv_index ? rp.kv_index[pos] : pos) * rp.kvw;
-  for (;;) {
+  const int64_t slot = (int64_t)(rp.kv_index ? rp.kv_index[pos] : pos) * (Q8 ? cache_row(MI_CACHE_Q8, rp.kvw) : rp.kvw);
+  __shared__ float q8buf[Q8 ? 2 : 1][32];
+  // q8buf alternates: a block's groups go q rows first, then k and v rows
+  // (each with a barrier), so a buffer is written again only after every
+  // wave has passed the next group's barrier, which wave 0 reaches once it
+  // has read the buffer
+  for (int it = 0;; it++) {
     // rope_theta's arithmetic on the preloaded step and factor
     float c = 1.0f, sn = 0.0f;
     if (pr.rot) {
@@ -188,7 +198,32 @@ __global__ __launch_bounds__(12 * 64) void qkv_norm_kernel(const RowSegs sg, int
     const float a = acc[0], b = acc[1];
     const float o = !pr.rot ? (lane == 0 ? a : b) : (lane == 0 ? a * c - b * sn : a * sn + b * c);
     const int row = pr.row0 + lane;
-    if (lane < RPW && row < rows) {
+    if constexpr (Q8) {
+      // the group is all q, all k or all v rows (block-uniform)
+      const int grow0 = g * W * RPW;
+      if (grow0 < rp.qw) {
+        if (lane < RPW && row < rows) y[row] = o;
+      } else {
+        float* qb = q8buf[it & 1];
+        if (lane < RPW) qb[wave * RPW + lane] = o;
+        __syncthreads();
+        if (wave == 0) {
+          // q8_0 of the 32 values (both half-waves compute the same block)
+          const int l32 = lane & 31;
+          const float x = qb[l32];
+          const float amax = lanes::reduce<32>(fabsf(x), lanes::Max{});
+          const float inv = amax == 0.0f ? 0.0f : 127.0f / amax;
+          const float yv = x * inv;
+          const float r = yv >= 0.0f ? yv + 0.5f : yv - 0.5f;
+          const int qi = max(-127, min(127, (int)r));
+          const bool is_k = grow0 < rp.qw + rp.kvw;
+          __half* rowp = (is_k ? rp.k_cache : rp.v_cache) + slot;
+          const int b = (grow0 - rp.qw - (is_k ? 0 : rp.kvw)) >> 5;
+          if (lane < 32) ((int8_t*)rowp)[b * 32 + l32] = (int8_t)qi;
+          if (lane == 0) rowp[(rp.kvw >> 1) + b] = __float2half_rn(amax / 127.0f);
+        }
+      }
+    } else if (lane < RPW && row < rows) {
       if (pr.is_q) y[row] = o;
       else if (pr.is_k) rp.k_cache[slot + (row - rp.qw)] = __float2half_rn(o);
       else rp.v_cache[slot + (row - rp.qw - rp.kvw)] = __float2half_rn(o);
@@ -291,10 +326,17 @@ bool q4k_qkv_norm_fits(int32_t cols, int32_t head_dim, int32_t rope_dim, const v
 }
 
 int launch_q4k_qkv_norm(hipStream_t s, const RowSegs& sg, int32_t cols, const float* x, const float* gain,
-                        float eps, float* q, const QkvRope& rp) {
+                        float eps, float* q, const QkvRope& rp, bool q8) {
   if (!q4k_qkv_norm_fits(cols, rp.head_dim, rp.rope_dim, x, gain) || !rp.steps)
     return fail(MI_ERR_SHAPE, "matvec: no normed q|k|v for %d columns, head_dim %d", cols, rp.head_dim);
   const int rows = sg.end[sg.nseg - 1];
+  if (q8) {
+    if (rp.qw % 32 || rp.kvw % 32)
+      return fail(MI_ERR_SHAPE, "matvec: q8_0 q|k|v needs q and kv widths of whole 32-value blocks");
+    hipLaunchKernelGGL((qkv_norm_kernel<1, true>), dim3(std::min((rows + 31) / 32, cu_count())), dim3(16 * 64), 0,
+                       s, sg, cols, q, NormIn{x, gain, eps}, rp);
+    return hip_check(hipGetLastError(), "matvec launch");
+  }
   const int groups = (rows + 23) / 24;
   hipLaunchKernelGGL(qkv_norm_kernel<1>, dim3(std::min(groups, cu_count())), dim3(12 * 64), 0, s, sg, cols, q,
                      NormIn{x, gain, eps}, rp);

@@ -80,8 +80,10 @@ int launch_q4k_glu(hipStream_t s, const void* gate, const void* up, int64_t row_
 // q|k|v with the rope epilogue, taking the RMSNorm of x (gain, eps) itself
 // and computing its (cos, sin) from rp.steps / rp.factors: no norm launch.
 bool q4k_qkv_norm_fits(int32_t cols, int32_t head_dim, int32_t rope_dim, const void* x, const void* gain);
+// q8: the caches are q8_0 rows (rp.qw and rp.kvw multiples of 32); k and v
+// go to them as whole 32-value blocks.
 int launch_q4k_qkv_norm(hipStream_t s, const RowSegs& sg, int32_t cols, const float* x, const float* gain,
-                        float eps, float* q, const QkvRope& rp);
+                        float eps, float* q, const QkvRope& rp, bool q8 = false);
 // The same with the grouped xq_out, taking the RMSNorm of x (gain, eps)
 // itself instead of an xq input: the layer's ffn norm needs no launch.
 bool q4k_glu_norm_fits(int32_t rows, int32_t cols, const void* x, const void* gain);
