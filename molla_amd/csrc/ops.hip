@@ -958,6 +958,146 @@ __global__ __launch_bounds__(NT) void attend_wide_kernel(
     *(float2*)(part_acc + (slot0 + (int64_t)g * max_chunks + c) * D + 2 * e) = make_float2(a0, a1);
 }
 
+// attend_wide_q8_kernel: attend_wide_kernel over a q8_0 cache (the row's
+// quants of every key head, then its factors: cache_row), the arithmetic of
+// attend_split_q8_kernel (each key or value element float(quant) *
+// float(factor) before it is used) spread the same way as the f16 form:
+// a score is SPL threads of DPT dims (whole 32-value blocks, so one factor a
+// block), a weighted value pair is KQ threads over interleaved keys, and the
+// slice softmax is one wave per query head.
+template <int GROUP, int D, int NT>
+__global__ __launch_bounds__(NT) void attend_wide_q8_kernel(
+    const float* __restrict__ q, int64_t q_stride, const __half* __restrict__ kc, const __half* __restrict__ vc,
+    int64_t cache_stride, int row, int heads, int kv_heads, float scale, const int32_t* __restrict__ pos_dev,
+    int count_host, int max_chunks, float* __restrict__ part_acc, float* __restrict__ part_ml,
+    const int32_t* __restrict__ kv_index, int64_t index_stride) {
+#pragma clang fp contract(off)
+  using S = WideShape<GROUP, D, NT>;
+  constexpr int KK = kWideKeys, NB = D / 32, PIECES = D / 16, TOTAL = KK * PIECES, PAIRS = D / 2;
+  constexpr int PER = (TOTAL + NT - 1) / NT;  // 16-byte pieces of K (and of V) per thread
+  constexpr int KQR = D + 16;                 // LDS key rows in bytes (16 bytes of pad)
+  static_assert(GROUP * D / 4 <= NT && S::KQ >= 1 && S::KQ <= 64, "shape");
+  if constexpr (S::DPT % 16 != 0) {
+    return;  // never launched (wide_q8_fits): a score part is whole 16-byte pieces
+  } else {
+  __shared__ __align__(16) int8_t Kq[KK * KQR];
+  __shared__ __align__(16) int8_t Vq[KK * D];
+  __shared__ float Ksc[KK * NB], Vsc[KK * NB];
+  __shared__ __align__(16) float Qs[GROUP * D];
+  __shared__ float Ss[GROUP * KK];
+  const int c = blockIdx.x, kvh = blockIdx.y, t = blockIdx.z;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int count = pos_dev ? pos_dev[t] + 1 : count_host;
+  const int start = c * KK;
+  if (start >= count) return;
+  const int nk = min(KK, count - start);
+  const int kvw = kv_heads * D;
+
+  const float* qg = q + (int64_t)t * q_stride + (int64_t)kvh * GROUP * D;
+  const bool has_q = tid < GROUP * D / 4;
+  const float4 qv = ((const float4*)qg)[has_q ? tid : 0];
+  const int64_t seq = kv_index ? 0 : (int64_t)t * cache_stride;
+  const int8_t* kseq = (const int8_t*)(kc + seq);
+  const int8_t* vseq = (const int8_t*)(vc + seq);
+  uint4 kraw[PER], vraw[PER];
+#pragma unroll
+  for (int j = 0; j < PER; j++) {
+    const int i = min(tid + j * NT, TOTAL - 1);
+    const int key = i / PIECES, pc = i % PIECES;
+    const int cell = max(kv_cell(kv_index, index_stride, t, start + min(key, nk - 1)), 0);
+    const int64_t off = (int64_t)cell * row * 2 + (int64_t)kvh * D + pc * 16;  // bytes
+    kraw[j] = *(const uint4*)(kseq + off);
+    vraw[j] = *(const uint4*)(vseq + off);
+  }
+  // the factors: KK * NB of each, at most one of each a thread
+  const bool has_f = tid < KK * NB;
+  float kf = 0.0f, vf = 0.0f;
+  {
+    const int i = has_f ? tid : 0, key = i / NB, b = i % NB;
+    const int cell = max(kv_cell(kv_index, index_stride, t, start + min(key, nk - 1)), 0);
+    const int64_t at = (int64_t)cell * row + (kvw >> 1) + (kvh * D >> 5) + b;  // halves
+    kf = __half2float(kc[seq + at]);
+    vf = __half2float(vc[seq + at]);
+  }
+  if (has_q) ((float4*)Qs)[tid] = qv;
+  if (has_f) {
+    Ksc[tid] = kf;
+    Vsc[tid] = vf;
+  }
+#pragma unroll
+  for (int j = 0; j < PER; j++) {
+    const int i = tid + j * NT;
+    const int key = i / PIECES, pc = i % PIECES;
+    if (i < TOTAL) {
+      *(uint4*)(Kq + key * KQR + pc * 16) = kraw[j];
+      *(uint4*)(Vq + key * D + pc * 16) = vraw[j];
+    }
+  }
+  __syncthreads();
+
+  // scores: thread = (query head g, key, part of DPT dims)
+  {
+    const int dot = tid / S::SPL, part = tid % S::SPL;
+    const int g = dot / KK, key = dot % KK;
+    float sdot = 0.0f;
+    if (dot < GROUP * KK) {
+      const int8_t* kr = Kq + key * KQR + part * S::DPT;
+      const float* qq = Qs + g * D + part * S::DPT;
+#pragma unroll
+      for (int d = 0; d < S::DPT; d += 16) {
+        const float f = Ksc[key * NB + (part * S::DPT + d) / 32];
+        const uint4 raw = *(const uint4*)(kr + d);
+        const int8_t* b = (const int8_t*)&raw;
+#pragma unroll
+        for (int i = 0; i < 16; i++) sdot = fmaf(qq[d + i], (float)b[i] * f, sdot);
+      }
+    }
+    sdot = lanes::reduce<S::SPL>(sdot, lanes::Add{});
+    if (part == 0 && dot < GROUP * KK) {
+      const bool live = key < nk && (!kv_index || kv_cell(kv_index, index_stride, t, start + key) >= 0);
+      Ss[g * KK + key] = live ? sdot * scale : -INFINITY;
+    }
+  }
+  __syncthreads();
+  const int64_t slot0 = ((int64_t)t * heads + (int64_t)kvh * GROUP) * max_chunks;
+  if (wave < GROUP) {
+    const float sc = Ss[wave * KK + lane];
+    const float m = lanes::reduce<64>(sc, lanes::Max{});
+    const float pr = sc == -INFINITY ? 0.0f : expf(sc - m);
+    const float l = lanes::reduce<64>(pr, lanes::Add{});
+    Ss[wave * KK + lane] = pr;
+    if (lane == 0) *(float2*)(part_ml + (slot0 + (int64_t)wave * max_chunks + c) * 2) = make_float2(m, l);
+  }
+  __syncthreads();
+  // unnormalised weighted values: thread = (query head, dim pair, key residue kq)
+  const int kq = tid % S::KQ, oe = tid / S::KQ;
+  const int g = oe / PAIRS, e = oe % PAIRS;
+  float a0 = 0.0f, a1 = 0.0f;
+  if (oe < GROUP * PAIRS) {
+    const float* pg = Ss + g * KK;
+    const int b = (2 * e) >> 5;
+#pragma unroll 4
+    for (int k = kq; k < KK; k += S::KQ) {
+      const float p = pg[k];
+      const char2 v = *(const char2*)(Vq + k * D + 2 * e);
+      const float f = Vsc[k * NB + b];
+      a0 = fmaf(p, (float)v.x * f, a0);
+      a1 = fmaf(p, (float)v.y * f, a1);
+    }
+  }
+  a0 = lanes::reduce<S::KQ>(a0, lanes::Add{});
+  a1 = lanes::reduce<S::KQ>(a1, lanes::Add{});
+  if (kq == 0 && oe < GROUP * PAIRS)
+    *(float2*)(part_acc + (slot0 + (int64_t)g * max_chunks + c) * D + 2 * e) = make_float2(a0, a1);
+  }
+}
+
+// whether attend_wide_q8_kernel takes a shape: each score thread's dims are
+// whole 16-byte pieces
+__host__ __device__ constexpr bool wide_q8_fits(int group, int d, int nt) {
+  return d % (16 * (nt / (group * kWideKeys) < d / 8 ? nt / (group * kWideKeys) : d / 8)) == 0;
+}
+
 // ---- the optional layer parts of other families ----------------------------
 // kernel.mojo:400 rms_norm_at over runs: every head of q (or k) in a row of
 // the fused q|k|v, in place (gpu_block.mojo device_rms_norm_run, Qwen 3's
@@ -1179,10 +1319,20 @@ int launch_attend(hipStream_t s, const float* q, int64_t q_stride, const uint16_
       ((size_t)chunks * 2 + (chunks + kMergeBatch - 1) / kMergeBatch * kMergeBatch) * sizeof(float);
   // decode (at most 8 tokens, one each per sequence, f16 cache): the
   // 1024-thread slice kernel
-  if (tokens <= kMaxTokens && form != MI_CACHE_Q8 && (head_dim == 64 || head_dim == 128)) {
+  if (tokens <= kMaxTokens && (head_dim == 64 || head_dim == 128) &&
+      (form != MI_CACHE_Q8 || wide_q8_fits(group, head_dim, tokens == 1 ? 1024 : 512))) {
     dim3 grid(chunks, kv_heads, tokens);
+    const int qrow = cache_row(MI_CACHE_Q8, kv_heads * head_dim);
 #define MI_WIDE(G, DD)                                                                                       \
-  if (tokens == 1)                                                                                           \
+  if (form == MI_CACHE_Q8 && tokens == 1)                                                                    \
+    hipLaunchKernelGGL((attend_wide_q8_kernel<G, DD, 1024>), grid, dim3(1024), 0, s, q, q_stride,            \
+                       (const __half*)k_cache, (const __half*)v_cache, cache_stride, qrow, heads, kv_heads,   \
+                       scale, pos_dev, count_host, chunks, part_acc, part_ml, kv_index, index_stride);        \
+  else if (form == MI_CACHE_Q8)                                                                              \
+    hipLaunchKernelGGL((attend_wide_q8_kernel<G, DD, 512>), grid, dim3(512), 0, s, q, q_stride,              \
+                       (const __half*)k_cache, (const __half*)v_cache, cache_stride, qrow, heads, kv_heads,   \
+                       scale, pos_dev, count_host, chunks, part_acc, part_ml, kv_index, index_stride);        \
+  else if (tokens == 1)                                                                                      \
     hipLaunchKernelGGL((attend_wide_kernel<G, DD, 1024>), grid, dim3(1024), 0, s, q, q_stride,               \
                        (const __half*)k_cache, (const __half*)v_cache, cache_stride, heads, kv_heads, scale,   \
                        pos_dev, count_host, chunks, part_acc, part_ml, kv_index, index_stride);               \
