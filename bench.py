@@ -57,7 +57,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-decode", action="store_true", help="skip the synthetic 8B decode step")
     ap.add_argument("--decode-tokens", type=int, default=256)
-    ap.add_argument("--decode-batch", type=int, nargs="+", default=[1, 4])
+    ap.add_argument("--decode-batch", type=int, nargs="+", default=[1, 4, 8])
     ap.add_argument("--decode-q8", type=int, nargs="*", default=[1],
                     help="decode batch sizes also run over a q8_0 KV cache")
     ap.add_argument("--prompt", type=int, default=2048)
