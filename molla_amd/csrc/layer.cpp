@@ -546,12 +546,12 @@ static int decoder_layer(mi_stream stream, const mi_layer_desc* d, float* resid,
     return launch_matvec(s, d->down.kind, d->down.data, d->down.row_bytes, d->width, d->hidden, xq2, tokens,
                          resid, d->width, MI_EPI_ADD, nullptr);
   }
-  if (tokens > 4 && d->gate.kind == MI_Q4_K && d->up.kind == MI_Q4_K && d->gate.row_bytes == d->up.row_bytes &&
+  if (tokens >= 4 && d->gate.kind == MI_Q4_K && d->up.kind == MI_Q4_K && d->gate.row_bytes == d->up.row_bytes &&
       htile_glu_fits(d->hidden, d->width, tokens)) {
-    // a batch of 5..8: the norm (with the hx form), then gate and up on the
+    // a batch of 4..8: the norm (with the hx form), then gate and up on the
     // f16 matrix-core tile, which writes act(gate) * up straight into down's
-    // xq (at 8 tokens 3.86 against 4.50 ms a decode step with the int8 GLU
-    // tile below; at 4 tokens the int8 tile is 1% ahead)
+    // xq and hx forms (at 4 tokens 3.084 against 3.115 ms a decode step with
+    // the int8 GLU tile below, at 8 tokens 3.86 against 4.50 ms)
     void* hx2 = (uint8_t*)xq + (size_t)xq_token_bytes(d->width) * tokens;
     void* xq2 = base + c.xq2;
     if ((rc = launch_rms_norm(s, resid, d->ffn_norm, d->width, tokens, d->eps, nullptr, xq, hx2))) return rc;
