@@ -100,10 +100,12 @@ def llama31_factors(pairs):
     # tile split over two 4096-column parts (the GLU tile writes its hx form)
     ((1024, 8192, 8, 2, 128), 200, 4, False),
     ((1024, 8192, 8, 2, 128), 200, 8, False),
-    # an MLP of 14336: four 3584-column parts, from the int8 GLU tile (4
-    # tokens) and the f16 GLU tile (6 tokens)
+    # an MLP of 14336: four 3584-column parts, from the f16 GLU tile
     ((1024, 14336, 8, 2, 128), 200, 4, False),
     ((1024, 14336, 8, 2, 128), 200, 6, False),
+    # a width of 768 (not a multiple of 512): gate|up on the int8 GLU tile,
+    # which then also writes the hx form for down's f16 split
+    ((768, 8192, 12, 3, 64), 150, 4, False),
     # full multi-head attention: a q|k|v of 12288 rows is more 24-row groups
     # than CUs, so the folded-norm q|k|v kernel loops (rope step and factor
     # reloaded per group)
