@@ -234,7 +234,9 @@ __device__ __forceinline__ void sb_product_q6k(const uint8_t* lrows, int sb, con
 // ROPE (Q4_K, q|k|v rows): the epilogue of the batched int8 tile's rope form
 // (matvec_tile.hip): rows of q and k rotated in adjacent pairs at each
 // token's position, q to y, k and v to the f16 caches (rp).
-template <int TN, int KIND, bool GLU, bool ROPE = false>
+// SPLIT: the split-K form (block row blockIdx.y reads a column part of
+// longer rows); the tile's rows are then not one run of memory.
+template <int TN, int KIND, bool GLU, bool ROPE = false, bool SPLIT = false>
 __global__ __launch_bounds__(kMaxHWaves * 64) void htile_kernel(const RowSegs sg, int cols,
                                                                      const uint8_t* __restrict__ xq,
                                                                      const uint8_t* __restrict__ hx,
@@ -277,7 +279,11 @@ __global__ __launch_bounds__(kMaxHWaves * 64) void htile_kernel(const RowSegs sg
   // This lane's share of a tile: 8-byte words threadIdx.x + blockDim.x * j,
   // and where each lands in the padded LDS rows.
   int ldso[kLoads];
-  uint32_t woff[kLoads], wfull[kLoads];
+  // Q4_K (and the split form): each word's byte offset from row 0 of the
+  // tile, clamped per tile with one min; Q6_K keeps the word index (the
+  // offsets cost its 8-token form 34 spilled VGPRs, 133 -> 210 us on the head)
+  constexpr bool kOff = SPLIT || KIND == MI_Q4_K;
+  uint32_t wfull[kOff ? kLoads : 1];
 #pragma unroll
   for (int j = 0; j < kLoads; j++) {
     // o / rb through a float reciprocal (o < 2^16: exact after one
@@ -289,17 +295,24 @@ __global__ __launch_bounds__(kMaxHWaves * 64) void htile_kernel(const RowSegs sg
     row -= row * rb > o;
     row += (row + 1) * rb <= o;
     ldso[j] = row * kLdsRow + (o - row * rb);
-    woff[j] = o - row * rb;
-    wfull[j] = (uint32_t)row * (uint32_t)rstride + woff[j];  // 16 rows of a row stride < 2^27
+    if constexpr (kOff) wfull[j] = (uint32_t)row * (uint32_t)rstride + (uint32_t)(o - row * rb);
   }
+  (void)rstride;
   // A last tile of fewer than 16 rows reads its last word again in place of
   // the missing rows (whose sums are never stored): loads stay unconditional.
   auto load_tile = [&](uint2 (&r)[kLoads], int tl) __attribute__((always_inline)) {
-    const uint8_t* src = rows::seg_row(sg, tl * 16) + (int64_t)blockIdx.y * rb;
-    // a word of a missing row (past `last`) reads the same word of row last
-    const uint32_t lastoff = (uint32_t)(min(16, rows - tl * 16) - 1) * (uint32_t)rstride;
+    if constexpr (kOff) {
+      const uint8_t* src = rows::seg_row(sg, tl * 16) + (int64_t)blockIdx.y * rb;
+      // a word of a missing row reads the last word of the last row
+      const uint32_t lastw = (uint32_t)(min(16, rows - tl * 16) - 1) * (uint32_t)rstride + (uint32_t)(rb - 8);
 #pragma unroll
-    for (int j = 0; j < kLoads; j++) r[j] = *(const uint2*)(src + min(wfull[j], lastoff + woff[j]));
+      for (int j = 0; j < kLoads; j++) r[j] = *(const uint2*)(src + min(wfull[j], lastw));
+    } else {
+      const uint2* src = (const uint2*)rows::seg_row(sg, tl * 16);
+      const int words = min(16, rows - tl * 16) * (rb >> 3);
+#pragma unroll
+      for (int j = 0; j < kLoads; j++) r[j] = src[min((int)threadIdx.x + (int)blockDim.x * j, words - 1)];
+    }
   };
   auto store_tile = [&](const uint2 (&r)[kLoads], int buf) __attribute__((always_inline)) {
 #pragma unroll
@@ -617,7 +630,8 @@ int launch_htile_split(hipStream_t s, const void* w, int64_t row_bytes, int32_t 
   const int64_t ysplit = (int64_t)tokens * rows;
 #define MI_HS(T)                                                                                              \
   case T:                                                                                                     \
-    hipLaunchKernelGGL((htile_kernel<T, MI_Q4_K, false>), dim3(grid, n), dim3(waves * 64), 0, s, sg, pc,      \
+    hipLaunchKernelGGL((htile_kernel<T, MI_Q4_K, false, false, true>), dim3(grid, n), dim3(waves * 64), 0, s, \
+                       sg, pc,                                                                                \
                        (const uint8_t*)xq, (const uint8_t*)hx, part, (int64_t)rows, MI_EPI_NONE, nullptr,     \
                        nullptr, cols / 32, ysplit, QkvRope{});                                                \
     break;
