@@ -1190,22 +1190,28 @@ __global__ __launch_bounds__(1024) void argmax4_kernel(const float* __restrict__
   const int t = blockIdx.x;
   const float4* xr = (const float4*)(x + (int64_t)t * n);
   const int n4 = n >> 2;
-  float4 v[PER];
-#pragma unroll
-  for (int k = 0; k < PER; k++) {
-    const int j = threadIdx.x + k * 1024;
-    v[k] = j < n4 ? xr[j] : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
-  }
+  // rounds of at most 16 loads a thread: 32 float4 are the 128 registers a
+  // 1024-thread block has, and spilled
+  constexpr int R = PER < 16 ? PER : 16;
   float bv = -INFINITY;
   int bi = n;
 #pragma unroll
-  for (int k = 0; k < PER; k++) {
-    const int i = 4 * (threadIdx.x + k * 1024);
-    if (i < n) {
-      better(bv, bi, v[k].x, i);
-      better(bv, bi, v[k].y, i + 1);
-      better(bv, bi, v[k].z, i + 2);
-      better(bv, bi, v[k].w, i + 3);
+  for (int k0 = 0; k0 < PER; k0 += R) {
+    float4 v[R];
+#pragma unroll
+    for (int k = 0; k < R; k++) {
+      const int j = threadIdx.x + (k0 + k) * 1024;
+      v[k] = j < n4 ? xr[j] : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+    }
+#pragma unroll
+    for (int k = 0; k < R; k++) {
+      const int i = 4 * (threadIdx.x + (k0 + k) * 1024);
+      if (i < n) {
+        better(bv, bi, v[k].x, i);
+        better(bv, bi, v[k].y, i + 1);
+        better(bv, bi, v[k].z, i + 2);
+        better(bv, bi, v[k].w, i + 3);
+      }
     }
   }
   argmax_finish(bv, bi, n, out + t);
