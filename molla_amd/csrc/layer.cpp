@@ -505,8 +505,15 @@ static int decoder_layer(mi_stream stream, const mi_layer_desc* d, float* resid,
           rc = launch_q4k_tile_qkv_rope(s, tg, d->width, xq, tokens, qkv, qkv_stride, rp);
         if (rc) return rc;
         roped = true;
-      } else if ((rc = launch_q4k_tile_segs(s, tg, d->width, xq, tokens, qkv, qkv_stride))) {
-        return rc;
+      } else {
+        // a q8_0 cache or neox pairing: unrotated q|k|v for rope_store, on
+        // the f16 tile where its segments fit
+        if (htile_qkv_rope_fits(tg, d->width, tokens, d->head_dim, d->rope_dim))
+          rc = launch_htile(s, MI_Q4_K, tg, qw + 2 * (int32_t)kvw, d->width, xq, hxn, tokens, qkv, qkv_stride,
+                            MI_EPI_NONE, nullptr);
+        else
+          rc = launch_q4k_tile_segs(s, tg, d->width, xq, tokens, qkv, qkv_stride);
+        if (rc) return rc;
       }
     } else {
       if ((rc = launch_matvec(s, d->wq.kind, d->wq.data, d->wq.row_bytes, qw, d->width, xq, tokens, qkv,
