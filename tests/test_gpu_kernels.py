@@ -348,12 +348,19 @@ def q8_decode(halves, kvw, count):
 
 
 @pytest.mark.parametrize("count", [1, 40, 129, 2049])
-def test_attention_q8_cache(ctx, count):
+@pytest.mark.parametrize("heads,kv,hd", [
+    (8, 2, 32),    # the 256-thread slice kernel
+    (8, 2, 64),    # attend_wide_q8_kernel, groups of 4
+    (8, 2, 128),
+    (16, 2, 128),  # groups of 8
+    (4, 2, 128),   # groups of 2
+    (2, 2, 64),    # groups of 1: score parts below a 16-byte piece, the slice kernel
+])
+def test_attention_q8_cache(ctx, count, heads, kv, hd):
     """tests/test_gpu_ops.mojo test_attend_q8: rows stored by the q8 store
     kernel read back exactly as the host quantizer says, and attention over
     them matches the oracle attending to those values."""
     from molla_amd import gpu
-    heads, kv, hd = 8, 2, 32
     kvw = kv * hd
     i = np.arange(count * kvw)
     raw_k = ((i * 31 % 173) / 173 - 0.5).astype(np.float32)
