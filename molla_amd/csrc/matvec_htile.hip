@@ -439,17 +439,26 @@ __global__ __launch_bounds__(kMaxHWaves * 64) void htile_kernel(const RowSegs sg
     const int tl = tile_of(kk);
     for (int ix = lane * nw + wave; ix < 16 * TN; ix += 64 * nw) {
       const int rr = ix & 15, u = ix >> 4;
+      // every wave's pair is read unconditionally (a wave past nw reads
+      // the last one again and adds nothing), so the reads go out together
+      // instead of one LDS round trip per wave behind a branch
       float v = 0.0f;
 #pragma unroll
-      for (int w = 0; w < kMaxHWaves; w++)
-        if (w < nw) v += part[buf][w][rr][2 * u] + part[buf][w][rr][2 * u + 1];
+      for (int w = 0; w < kMaxHWaves; w++) {
+        const int ww = min(w, nw - 1);
+        const float h = part[buf][ww][rr][2 * u] + part[buf][ww][rr][2 * u + 1];
+        v += w < nw ? h : 0.0f;
+      }
       if constexpr (ROPE) {
 #pragma clang fp contract(off)
         // the partner row's sum, added in the same order as its own thread's
         float pv = 0.0f;
 #pragma unroll
-        for (int w = 0; w < kMaxHWaves; w++)
-          if (w < nw) pv += part[buf][w][rr ^ 1][2 * u] + part[buf][w][rr ^ 1][2 * u + 1];
+        for (int w = 0; w < kMaxHWaves; w++) {
+          const int ww = min(w, nw - 1);
+          const float h = part[buf][ww][rr ^ 1][2 * u] + part[buf][ww][rr ^ 1][2 * u + 1];
+          pv += w < nw ? h : 0.0f;
+        }
         const int r = tl * 16 + rr;
         if (r >= rows) continue;
         // rope.mojo:294 rotate_scaled, adjacent pairs: (a, b) <- (a c - b s, a s + b c)
