@@ -565,17 +565,6 @@ __global__ void htile_split_reduce_kernel(const float* __restrict__ part, int ns
   epilogue(y, aux, epi, (int64_t)t * ldy + r, r, v);
 }
 
-int cu_count_h() {
-  static int cus[64];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (!cus[dev]) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-    cus[dev] = n;
-  }
-  return cus[dev];
-}
 
 }  // namespace
 
@@ -591,7 +580,7 @@ int launch_htile(hipStream_t s, int kind, const RowSegs& sg, int32_t rows, int32
     if ((i < sg.nseg - 1 && sg.end[i] % 16) || sg.rb[i] != (int64_t)(cols / 256) * sbb || ((uintptr_t)sg.w[i] & 7))
       return fail(MI_ERR_SHAPE, "htile: segments must be whole 16-row tiles of %d-column rows, 8-byte aligned", cols);
   const int waves = cols / (256 * kSBW);
-  const int grid = std::min((rows + 15) / 16, cu_count_h());
+  const int grid = std::min((rows + 15) / 16, cu_count());
 #define MI_HT(T)                                                                                              \
   case T:                                                                                                     \
     if (kind == MI_Q6_K)                                                                                      \
@@ -635,7 +624,7 @@ int launch_htile_split(hipStream_t s, const void* w, int64_t row_bytes, int32_t 
   const int n = htile_nsplit(cols), pc = cols / n;
   const RowSegs sg = rows::one_matrix(w, row_bytes, rows);
   const int waves = pc / (256 * kSBW);
-  const int grid = std::min((rows + 15) / 16, std::max(1, cu_count_h() / n));
+  const int grid = std::min((rows + 15) / 16, std::max(1, cu_count() / n));
   const int64_t ysplit = (int64_t)tokens * rows;
 #define MI_HS(T)                                                                                              \
   case T:                                                                                                     \
@@ -672,7 +661,7 @@ int launch_htile_qkv_rope(hipStream_t s, const RowSegs& sg, int32_t cols, const 
     return fail(MI_ERR_SHAPE, "htile: no rope tile for %d columns at %d tokens", cols, tokens);
   const int rows = sg.end[sg.nseg - 1];
   const int waves = cols / (256 * kSBW);
-  const int grid = std::min((rows + 15) / 16, cu_count_h());
+  const int grid = std::min((rows + 15) / 16, cu_count());
 #define MI_HR(T)                                                                                              \
   case T:                                                                                                     \
     hipLaunchKernelGGL((htile_kernel<T, MI_Q4_K, false, true>), dim3(grid), dim3(waves * 64), 0, s, sg, cols, \
@@ -704,7 +693,7 @@ int launch_htile_glu(hipStream_t s, const void* gate, const void* up, int64_t ro
   sg.end[1] = sg.end[2] = 2 * rows;
   sg.nseg = 2;
   const int waves = cols / (256 * kSBW);
-  const int grid = std::min(rows / 32, cu_count_h());
+  const int grid = std::min(rows / 32, cu_count());
 #define MI_HTG(T)                                                                                             \
   case T:                                                                                                     \
     hipLaunchKernelGGL((htile_kernel<T, MI_Q4_K, true>), dim3(grid), dim3(waves * 64), 0, s, sg, cols,        \

@@ -238,6 +238,10 @@ __global__ __launch_bounds__((Q8 ? 16 : 12) * 64) void qkv_norm_kernel(const Row
   }
 }
 
+
+}  // namespace
+
+// Compute units of the current device (cached per device).
 int cu_count() {
   static int cus[64];
   int dev = 0;
@@ -249,8 +253,6 @@ int cu_count() {
   }
   return cus[dev];
 }
-
-}  // namespace
 
 bool rows_fits(int kind, int32_t cols) {
   const bool k = kind == MI_Q4_K || kind == MI_Q5_K;

@@ -164,6 +164,9 @@ int launch_matvec(hipStream_t s, int kind, const void* w, int64_t row_bytes, int
 // Internal epilogue bit of the GLU tiles: the quantized output xq_out is
 // followed, tokens * 4 * rows bytes on, by its hx form (the f16 tile's input).
 constexpr int kEpiHx = 1 << 16;
+// Compute units of the current device (cached per device).
+int cu_count();
+
 bool htile_fits(int kind, int32_t rows, int32_t cols, int32_t tokens);
 // Q4_K rows longer than 4096 columns on the f16 tile: K split over column
 // parts (part: htile_split_bytes of scratch), then one reduce launch that adds
