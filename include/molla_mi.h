@@ -243,6 +243,16 @@ typedef struct {
   const float* ffn_post_norm;
   int32_t ungated;             /* 1: the MLP is down(act(up(x))), gate unused */
   int32_t act;                 /* 0 silu, MI_ACT_GELU gelu (tanh form, kernel.mojo:499) */
+  /* Chaining layers at 2..8 tokens (no counterpart in the reference, which
+   * norms each layer's input in that layer): with next_norm set (device
+   * f32[width], the next layer's attn_norm), the layer also leaves that
+   * RMSNorm of its output in the workspace, in the forms its first matvec
+   * reads; a call with prenormed = 1 on the same workspace, tokens and
+   * shapes then starts from it instead of norming resid itself.  Where the
+   * down projection runs split over K on the f16 tile, the residual add and
+   * that norm are one launch.  Both are ignored at 1 token and above 8. */
+  const float* next_norm;
+  int32_t prenormed;
 } mi_layer_desc;
 
 /* One Llama layer for `tokens` independent sequences (batch decode, one token

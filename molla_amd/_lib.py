@@ -28,7 +28,7 @@ class MiLayerDesc(ctypes.Structure):
                [("rope_factors", P), ("cache_form", I32)] + \
                [(n, P) for n in ("q_bias", "k_bias", "v_bias", "q_norm", "k_norm", "attn_post_norm",
                                  "ffn_post_norm")] + \
-               [("ungated", I32), ("act", I32)]
+               [("ungated", I32), ("act", I32), ("next_norm", P), ("prenormed", I32)]
 
 
 # Every symbol include/molla_mi.h declares, with its C signature.

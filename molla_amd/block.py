@@ -103,6 +103,15 @@ def with_cache_form(desc: MiLayerDesc, form: int) -> MiLayerDesc:
     return d
 
 
+def chain_layers(descs: list) -> None:
+    """Link consecutive layer descriptors (run in order on one workspace):
+    layer i norms its output with layer i + 1's attn_norm, and layer i + 1
+    starts from that instead of norming its input itself."""
+    for a, b in zip(descs, descs[1:]):
+        a.next_norm = b.attn_norm
+        b.prenormed = 1
+
+
 def device_layer(ctx: gpu.DeviceContext, layer: DeviceLayer, x: torch.Tensor, k_cache: torch.Tensor,
                  v_cache: torch.Tensor, cache_stride: int, pos: torch.Tensor, max_count: int, tokens: int = 1,
                  work: torch.Tensor | None = None, form: int = gpu.CACHE_F16) -> None:
@@ -201,6 +210,9 @@ class DeviceSession:
         self.cache_form = cache_form
         self.cache_stride = context * gpu.cache_row(cache_form, kvw)
         self.descs = [with_cache_form(l.desc, cache_form) for l in model.layers]
+        # at 2..8 tokens each layer also norms its output for the next one
+        # (mi_layer_desc next_norm / prenormed; ignored at 1 token and above 8)
+        chain_layers(self.descs)
         dev = ctx.device
         self.k = [torch.empty(batch * self.cache_stride, dtype=torch.float16, device=dev) for _ in model.layers]
         self.v = [torch.empty(batch * self.cache_stride, dtype=torch.float16, device=dev) for _ in model.layers]

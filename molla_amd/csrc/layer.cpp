@@ -163,7 +163,8 @@ bool extended(const mi_layer_desc* d) {
 // Llama kernels stay for the Llama layer.
 static int extended_layer(hipStream_t s, const mi_layer_desc* d, float* resid, uint16_t* k_cache,
                           uint16_t* v_cache, int64_t cache_stride, const int32_t* kv_index, int64_t index_stride,
-                          const int32_t* pos, int32_t max_count, int32_t tokens, char* base, const Carve& c) {
+                          const int32_t* pos, int32_t max_count, int32_t tokens, char* base, const Carve& c,
+                          bool pre) {
   void* xq = base + c.xq;
   void* xq2 = base + c.xq2;
   float* qkv = (float*)(base + c.qkv);
@@ -175,7 +176,7 @@ static int extended_layer(hipStream_t s, const mi_layer_desc* d, float* resid, u
   const int32_t bias = d->q_bias ? MI_EPI_BIAS : MI_EPI_NONE;
   int rc;
   // attention_layer (block.mojo:319)
-  if ((rc = launch_rms_norm(s, resid, d->attn_norm, d->width, tokens, d->eps, nullptr, xq))) return rc;
+  if (!pre && (rc = launch_rms_norm(s, resid, d->attn_norm, d->width, tokens, d->eps, nullptr, xq))) return rc;
   if ((rc = launch_matvec(s, d->wq.kind, d->wq.data, d->wq.row_bytes, qw, d->width, xq, tokens, qkv, qkv_stride,
                           bias, d->q_bias)))
     return rc;
@@ -347,6 +348,13 @@ static int prefill_layer(hipStream_t s, const mi_layer_desc* d, float* resid, ui
   return mat(d->down, d->width, d->hidden, h, resid, d->width, MI_EPI_ADD, nullptr);
 }
 
+// The next layer's attention norm, when the caller asks for it (gain set):
+// done once a launch of this layer has written it.
+struct NextNorm {
+  const float* gain;
+  bool done;
+};
+
 // The down projection at 2..8 tokens from a GLU tile's output xq2: at 4 or
 // more tokens on the f16 tile split over K (the GLU tile then also writes
 // the hx form, down_htile), else the int8 tile split in two, or the
@@ -358,10 +366,17 @@ static bool down_htile(const mi_layer_desc* d, int32_t tokens) {
 }
 
 static int down_batch(hipStream_t s, const mi_layer_desc* d, const void* xq2, int32_t tokens, float* resid,
-                      void* part) {
+                      void* part, NextNorm* nn, void* xq) {
+  const void* hx2 = (const uint8_t*)xq2 + (size_t)xq_token_bytes(d->hidden) * tokens;
+  if (down_htile(d, tokens) && nn->gain && htile_split_norm_fits(d->width, d->hidden, tokens)) {
+    // the residual add and the next layer's norm in one launch after the parts
+    nn->done = true;
+    return launch_htile_split_norm(s, d->down.data, d->down.row_bytes, d->width, d->hidden, xq2, hx2, tokens, resid,
+                                   nn->gain, d->eps, (float*)part, xq,
+                                   (uint8_t*)xq + (size_t)xq_token_bytes(d->width) * tokens);
+  }
   if (down_htile(d, tokens))
-    return launch_htile_split(s, d->down.data, d->down.row_bytes, d->width, d->hidden, xq2,
-                              (const uint8_t*)xq2 + (size_t)xq_token_bytes(d->hidden) * tokens, tokens, resid,
+    return launch_htile_split(s, d->down.data, d->down.row_bytes, d->width, d->hidden, xq2, hx2, tokens, resid,
                               d->width, MI_EPI_ADD, nullptr, (float*)part);
   if (d->down.kind == MI_Q4_K && q4k_tile_split_fits(d->width, d->hidden, tokens))
     // 128 tiles over a 14336-value K: two blocks per tile and an ordered reduce
@@ -370,6 +385,10 @@ static int down_batch(hipStream_t s, const mi_layer_desc* d, const void* xq2, in
   return launch_matvec(s, d->down.kind, d->down.data, d->down.row_bytes, d->width, d->hidden, xq2, tokens, resid,
                        d->width, MI_EPI_ADD, nullptr);
 }
+
+static int llama_layer(hipStream_t s, const mi_layer_desc* d, float* resid, uint16_t* k_cache, uint16_t* v_cache,
+                       int64_t cache_stride, const int32_t* kv_index, int64_t index_stride, const int32_t* pos,
+                       int32_t max_count, int32_t tokens, char* base, const Carve& c, bool pre, NextNorm* nn);
 
 static int decoder_layer(mi_stream stream, const mi_layer_desc* d, float* resid, uint16_t* k_cache,
                          uint16_t* v_cache, int64_t cache_stride, const int32_t* kv_index, int64_t index_stride,
@@ -403,9 +422,26 @@ static int decoder_layer(mi_stream stream, const mi_layer_desc* d, float* resid,
 
   hipStream_t s = (hipStream_t)stream;
   char* base = (char*)work;
-  if (extended(d))
-    return extended_layer(s, d, resid, k_cache, v_cache, cache_stride, kv_index, index_stride, pos, max_count,
-                          tokens, base, c);
+  // 2..8 tokens: the input's norm may already be in the workspace, and the
+  // next layer's may be asked for (mi_layer_desc next_norm / prenormed)
+  const bool pre = tokens > 1 && d->prenormed;
+  NextNorm nn{tokens > 1 ? d->next_norm : nullptr, false};
+  rc = extended(d) ? extended_layer(s, d, resid, k_cache, v_cache, cache_stride, kv_index, index_stride, pos,
+                                    max_count, tokens, base, c, pre)
+                   : llama_layer(s, d, resid, k_cache, v_cache, cache_stride, kv_index, index_stride, pos, max_count,
+                                 tokens, base, c, pre, &nn);
+  if (rc || !nn.gain || nn.done) return rc;
+  return launch_rms_norm(s, resid, nn.gain, d->width, tokens, d->eps, nullptr, base + c.xq,
+                         (uint8_t*)(base + c.xq) + (size_t)xq_token_bytes(d->width) * tokens);
+}
+
+// The Llama layer at 1..8 tokens on the fused kernels (pre: the attention
+// norm's xq and hx forms are in the workspace already, 2..8 tokens).
+static int llama_layer(hipStream_t s, const mi_layer_desc* d, float* resid, uint16_t* k_cache, uint16_t* v_cache,
+                       int64_t cache_stride, const int32_t* kv_index, int64_t index_stride, const int32_t* pos,
+                       int32_t max_count, int32_t tokens, char* base, const Carve& c, bool pre, NextNorm* nn) {
+  int rc;
+  const int64_t kvw = (int64_t)d->kv_heads * d->head_dim;
   void* xq = base + c.xq;
   float* qkv = (float*)(base + c.qkv);
   float* up = (float*)(base + c.up);
@@ -464,7 +500,8 @@ static int decoder_layer(mi_stream stream, const mi_layer_desc* d, float* resid,
   } else {
     // at 2..8 tokens the norm also writes the hx form (the f16 tile's input)
     void* hxn = tokens > 1 ? (uint8_t*)xq + (size_t)xq_token_bytes(d->width) * tokens : nullptr;
-    if ((rc = launch_rms_norm(s, resid, d->attn_norm, d->width, tokens, d->eps, nullptr, xq, hxn))) return rc;
+    if (!pre && (rc = launch_rms_norm(s, resid, d->attn_norm, d->width, tokens, d->eps, nullptr, xq, hxn)))
+      return rc;
     bool roped = false;
     const bool tile_qkv = tokens > 1 && d->wq.kind == MI_Q4_K && d->wk.kind == MI_Q4_K &&
                           d->wv.kind == MI_Q4_K && q4k_tile_fits(d->width, tokens);
@@ -565,7 +602,7 @@ static int decoder_layer(mi_stream stream, const mi_layer_desc* d, float* resid,
     if ((rc = launch_htile_glu(s, d->gate.data, d->up.data, d->gate.row_bytes, d->hidden, d->width, xq, hx2, tokens,
                                MI_EPI_NONE, xq2, down_htile(d, tokens))))
       return rc;
-    return down_batch(s, d, xq2, tokens, resid, base + c.part);
+    return down_batch(s, d, xq2, tokens, resid, base + c.part, nn, xq);
   }
   if ((rc = launch_rms_norm(s, resid, d->ffn_norm, d->width, tokens, d->eps, nullptr, xq))) return rc;
   if (tokens == 1 && d->gate.kind == MI_Q4_K && d->up.kind == MI_Q4_K && d->gate.row_bytes == d->up.row_bytes &&
@@ -590,7 +627,7 @@ static int decoder_layer(mi_stream stream, const mi_layer_desc* d, float* resid,
     if ((rc = launch_q4k_tile_glu(s, d->gate.data, d->up.data, d->gate.row_bytes, d->hidden, d->width, xq, tokens,
                                   gate, d->hidden, down_htile(d, tokens) ? kEpiHx : MI_EPI_NONE, xq2)))
       return rc;
-    return down_batch(s, d, xq2, tokens, resid, base + c.part);
+    return down_batch(s, d, xq2, tokens, resid, base + c.part, nn, xq);
   } else {
     if ((rc = launch_matvec(s, d->up.kind, d->up.data, d->up.row_bytes, d->hidden, d->width, xq, tokens, up,
                             d->hidden, MI_EPI_NONE, nullptr)))

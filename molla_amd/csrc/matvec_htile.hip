@@ -236,7 +236,11 @@ __device__ __forceinline__ void sb_product_q6k(const uint8_t* lrows, int sb, con
 // token's position, q to y, k and v to the f16 caches (rp).
 // SPLIT: the split-K form (block row blockIdx.y reads a column part of
 // longer rows); the tile's rows are then not one run of memory.
-template <int TN, int KIND, bool GLU, bool ROPE = false, bool SPLIT = false>
+// COPY (SPLIT): the blocks also copy aux[0 .. ysplit) (the residual row the
+// parts are added to) into the slot after the last part, one value a
+// thread, so that the launch which adds the parts can write the residual
+// in place while every block of it still reads the old values.
+template <int TN, int KIND, bool GLU, bool ROPE = false, bool SPLIT = false, bool COPY = false>
 __global__ __launch_bounds__(kMaxHWaves * 64) void htile_kernel(const RowSegs sg, int cols,
                                                                      const uint8_t* __restrict__ xq,
                                                                      const uint8_t* __restrict__ hx,
@@ -328,6 +332,15 @@ __global__ __launch_bounds__(kMaxHWaves * 64) void htile_kernel(const RowSegs sg
   // weight buffers' space; each lane reads its fragments there.  (Per-lane
   // gathers of the fragments straight from memory, or a copy loop that
   // waits on each load, cost several times longer.)
+  static_assert(!COPY || SPLIT, "COPY is a split-K form");
+  float cpv = 0.0f;
+  int64_t cpi = 0;
+  if constexpr (COPY) {
+    // sent for first: the store below, after the first weight loads, then
+    // waits for this load only
+    cpi = min((int64_t)(blockIdx.y * gridDim.x + blockIdx.x) * blockDim.x + threadIdx.x, ysplit - 1);
+    cpv = aux[cpi];
+  }
   const int t = lm >> 1, part_hl = lm & 1;
   const bool live_col = t < TN;
   const int wave_bytes = kSBW * 8 * 128;  // one token's hx for one wave
@@ -346,6 +359,7 @@ __global__ __launch_bounds__(kMaxHWaves * 64) void htile_kernel(const RowSegs sg
   for (int u = 0; u < TN; u++) scl[u] = scale_src[u * (tok_bytes / 4) + sg_g * 4];
   uint2 ra[kLoads], rb_[kLoads];
   load_tile(ra, tile_of(0));  // the grid is at most `tiles` (GLU: groups) blocks
+  if constexpr (COPY) y[(int64_t)(gridDim.y - blockIdx.y) * ysplit + cpi] = cpv;
   // A block with more tiles than this one sends for tile 1 only after its
   // prologue: the prologue's own loads then compete with fewer weight loads
   // of the whole chip (14336 rows at 4 tokens: 16.4 against 17.5 us).  Split
@@ -611,8 +625,37 @@ bool htile_split_fits(int32_t rows, int32_t cols, int32_t tokens) {
   return n > 1 && htile_fits(MI_Q4_K, rows, cols / n, tokens);
 }
 
+// the parts, and one more slot for launch_htile_split_norm's residual copy
 size_t htile_split_bytes(int32_t rows, int32_t cols, int32_t tokens) {
-  return sizeof(float) * (size_t)htile_nsplit(cols) * rows * tokens;
+  return sizeof(float) * (size_t)(htile_nsplit(cols) + 1) * rows * tokens;
+}
+
+static int launch_split_main(hipStream_t s, const void* w, int64_t row_bytes, int32_t rows, int32_t cols,
+                             const void* xq, const void* hx, int32_t tokens, const float* resid, float* part) {
+  const int n = htile_nsplit(cols), pc = cols / n;
+  const RowSegs sg = rows::one_matrix(w, row_bytes, rows);
+  const int waves = pc / (256 * kSBW);
+  const int grid = std::min((rows + 15) / 16, std::max(1, cu_count() / n));
+  const int64_t ysplit = (int64_t)tokens * rows;
+  if (resid && (int64_t)grid * n * waves * 64 < ysplit)
+    return fail(MI_ERR_SHAPE, "htile: %d x %d blocks cannot copy %lld residual values", grid, n, (long long)ysplit);
+#define MI_HS(T)                                                                                              \
+  case T:                                                                                                     \
+    if (resid)                                                                                                \
+      hipLaunchKernelGGL((htile_kernel<T, MI_Q4_K, false, false, true, true>), dim3(grid, n), dim3(waves * 64), \
+                         0, s, sg, pc, (const uint8_t*)xq, (const uint8_t*)hx, part, (int64_t)rows, MI_EPI_NONE, \
+                         resid, nullptr, cols / 32, ysplit, QkvRope{});                                       \
+    else                                                                                                      \
+      hipLaunchKernelGGL((htile_kernel<T, MI_Q4_K, false, false, true>), dim3(grid, n), dim3(waves * 64), 0,  \
+                         s, sg, pc, (const uint8_t*)xq, (const uint8_t*)hx, part, (int64_t)rows, MI_EPI_NONE, \
+                         nullptr, nullptr, cols / 32, ysplit, QkvRope{});                                     \
+    break;
+  switch (tokens) {
+    MI_HS(2) MI_HS(3) MI_HS(4) MI_HS(5) MI_HS(6) MI_HS(7) MI_HS(8)
+    default: return fail(MI_ERR_ARG, "htile: %d tokens", tokens);
+  }
+#undef MI_HS
+  return hip_check(hipGetLastError(), "htile launch");
 }
 
 int launch_htile_split(hipStream_t s, const void* w, int64_t row_bytes, int32_t rows, int32_t cols, const void* xq,
@@ -621,28 +664,29 @@ int launch_htile_split(hipStream_t s, const void* w, int64_t row_bytes, int32_t 
   if (!htile_split_fits(rows, cols, tokens) || row_bytes != (int64_t)(cols / 256) * HGeo<MI_Q4_K>::SB ||
       ((uintptr_t)w & 7))
     return fail(MI_ERR_SHAPE, "htile: no split-K tile for %d x %d at %d tokens", rows, cols, tokens);
-  const int n = htile_nsplit(cols), pc = cols / n;
-  const RowSegs sg = rows::one_matrix(w, row_bytes, rows);
-  const int waves = pc / (256 * kSBW);
-  const int grid = std::min((rows + 15) / 16, std::max(1, cu_count() / n));
-  const int64_t ysplit = (int64_t)tokens * rows;
-#define MI_HS(T)                                                                                              \
-  case T:                                                                                                     \
-    hipLaunchKernelGGL((htile_kernel<T, MI_Q4_K, false, false, true>), dim3(grid, n), dim3(waves * 64), 0, s, \
-                       sg, pc,                                                                                \
-                       (const uint8_t*)xq, (const uint8_t*)hx, part, (int64_t)rows, MI_EPI_NONE, nullptr,     \
-                       nullptr, cols / 32, ysplit, QkvRope{});                                                \
-    break;
-  switch (tokens) {
-    MI_HS(2) MI_HS(3) MI_HS(4) MI_HS(5) MI_HS(6) MI_HS(7) MI_HS(8)
-    default: return fail(MI_ERR_ARG, "htile: %d tokens", tokens);
-  }
-#undef MI_HS
-  int rc = hip_check(hipGetLastError(), "htile launch");
+  int rc = launch_split_main(s, w, row_bytes, rows, cols, xq, hx, tokens, nullptr, part);
   if (rc) return rc;
-  hipLaunchKernelGGL(htile_split_reduce_kernel, dim3((tokens * rows + 255) / 256), dim3(256), 0, s, part, n, tokens,
-                     rows, y, ldy, epi, aux);
+  hipLaunchKernelGGL(htile_split_reduce_kernel, dim3((tokens * rows + 255) / 256), dim3(256), 0, s, part,
+                     htile_nsplit(cols), tokens, rows, y, ldy, epi, aux);
   return hip_check(hipGetLastError(), "htile split reduce");
+}
+
+bool htile_split_norm_fits(int32_t rows, int32_t cols, int32_t tokens) {
+  const int n = htile_nsplit(cols);
+  return htile_split_fits(rows, cols, tokens) && n <= kMaxNormSplit && rows % 32 == 0 &&
+         (int64_t)std::min((rows + 15) / 16, std::max(1, cu_count() / n)) * n * (cols / n / 256 / kSBW) * 64 >=
+             (int64_t)tokens * rows;
+}
+
+int launch_htile_split_norm(hipStream_t s, const void* w, int64_t row_bytes, int32_t rows, int32_t cols,
+                            const void* xq, const void* hx, int32_t tokens, float* resid, const float* gain,
+                            float eps, float* part, void* xq_out, void* hx_out) {
+  if (!htile_split_norm_fits(rows, cols, tokens) || row_bytes != (int64_t)(cols / 256) * HGeo<MI_Q4_K>::SB ||
+      ((uintptr_t)w & 7))
+    return fail(MI_ERR_SHAPE, "htile: no split-K tile with a norm for %d x %d at %d tokens", rows, cols, tokens);
+  int rc = launch_split_main(s, w, row_bytes, rows, cols, xq, hx, tokens, resid, part);
+  if (rc) return rc;
+  return launch_split_add_norm(s, part, htile_nsplit(cols), resid, gain, rows, tokens, eps, xq_out, hx_out);
 }
 
 bool htile_qkv_rope_fits(const RowSegs& sg, int32_t cols, int32_t tokens, int32_t head_dim, int32_t rope_dim) {

@@ -181,6 +181,20 @@ size_t htile_split_bytes(int32_t rows, int32_t cols, int32_t tokens);
 int launch_htile_split(hipStream_t s, const void* w, int64_t row_bytes, int32_t rows, int32_t cols, const void* xq,
                        const void* hx, int32_t tokens, float* y, int64_t ldy, int32_t epi, const float* aux,
                        float* part);
+// The same split with the residual add and the next RMSNorm after it in
+// one launch: resid += the parts (added in order, as the reduce above with
+// MI_EPI_ADD), then gain's norm of the new rows written in matvec form into
+// xq_out and in the hx form into hx_out.  Up to kMaxNormSplit parts.
+constexpr int kMaxNormSplit = 4;
+bool htile_split_norm_fits(int32_t rows, int32_t cols, int32_t tokens);
+int launch_htile_split_norm(hipStream_t s, const void* w, int64_t row_bytes, int32_t rows, int32_t cols,
+                            const void* xq, const void* hx, int32_t tokens, float* resid, const float* gain,
+                            float eps, float* part, void* xq_out, void* hx_out);
+// part[k][t][r] for k < nsplit, and the old residual in slot nsplit:
+// resid[t][r] = old + (part 0 + ... + part nsplit-1), then its RMSNorm by
+// gain (rms_norm_kernel's arithmetic) into xq and hx.
+int launch_split_add_norm(hipStream_t s, const float* part, int nsplit, float* resid, const float* gain, int32_t n,
+                          int32_t tokens, float eps, void* xq, void* hx);
 int launch_htile(hipStream_t s, int kind, const RowSegs& sg, int32_t rows, int32_t cols, const void* xq,
                  const void* hx, int32_t tokens, float* y, int64_t ldy, int32_t epi, const float* aux);
 // The gated MLP's input side on the same tile (Q4_K gate and up of `rows` x

@@ -31,7 +31,12 @@ constexpr int kNormThreads = 256;
 // With `trig`, the last block also writes (cos, sin) of the angle of pair p at
 // pos[0] for p < pairs, in float64 as rope.mojo:253-285, for the layer's fused
 // q|k|v rope; it has no other use for its spare threads' time.
-template <int PER>
+//
+// NS > 0: the row is the residual after a split-K matvec's parts are added
+// (x = part[k * pstride + ...] for k < NS, the old residual in slot NS; the
+// sums in htile_split_reduce_kernel's order), and each block also writes its
+// slice of that row to `out` (the residual, in place: no block reads it).
+template <int PER, int NS = 0>
 __global__ __launch_bounds__(kNormThreads) void rms_norm_kernel(const float* __restrict__ x,
                                                                 const float* __restrict__ gain, int n,
                                                                 float eps, float* __restrict__ out,
@@ -40,7 +45,7 @@ __global__ __launch_bounds__(kNormThreads) void rms_norm_kernel(const float* __r
                                                                 const int32_t* __restrict__ pos,
                                                                 const float* __restrict__ steps,
                                                                 const float* __restrict__ factors, int pairs,
-                                                                float2* __restrict__ trig) {
+                                                                float2* __restrict__ trig, int64_t pstride) {
 #pragma clang fp contract(off)
   const int t = blockIdx.y;
   if (trig && blockIdx.x == gridDim.x - 1) {
@@ -53,10 +58,28 @@ __global__ __launch_bounds__(kNormThreads) void rms_norm_kernel(const float* __r
   const int mine = blockIdx.x * kNormThreads + threadIdx.x;
   const bool live = mine < n;
   float xv[PER];
+  if constexpr (NS > 0) {
+    float pv[NS + 1][PER];
 #pragma unroll
-  for (int k = 0; k < PER; k++) {
-    const int i = threadIdx.x + k * kNormThreads;
-    xv[k] = i < n ? xr[i] : 0.0f;
+    for (int j = 0; j <= NS; j++)
+#pragma unroll
+      for (int k = 0; k < PER; k++) {
+        const int i = min((int)threadIdx.x + k * kNormThreads, n - 1);
+        pv[j][k] = xr[j * pstride + i];
+      }
+#pragma unroll
+    for (int k = 0; k < PER; k++) {
+      float v = pv[0][k];
+#pragma unroll
+      for (int j = 1; j < NS; j++) v += pv[j][k];
+      xv[k] = threadIdx.x + k * kNormThreads < n ? pv[NS][k] + v : 0.0f;
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < PER; k++) {
+      const int i = threadIdx.x + k * kNormThreads;
+      xv[k] = i < n ? xr[i] : 0.0f;
+    }
   }
   const float gm = live ? gain[mine] : 0.0f;
   // this thread's own value is one it already loaded for the sum (a second
@@ -77,7 +100,11 @@ __global__ __launch_bounds__(kNormThreads) void rms_norm_kernel(const float* __r
   for (int i = 0; i < kNormThreads / kWave; i++) sum += part[i];
   const float scale = (float)(1.0 / sqrt(sum / (double)n + (double)eps));
   const float v = xm * scale * gm;
-  if (out && live) out[(int64_t)t * n + mine] = v;
+  if constexpr (NS > 0) {
+    if (live) out[(int64_t)t * n + mine] = xm;
+  } else {
+    if (out && live) out[(int64_t)t * n + mine] = v;
+  }
   // A half-wave is one 32-value group; n is a multiple of 32 whenever xq
   // is asked for, so a group is either entirely live or entirely past the end.
   if (xq)
@@ -1239,7 +1266,7 @@ static int norm_launch(hipStream_t s, const float* x, const float* gain, int32_t
   dim3 grid(per, tokens);
 #define MI_NORM(P)                                                                                      \
   hipLaunchKernelGGL(rms_norm_kernel<P>, grid, dim3(kNormThreads), 0, s, x, gain, n, eps, out, (uint8_t*)xq, \
-                     (uint8_t*)hx, pos, steps, factors, pairs, (float2*)trig)
+                     (uint8_t*)hx, pos, steps, factors, pairs, (float2*)trig, 0)
   if (per <= 4) MI_NORM(4);
   else if (per <= 8) MI_NORM(8);
   else if (per <= 16) MI_NORM(16);
@@ -1248,6 +1275,31 @@ static int norm_launch(hipStream_t s, const float* x, const float* gain, int32_t
   else return fail(MI_ERR_SHAPE, "rms_norm: %d values per row is more than %d", n, 64 * kNormThreads);
 #undef MI_NORM
   return hip_check(hipGetLastError(), "rms_norm launch");
+}
+
+int launch_split_add_norm(hipStream_t s, const float* part, int nsplit, float* resid, const float* gain, int32_t n,
+                          int32_t tokens, float eps, void* xq, void* hx) {
+  const int per = (n + kNormThreads - 1) / kNormThreads;
+  if (n % 32 || !xq || !hx) return fail(MI_ERR_SHAPE, "split norm: %d values a row, xq and hx forms", n);
+  const int64_t ps = (int64_t)tokens * n;
+  dim3 grid(per, tokens);
+#define MI_SNORM(P, K)                                                                                         \
+  hipLaunchKernelGGL((rms_norm_kernel<P, K>), grid, dim3(kNormThreads), 0, s, part, gain, n, eps, resid,       \
+                     (uint8_t*)xq, (uint8_t*)hx, nullptr, nullptr, nullptr, 0, nullptr, ps)
+#define MI_SNORM_P(K)                                                                                          \
+  if (per <= 4) MI_SNORM(4, K);                                                                                \
+  else if (per <= 8) MI_SNORM(8, K);                                                                           \
+  else if (per <= 16) MI_SNORM(16, K);                                                                         \
+  else return fail(MI_ERR_SHAPE, "split norm: %d values per row is more than %d", n, 16 * kNormThreads);
+  switch (nsplit) {
+    case 2: MI_SNORM_P(2) break;
+    case 3: MI_SNORM_P(3) break;
+    case 4: MI_SNORM_P(4) break;
+    default: return fail(MI_ERR_ARG, "split norm: %d parts", nsplit);
+  }
+#undef MI_SNORM_P
+#undef MI_SNORM
+  return hip_check(hipGetLastError(), "split norm launch");
 }
 
 int launch_rms_norm(hipStream_t s, const float* x, const float* gain, int32_t n, int32_t tokens, float eps,

@@ -133,7 +133,7 @@ def test_mojo_binding_covers_the_header():
                "Q_BIAS": D.q_bias.offset, "K_BIAS": D.k_bias.offset, "V_BIAS": D.v_bias.offset,
                "Q_NORM": D.q_norm.offset, "K_NORM": D.k_norm.offset, "ATTN_POST_NORM": D.attn_post_norm.offset,
                "FFN_POST_NORM": D.ffn_post_norm.offset, "UNGATED": D.ungated.offset, "ACT": D.act.offset,
-               "SIZE": ctypes.sizeof(D)}
+               "NEXT_NORM": D.next_norm.offset, "PRENORMED": D.prenormed.offset, "SIZE": ctypes.sizeof(D)}
     for name, want in offsets.items():
         m = re.search(rf"comptime {name} = (\d+)", text)
         assert m and int(m.group(1)) == want, (name, want)

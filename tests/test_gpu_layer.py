@@ -561,3 +561,51 @@ def test_layer_chunk_of_one_sequence(paged, tokens, dims):
         kr, vr = kr.reshape(count, kvw), vr.reshape(count, kvw)
         assert np.allclose(got_k[p], kr[p], rtol=2e-3, atol=1e-3)
         assert np.allclose(got_v[p], vr[p], rtol=2e-3, atol=1e-3)
+
+
+@pytest.mark.parametrize("dims,tokens", [
+    ((1024, 14336, 8, 2, 128), 4),  # down split in four parts: add and norm in one launch
+    ((1024, 8192, 8, 2, 128), 8),   # two parts
+    ((512, 1024, 8, 2, 64), 3),     # int8 tiles: the next norm as its own launch
+])
+def test_chained_layers_match_unchained(dims, tokens):
+    """Three layers chained (mi_layer_desc next_norm / prenormed: each layer
+    norms its output for the next on the shared workspace) leave exactly the
+    residual stream and caches of the same layers run one by one."""
+    from molla_amd import block, gpu
+    from molla_amd._lib import MiLayerDesc, check, lib
+    import ctypes
+    ctx = gpu.DeviceContext(0)
+    spec = spec_of(*dims)
+    layers = [device_layer_from(make_layer_weights(spec, 11 + i), spec)[1] for i in range(3)]
+    bs = block.BlockSpec(width=spec["width"], hidden=spec["hidden"], heads=spec["heads"], kv_heads=spec["kv_heads"],
+                         head_dim=spec["head_dim"], rope_dim=spec["rope_dim"], rope_base=spec["rope_base"])
+    kvw = bs.kv_width()
+    pos = 150
+    count = pos + 1
+    cache_stride = count * kvw
+    k0 = synth.normal(tokens * cache_stride, 50).half().cuda()
+    v0 = synth.normal(tokens * cache_stride, 51).half().cuda()
+    x0 = synth.normal(tokens * bs.width, 52).cuda()
+    posd = torch.full((tokens,), pos, dtype=torch.int32, device="cuda")
+    need = max(block.layer_workspace(l, count, tokens) for l in layers)
+    L = lib()
+
+    def run(chained):
+        descs = [MiLayerDesc.from_buffer_copy(l.desc) for l in layers]
+        if chained:
+            block.chain_layers(descs)
+        x = x0.clone()
+        ks = [k0.clone() for _ in layers]
+        vs = [v0.clone() for _ in layers]
+        work = torch.zeros(need + 256, dtype=torch.uint8, device="cuda")
+        for i, d in enumerate(descs):
+            check(L.mi_decoder_layer(ctx.handle, ctypes.byref(d), x.data_ptr(), ks[i].data_ptr(), vs[i].data_ptr(),
+                                     cache_stride, posd.data_ptr(), count, tokens, work.data_ptr(), work.numel()))
+        ctx.synchronize()
+        return x.cpu(), [k.cpu() for k in ks], [v.cpu() for v in vs]
+
+    xa, ka, va = run(False)
+    xb, kb, vb = run(True)
+    assert torch.equal(xa, xb)
+    assert all(torch.equal(a, b) for a, b in zip(ka + va, kb + vb))
