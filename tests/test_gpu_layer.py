@@ -563,12 +563,14 @@ def test_layer_chunk_of_one_sequence(paged, tokens, dims):
         assert np.allclose(got_v[p], vr[p], rtol=2e-3, atol=1e-3)
 
 
-@pytest.mark.parametrize("dims,tokens", [
-    ((1024, 14336, 8, 2, 128), 4),  # down split in four parts: add and norm in one launch
-    ((1024, 8192, 8, 2, 128), 8),   # two parts
-    ((512, 1024, 8, 2, 64), 3),     # int8 tiles: the next norm as its own launch
+@pytest.mark.parametrize("dims,tokens,family", [
+    ((1024, 14336, 8, 2, 128), 4, None),  # down split in four parts: add and norm in one launch
+    ((1024, 8192, 8, 2, 128), 8, None),   # two parts
+    ((512, 1024, 8, 2, 64), 3, None),     # int8 tiles: the next norm as its own launch
+    ((512, 1024, 8, 2, 64), 4, "qwen2"),  # the layer of other families: its own launches
+    ((512, 1024, 8, 2, 64), 4, "gemma2"),
 ])
-def test_chained_layers_match_unchained(dims, tokens):
+def test_chained_layers_match_unchained(dims, tokens, family):
     """Three layers chained (mi_layer_desc next_norm / prenormed: each layer
     norms its output for the next on the shared workspace) leave exactly the
     residual stream and caches of the same layers run one by one."""
@@ -577,7 +579,11 @@ def test_chained_layers_match_unchained(dims, tokens):
     import ctypes
     ctx = gpu.DeviceContext(0)
     spec = spec_of(*dims)
-    layers = [device_layer_from(make_layer_weights(spec, 11 + i), spec)[1] for i in range(3)]
+    if family:
+        from tests.test_gpu_families import device_family_layer, family_host
+        layers = [device_family_layer(*family_host(family, spec, 31 + i))[1] for i in range(3)]
+    else:
+        layers = [device_layer_from(make_layer_weights(spec, 11 + i), spec)[1] for i in range(3)]
     bs = block.BlockSpec(width=spec["width"], hidden=spec["hidden"], heads=spec["heads"], kv_heads=spec["kv_heads"],
                          head_dim=spec["head_dim"], rope_dim=spec["rope_dim"], rope_base=spec["rope_base"])
     kvw = bs.kv_width()
