@@ -673,7 +673,8 @@ int launch_htile_split(hipStream_t s, const void* w, int64_t row_bytes, int32_t 
 
 bool htile_split_norm_fits(int32_t rows, int32_t cols, int32_t tokens) {
   const int n = htile_nsplit(cols);
-  return htile_split_fits(rows, cols, tokens) && n <= kMaxNormSplit && rows % 32 == 0 &&
+  // launch_split_add_norm takes rows of up to 16 * 256 values
+  return htile_split_fits(rows, cols, tokens) && n <= kMaxNormSplit && rows % 32 == 0 && rows <= 4096 &&
          (int64_t)std::min((rows + 15) / 16, std::max(1, cu_count() / n)) * n * (cols / n / 256 / kSBW) * 64 >=
              (int64_t)tokens * rows;
 }

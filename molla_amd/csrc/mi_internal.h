@@ -184,7 +184,8 @@ int launch_htile_split(hipStream_t s, const void* w, int64_t row_bytes, int32_t 
 // The same split with the residual add and the next RMSNorm after it in
 // one launch: resid += the parts (added in order, as the reduce above with
 // MI_EPI_ADD), then gain's norm of the new rows written in matvec form into
-// xq_out and in the hx form into hx_out.  Up to kMaxNormSplit parts.
+// xq_out and in the hx form into hx_out.  Up to kMaxNormSplit parts and
+// 4096 rows.
 constexpr int kMaxNormSplit = 4;
 bool htile_split_norm_fits(int32_t rows, int32_t cols, int32_t tokens);
 int launch_htile_split_norm(hipStream_t s, const void* w, int64_t row_bytes, int32_t rows, int32_t cols,
