@@ -104,7 +104,9 @@ int mi_dequant(mi_stream stream, int kind, const void* w, int64_t count, float* 
  * (22 bits) and the weights as the exact integer codes of their blocks, so
  * the result stays within ~1e-6 relative of the fp32 host dot.  It needs
  * mi_matvec_workspace(cols, tokens) bytes; given mi_matmul_workspace(rows,
- * cols, tokens) it may also split long reductions across more blocks. */
+ * cols, tokens) it may also split long reductions across more blocks, and so
+ * may a batch of 2..8 tokens of a Q4_K matrix with few rows for its long K
+ * (the down projection, 4096 x 14336). */
 size_t mi_matvec_workspace(int32_t cols, int32_t tokens);
 size_t mi_matmul_workspace(int32_t rows, int32_t cols, int32_t tokens);
 int mi_matvec(mi_stream stream, int kind, const void* w, int64_t row_bytes,

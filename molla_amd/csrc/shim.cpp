@@ -153,10 +153,23 @@ static void* hx_of(const void* xq, int32_t cols, int32_t tokens) {
   return tokens > 1 ? (uint8_t*)xq + xq_token_bytes(cols) * tokens : nullptr;
 }
 
+// 2..8 tokens: the activation forms, then (256-aligned) room for the parts
+// of a Q4_K matvec split over K (launch_htile_split, launch_q4k_tile_split).
+static size_t batch_act_bytes(int32_t cols, int32_t tokens) {
+  return (mi_matvec_workspace(cols, tokens) + 255) & ~(size_t)255;
+}
+static size_t batch_split_bytes(int32_t rows, int32_t cols, int32_t tokens) {
+  size_t b = 0;
+  if (htile_split_fits(rows, cols, tokens)) b = htile_split_bytes(rows, cols, tokens);
+  if (q4k_tile_split_fits(rows, cols, tokens)) b = std::max(b, q4k_tile_split_bytes(rows, tokens));
+  return b;
+}
+
 size_t mi_matmul_workspace(int32_t rows, int32_t cols, int32_t tokens) {
   if (rows <= 0 || cols <= 0 || tokens <= 0 || tokens > kMaxPrefill) return 0;
   if (tokens > kMaxTokens) return prefill_workspace(rows, cols, tokens);
-  return mi_matvec_workspace(cols, tokens);
+  const size_t split = tokens > 1 ? batch_split_bytes(rows, cols, tokens) : 0;
+  return split ? batch_act_bytes(cols, tokens) + split : mi_matvec_workspace(cols, tokens);
 }
 
 static int check_xq(const char* name, const void* xq, int32_t cols, int32_t tokens) {
@@ -174,16 +187,21 @@ int mi_quantize(mi_stream stream, const float* x, int32_t cols, int32_t tokens, 
   return launch_quantize((hipStream_t)stream, x, cols, tokens, xq, hx_of(xq, cols, tokens));
 }
 
+static int check_epi(int32_t epi, const float* aux) {
+  if (epi & ~(MI_EPI_BIAS | MI_EPI_ADD | MI_EPI_GLU | MI_ACT_GELU))
+    return fail(MI_ERR_ARG, "matvec: unknown epilogue bits 0x%x", epi);
+  if ((epi & MI_EPI_BIAS) && (epi & MI_EPI_GLU)) return fail(MI_ERR_ARG, "matvec: BIAS and GLU together");
+  if ((epi & (MI_EPI_BIAS | MI_EPI_GLU)) && !aux) return fail(MI_ERR_ARG, "matvec: epilogue needs aux");
+  return MI_OK;
+}
+
 int mi_matvec_xq(mi_stream stream, int kind, const void* w, int64_t row_bytes, int32_t rows,
                  int32_t cols, const void* xq, int32_t tokens, float* y, int32_t epi, const float* aux) {
   int rc = check_weight("matvec", kind, w, row_bytes, rows, cols);
   if (rc) return rc;
   if ((rc = check_xq("matvec", xq, cols, tokens))) return rc;
   if (!y) return fail(MI_ERR_ARG, "matvec: null output");
-  if (epi & ~(MI_EPI_BIAS | MI_EPI_ADD | MI_EPI_GLU | MI_ACT_GELU))
-    return fail(MI_ERR_ARG, "matvec: unknown epilogue bits 0x%x", epi);
-  if ((epi & MI_EPI_BIAS) && (epi & MI_EPI_GLU)) return fail(MI_ERR_ARG, "matvec: BIAS and GLU together");
-  if ((epi & (MI_EPI_BIAS | MI_EPI_GLU)) && !aux) return fail(MI_ERR_ARG, "matvec: epilogue needs aux");
+  if ((rc = check_epi(epi, aux))) return rc;
   return launch_matvec((hipStream_t)stream, kind, w, row_bytes, rows, cols, xq, tokens, y, rows, epi, aux,
                        hx_of(xq, cols, tokens));
 }
@@ -219,8 +237,27 @@ int mi_matvec(mi_stream stream, int kind, const void* w, int64_t row_bytes, int3
   if (work_bytes < mi_matvec_workspace(cols, tokens))
     return fail(MI_ERR_WORKSPACE, "matvec: workspace of %zu bytes, %zu needed", work_bytes,
                 mi_matvec_workspace(cols, tokens));
+  // 2..8 tokens of a Q4_K matrix with too few 16-row tiles for its long K,
+  // given room for the parts (mi_matmul_workspace): split over K, on the f16
+  // tile where it fits, else the int8 tile
+  const size_t act = batch_act_bytes(cols, tokens);
+  const bool split = tokens > 1 && kind == MI_Q4_K && batch_split_bytes(rows, cols, tokens) &&
+                     work_bytes >= act + batch_split_bytes(rows, cols, tokens);
+  if (!split) {
+    if ((rc = mi_quantize(stream, x, cols, tokens, work))) return rc;
+    return mi_matvec_xq(stream, kind, w, row_bytes, rows, cols, work, tokens, y, epi, aux);
+  }
+  if (!y) return fail(MI_ERR_ARG, "matvec: null output");
+  if ((rc = check_epi(epi, aux))) return rc;
   if ((rc = mi_quantize(stream, x, cols, tokens, work))) return rc;
-  return mi_matvec_xq(stream, kind, w, row_bytes, rows, cols, work, tokens, y, epi, aux);
+  hipStream_t s = (hipStream_t)stream;
+  float* part = (float*)((char*)work + act);
+  if (htile_split_fits(rows, cols, tokens) && row_bytes == (int64_t)(cols / 256) * 144 && !((uintptr_t)w & 7))
+    return launch_htile_split(s, w, row_bytes, rows, cols, work, hx_of(work, cols, tokens), tokens, y, rows, epi,
+                              aux, part);
+  if (q4k_tile_split_fits(rows, cols, tokens))
+    return launch_q4k_tile_split(s, w, row_bytes, rows, cols, work, tokens, y, rows, epi, aux, part);
+  return launch_matvec(s, kind, w, row_bytes, rows, cols, work, tokens, y, rows, epi, aux, hx_of(work, cols, tokens));
 }
 
 int mi_rms_norm(mi_stream stream, const float* x, const float* gain, int32_t n, int32_t tokens, float eps,
