@@ -53,6 +53,29 @@ __device__ __forceinline__ void kscale(uint32_t y, uint32_t z, uint32_t w4, int 
   m = __builtin_amdgcn_ubfe(hi ? w4 : z, s + 4 * hi, 4) | (__builtin_amdgcn_ubfe(z, s + 4 + 2 * hi, 2) << 4);
 }
 
+// The segment fields as scalar values for a per-lane row: selects between
+// the kernel argument's array elements by a per-lane row were folded back
+// into a per-lane index, which copied the whole struct to scratch memory
+// (72 bytes a lane) and read it back with vector loads at every launch.
+__device__ __forceinline__ int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
+__device__ __forceinline__ const uint8_t* uni(const uint8_t* p) {
+  const uint64_t v = (uint64_t)p;
+  return (const uint8_t*)((uint64_t)(uint32_t)uni((int)v) | ((uint64_t)(uint32_t)uni((int)(v >> 32)) << 32));
+}
+__device__ __forceinline__ int64_t uni(int64_t v) { return (int64_t)(uint64_t)uni((const uint8_t*)v); }
+
+__device__ __forceinline__ const uint8_t* lane_seg_row(const RowSegs& sg, int row) {
+  const int e0 = uni(sg.end[0]), e1 = uni(sg.end[1]);
+  const bool s0 = row < e0, s1 = !s0 && row < e1;
+  const uint8_t* w = s0 ? uni(sg.w[0]) : (s1 ? uni(sg.w[1]) : uni(sg.w[2]));
+  const int64_t rb = s0 ? uni(sg.rb[0]) : (s1 ? uni(sg.rb[1]) : uni(sg.rb[2]));
+  return w + (int64_t)(row - (s0 ? 0 : (s1 ? e0 : e1))) * rb;
+}
+__device__ __forceinline__ int lane_seg_rows(const RowSegs& sg) {
+  const int n = uni(sg.nseg);
+  return n >= 3 ? uni(sg.end[2]) : (n == 2 ? uni(sg.end[1]) : uni(sg.end[0]));
+}
+
 constexpr int kTileWaves = 8;  // waves per block for matrices of many tiles
 constexpr int kWideWaves = 16;  // ... and for few (<= 8192 rows): more waves split K
 
@@ -77,10 +100,10 @@ __global__ __launch_bounds__(KW * 64) void q4k_tile_kernel(const RowSegs sg, int
   __shared__ float red[NP][KW][T][32];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, ks = blockDim.x >> 6;
   const int n = lane & 31, kh = lane >> 5;
-  const int rows = GLU ? sg.end[0] : sg.end[sg.nseg - 1];
+  const int rows = GLU ? sg.end[0] : lane_seg_rows(sg);
   const int row = min(blockIdx.x * 32 + n, rows - 1);
   const uint8_t* wrow[NP];
-  wrow[0] = GLU ? sg.w[0] + (int64_t)row * sg.rb[0] : rows::seg_row(sg, row);
+  wrow[0] = GLU ? sg.w[0] + (int64_t)row * sg.rb[0] : lane_seg_row(sg, row);
   if (GLU) wrow[NP - 1] = sg.w[1] + (int64_t)row * sg.rb[1];
   const int nsb = cols >> 8, G = cols >> 5;
   // gridDim.y > 1 splits K over blocks: block y takes waves y * ks .. of the

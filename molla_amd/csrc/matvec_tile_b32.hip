@@ -231,8 +231,12 @@ int launch_k(hipStream_t s, const void* w, int64_t rb, int rows, int cols, const
              int64_t ldy, int epi, const float* aux) {
   switch (tokens) {
     case 2: return launch_t<KIND, 2>(s, w, rb, rows, cols, 2, xq, y, ldy, epi, aux);
-    case 3: return launch_t<KIND, 3>(s, w, rb, rows, cols, 3, xq, y, ldy, epi, aux);
-    case 4: return launch_t<KIND, 4>(s, w, rb, rows, cols, 4, xq, y, ldy, epi, aux);
+    // 3 tokens take the 4-token slots: with windows of 8 / 3 blocks the
+    // block index of a slot is a run-time division, and the chunk's codes
+    // went to scratch memory (304-400 bytes a lane; 54.8 against 35.5 us at
+    // 4096 x 14336)
+    case 3:
+    case 4: return launch_t<KIND, 4>(s, w, rb, rows, cols, tokens, xq, y, ldy, epi, aux);
     case 5:
     case 6:
     case 7:
