@@ -100,18 +100,29 @@ __device__ __forceinline__ float piece_dot(const Q6Piece& p, uint32_t sh, int a,
   return d * part;
 }
 
+// KS > 1 (rows longer than 4096 columns, the down projection's 14336): the
+// four waves of a block take one row together, wave k the units
+// [k U, (k + 1) U) with U = ceil(units / KS); their sums meet in LDS and wave
+// 0 adds them in wave order, so the result does not depend on timing.  The
+// block walks rows blockIdx.x, blockIdx.x + gridDim.x, ... with the next
+// row's loads in flight, as the single-wave form does.
+template <int KS>
 __global__ __launch_bounds__(256) void q6k_rows_kernel(const uint8_t* __restrict__ w, int64_t rb, int rows,
                                                        int cols, const uint8_t* __restrict__ xq,
                                                        float* __restrict__ y, int epi,
                                                        const float* __restrict__ aux) {
-  const int lane = threadIdx.x & 63;
-  const int nw = gridDim.x * 4;
-  const int wv = blockIdx.x * 4 + (threadIdx.x >> 6);
+  static_assert(KS == 1 || KS <= 4, "up to four waves split a row");
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int nw = KS == 1 ? gridDim.x * 4 : gridDim.x;
+  const int wv = KS == 1 ? blockIdx.x * 4 + wave : blockIdx.x;
   const int units = cols >> 6;
-  const bool act = lane < units;
-  const int u = act ? lane : units - 1;
+  const int per = (units + KS - 1) / KS;  // units of a wave's K-slice
+  const int ks = KS == 1 ? 0 : wave;
+  const bool act = lane < per && ks * per + lane < units;
+  const int u = act ? ks * per + lane : units - 1;
   const int sb = u >> 2, n = (u >> 1) & 1, a = u & 1;
   const int g0 = 8 * sb + 4 * n + a, g1 = g0 + 2;
+  __shared__ float part[2][KS > 1 ? KS : 1];
 
   XQ6Regs x;
   {
@@ -142,14 +153,14 @@ __global__ __launch_bounds__(256) void q6k_rows_kernel(const uint8_t* __restrict
   };
 
   int row = wv;
-  if (row >= rows) return;
+  if (row >= rows) return;  // uniform over a block when KS > 1
   Q6Piece cur, nxt;
   uint32_t sh_cur, sh_nxt;
   {
     const uint8_t* b = blk(row, sh_cur);
     load_piece(cur, b, sh_cur, n, a);
   }
-  while (true) {
+  for (int it = 0;; it++) {
     const int nrow = row + nw;
     const bool more = nrow < rows;
     if (more) {
@@ -158,7 +169,21 @@ __global__ __launch_bounds__(256) void q6k_rows_kernel(const uint8_t* __restrict
     }
     float v = act ? piece_dot(cur, sh_cur, a, x) : 0.0f;
     v = wave_sum(v);
-    if (lane == 0) epilogue(y, aux, epi, row, row, v);
+    if constexpr (KS > 1) {
+      // part alternates between two buffers: a row's buffer is written
+      // again two rows later, after every wave has passed the next row's
+      // barrier, which wave 0 reaches only once it has read this one
+      if (lane == 0) part[it & 1][ks] = v;
+      __syncthreads();
+      if (ks == 0 && lane == 0) {
+        float t = part[it & 1][0];
+#pragma unroll
+        for (int k = 1; k < KS; k++) t += part[it & 1][k];
+        epilogue(y, aux, epi, row, row, t);
+      }
+    } else {
+      if (lane == 0) epilogue(y, aux, epi, row, row, v);
+    }
     if (!more) break;
     cur = nxt;
     sh_cur = sh_nxt;
@@ -169,17 +194,30 @@ __global__ __launch_bounds__(256) void q6k_rows_kernel(const uint8_t* __restrict
 }  // namespace
 
 bool q6k_rows_fits(int32_t cols, int64_t row_bytes) {
-  return cols > 0 && cols % 256 == 0 && cols / 64 <= 64 && row_bytes % 4 == 0;
+  return cols > 0 && cols % 256 == 0 && cols / 64 <= 4 * 64 && row_bytes % 4 == 0;
 }
 
 int launch_q6k_rows(hipStream_t s, const void* w, int64_t row_bytes, int32_t rows, int32_t cols, const void* xq,
                     float* y, int32_t epi, const float* aux) {
   if (((uintptr_t)w & 3) || row_bytes % 4) return fail(MI_ERR_ALIGN, "matvec: Q6_K rows must be 4-byte aligned");
-  // four waves per SIMD over the whole chip; each wave then streams rows
-  const int waves = std::min(rows, 256 * 4 * 4);
-  const int blocks = (waves + 3) / 4;
-  hipLaunchKernelGGL(q6k_rows_kernel, dim3(blocks), dim3(256), 0, s, (const uint8_t*)w, row_bytes, rows, cols,
-                     (const uint8_t*)xq, y, epi, aux);
+  const int ks = (cols / 64 + 63) / 64;  // waves a row takes
+  if (ks == 1) {
+    // four waves per SIMD over the whole chip; each wave then streams rows
+    const int waves = std::min(rows, 256 * 4 * 4);
+    const int blocks = (waves + 3) / 4;
+    hipLaunchKernelGGL(q6k_rows_kernel<1>, dim3(blocks), dim3(256), 0, s, (const uint8_t*)w, row_bytes, rows, cols,
+                       (const uint8_t*)xq, y, epi, aux);
+  } else {
+    // a block of four waves a row, as many blocks as four waves a SIMD hold
+    const int blocks = std::min(rows, 256 * 4);
+#define MI_Q6R(K)                                                                                              \
+  hipLaunchKernelGGL(q6k_rows_kernel<K>, dim3(blocks), dim3(256), 0, s, (const uint8_t*)w, row_bytes, rows, cols, \
+                     (const uint8_t*)xq, y, epi, aux)
+    if (ks == 2) MI_Q6R(2);
+    else if (ks == 3) MI_Q6R(3);
+    else MI_Q6R(4);
+#undef MI_Q6R
+  }
   return hip_check(hipGetLastError(), "matvec launch");
 }
 

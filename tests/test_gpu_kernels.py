@@ -190,6 +190,15 @@ def test_matmul_tokens_epilogues(ctx, kind, tokens):
     (oracle.Q4_0, 4096, 14336, 4),
     (oracle.Q4_K, 14336, 4096, 4),
     (oracle.Q4_K, 4096, 14336, 4),
+    (oracle.Q4_K, 4096, 14336, 2),      # split over K at 2, 3 and 8 tokens too
+    (oracle.Q4_K, 4096, 14336, 3),
+    (oracle.Q4_K, 4096, 14336, 8),
+    (oracle.Q4_0, 4096, 14336, 3),      # 3 tokens on the 4-token slots
+    (oracle.Q8_0, 1000, 4096, 3),
+    # Q6_K rows longer than 4096 at one token: four, three and two waves a row
+    (oracle.Q6_K, 4096, 14336, 1),      # a Q4_K_M file's ffn_down
+    (oracle.Q6_K, 333, 12288, 1),
+    (oracle.Q6_K, 70, 5120, 1),
 ])
 def test_matvec_config_shapes(ctx, kind, rows, cols, tokens):
     from molla_amd import gpu
