@@ -361,22 +361,25 @@ struct NextNorm {
 // general matvec.  4096 x 14336 cold: 19.4 against 21.8 us at 4 tokens,
 // 21.4 against 32.5 us at 8.
 static bool down_htile(const mi_layer_desc* d, int32_t tokens) {
-  return tokens >= 4 && d->down.kind == MI_Q4_K && htile_split_fits(d->width, d->hidden, tokens) &&
-         d->down.row_bytes == (int64_t)(d->hidden / 256) * 144 && !((uintptr_t)d->down.data & 7);
+  const int k = d->down.kind;
+  return tokens >= 4 && (k == MI_Q4_K || k == MI_Q6_K) && htile_split_fits(k, d->width, d->hidden, tokens) &&
+         d->down.row_bytes == (int64_t)(d->hidden / 256) * (k == MI_Q6_K ? 210 : 144) &&
+         !((uintptr_t)d->down.data & (k == MI_Q6_K ? 3 : 7));
 }
 
 static int down_batch(hipStream_t s, const mi_layer_desc* d, const void* xq2, int32_t tokens, float* resid,
                       void* part, NextNorm* nn, void* xq) {
   const void* hx2 = (const uint8_t*)xq2 + (size_t)xq_token_bytes(d->hidden) * tokens;
-  if (down_htile(d, tokens) && nn->gain && htile_split_norm_fits(d->width, d->hidden, tokens)) {
+  if (down_htile(d, tokens) && nn->gain && htile_split_norm_fits(d->down.kind, d->width, d->hidden, tokens)) {
     // the residual add and the next layer's norm in one launch after the parts
     nn->done = true;
-    return launch_htile_split_norm(s, d->down.data, d->down.row_bytes, d->width, d->hidden, xq2, hx2, tokens, resid,
+    return launch_htile_split_norm(s, d->down.kind, d->down.data, d->down.row_bytes, d->width, d->hidden, xq2, hx2, tokens, resid,
                                    nn->gain, d->eps, (float*)part, xq,
                                    (uint8_t*)xq + (size_t)xq_token_bytes(d->width) * tokens);
   }
   if (down_htile(d, tokens))
-    return launch_htile_split(s, d->down.data, d->down.row_bytes, d->width, d->hidden, xq2, hx2, tokens, resid,
+    return launch_htile_split(s, d->down.kind, d->down.data, d->down.row_bytes, d->width, d->hidden, xq2, hx2,
+                              tokens, resid,
                               d->width, MI_EPI_ADD, nullptr, (float*)part);
   if (d->down.kind == MI_Q4_K && q4k_tile_split_fits(d->width, d->hidden, tokens))
     // 128 tiles over a 14336-value K: two blocks per tile and an ordered reduce

@@ -52,6 +52,9 @@ typedef _Float16 hh8 __attribute__((ext_vector_type(8)));
 typedef _Float16 hh2 __attribute__((ext_vector_type(2)));
 typedef float ff4 __attribute__((ext_vector_type(4)));
 typedef uint32_t uu4 __attribute__((ext_vector_type(4)));
+struct __attribute__((aligned(4))) U2a {
+  uint32_t x, y;
+};
 
 constexpr int kSBW = 2;                                  // superblocks per wave
 constexpr int kMaxHWaves = 8;                            // cols <= 8 * 512
@@ -310,7 +313,10 @@ __global__ __launch_bounds__(kMaxHWaves * 64) void htile_kernel(const RowSegs sg
       // a word of a missing row reads the last word of the last row
       const uint32_t lastw = (uint32_t)(min(16, rows - tl * 16) - 1) * (uint32_t)rstride + (uint32_t)(rb - 8);
 #pragma unroll
-      for (int j = 0; j < kLoads; j++) r[j] = *(const uint2*)(src + min(wfull[j], lastw));
+      for (int j = 0; j < kLoads; j++) {
+        const U2a v = *(const U2a*)(src + min(wfull[j], lastw));  // 4-byte aligned (Q6_K parts)
+        r[j] = make_uint2(v.x, v.y);
+      }
     } else {
       const uint2* src = (const uint2*)rows::seg_row(sg, tl * 16);
       const int words = min(16, rows - tl * 16) * (rb >> 3);
@@ -614,80 +620,99 @@ int launch_htile(hipStream_t s, int kind, const RowSegs& sg, int32_t rows, int32
 
 // Split K for rows longer than one block's 4096 columns (the down
 // projection's 14336 = 4 x 3584): parts of a multiple of 512 columns.
-static int htile_nsplit(int32_t cols) {
+// A part's row bytes must be whole 8-byte words (a tile is copied in 8-byte
+// words, row by row): any number of 144-byte Q4_K superblocks, a multiple of
+// four 210-byte Q6_K ones (14336 columns: seven parts of 2048).
+static int htile_nsplit(int kind, int32_t cols) {
   for (int n = (cols + 4095) / 4096; n <= 8; n++)
-    if (cols % (n * 256 * kSBW) == 0) return n;
+    if (cols % (n * 256 * kSBW) == 0 && (kind != MI_Q6_K || (cols / n / 256) % 4 == 0)) return n;
   return 0;
 }
 
-bool htile_split_fits(int32_t rows, int32_t cols, int32_t tokens) {
-  const int n = htile_nsplit(cols);
-  return n > 1 && htile_fits(MI_Q4_K, rows, cols / n, tokens);
+bool htile_split_fits(int kind, int32_t rows, int32_t cols, int32_t tokens) {
+  const int n = htile_nsplit(kind, cols);
+  return n > 1 && htile_fits(kind, rows, cols / n, tokens);
+}
+
+// Q4_K or Q6_K rows of whole superblocks, at the alignment the split's word
+// loads need (a Q6_K part starts 4 bytes past an 8-byte boundary when it
+// holds an odd number of 210-byte superblocks)
+static bool split_rows_ok(int kind, const void* w, int64_t row_bytes, int32_t cols) {
+  const int sbb = kind == MI_Q6_K ? HGeo<MI_Q6_K>::SB : HGeo<MI_Q4_K>::SB;
+  return (kind == MI_Q4_K || kind == MI_Q6_K) && row_bytes == (int64_t)(cols / 256) * sbb &&
+         !((uintptr_t)w & (kind == MI_Q6_K ? 3 : 7));
 }
 
 // the parts, and one more slot for launch_htile_split_norm's residual copy
 size_t htile_split_bytes(int32_t rows, int32_t cols, int32_t tokens) {
-  return sizeof(float) * (size_t)(htile_nsplit(cols) + 1) * rows * tokens;
+  // room for either kind's parts
+  const int n = std::max(htile_nsplit(MI_Q4_K, cols), htile_nsplit(MI_Q6_K, cols));
+  return sizeof(float) * (size_t)(n + 1) * rows * tokens;
 }
 
-static int launch_split_main(hipStream_t s, const void* w, int64_t row_bytes, int32_t rows, int32_t cols,
+static int launch_split_main(hipStream_t s, int kind, const void* w, int64_t row_bytes, int32_t rows, int32_t cols,
                              const void* xq, const void* hx, int32_t tokens, const float* resid, float* part) {
-  const int n = htile_nsplit(cols), pc = cols / n;
+  const int n = htile_nsplit(kind, cols), pc = cols / n;
   const RowSegs sg = rows::one_matrix(w, row_bytes, rows);
   const int waves = pc / (256 * kSBW);
   const int grid = std::min((rows + 15) / 16, std::max(1, cu_count() / n));
   const int64_t ysplit = (int64_t)tokens * rows;
   if (resid && (int64_t)grid * n * waves * 64 < ysplit)
     return fail(MI_ERR_SHAPE, "htile: %d x %d blocks cannot copy %lld residual values", grid, n, (long long)ysplit);
+#define MI_HSK(T, K)                                                                                          \
+  if (resid)                                                                                                  \
+    hipLaunchKernelGGL((htile_kernel<T, K, false, false, true, true>), dim3(grid, n), dim3(waves * 64), 0, s, \
+                       sg, pc, (const uint8_t*)xq, (const uint8_t*)hx, part, (int64_t)rows, MI_EPI_NONE, resid, \
+                       nullptr, cols / 32, ysplit, QkvRope{});                                                \
+  else                                                                                                        \
+    hipLaunchKernelGGL((htile_kernel<T, K, false, false, true>), dim3(grid, n), dim3(waves * 64), 0, s, sg,   \
+                       pc, (const uint8_t*)xq, (const uint8_t*)hx, part, (int64_t)rows, MI_EPI_NONE, nullptr,  \
+                       nullptr, cols / 32, ysplit, QkvRope{});
 #define MI_HS(T)                                                                                              \
   case T:                                                                                                     \
-    if (resid)                                                                                                \
-      hipLaunchKernelGGL((htile_kernel<T, MI_Q4_K, false, false, true, true>), dim3(grid, n), dim3(waves * 64), \
-                         0, s, sg, pc, (const uint8_t*)xq, (const uint8_t*)hx, part, (int64_t)rows, MI_EPI_NONE, \
-                         resid, nullptr, cols / 32, ysplit, QkvRope{});                                       \
-    else                                                                                                      \
-      hipLaunchKernelGGL((htile_kernel<T, MI_Q4_K, false, false, true>), dim3(grid, n), dim3(waves * 64), 0,  \
-                         s, sg, pc, (const uint8_t*)xq, (const uint8_t*)hx, part, (int64_t)rows, MI_EPI_NONE, \
-                         nullptr, nullptr, cols / 32, ysplit, QkvRope{});                                     \
+    if (kind == MI_Q6_K) {                                                                                    \
+      MI_HSK(T, MI_Q6_K)                                                                                      \
+    } else {                                                                                                  \
+      MI_HSK(T, MI_Q4_K)                                                                                      \
+    }                                                                                                         \
     break;
   switch (tokens) {
     MI_HS(2) MI_HS(3) MI_HS(4) MI_HS(5) MI_HS(6) MI_HS(7) MI_HS(8)
     default: return fail(MI_ERR_ARG, "htile: %d tokens", tokens);
   }
 #undef MI_HS
+#undef MI_HSK
   return hip_check(hipGetLastError(), "htile launch");
 }
 
-int launch_htile_split(hipStream_t s, const void* w, int64_t row_bytes, int32_t rows, int32_t cols, const void* xq,
-                       const void* hx, int32_t tokens, float* y, int64_t ldy, int32_t epi, const float* aux,
-                       float* part) {
-  if (!htile_split_fits(rows, cols, tokens) || row_bytes != (int64_t)(cols / 256) * HGeo<MI_Q4_K>::SB ||
-      ((uintptr_t)w & 7))
+int launch_htile_split(hipStream_t s, int kind, const void* w, int64_t row_bytes, int32_t rows, int32_t cols,
+                       const void* xq, const void* hx, int32_t tokens, float* y, int64_t ldy, int32_t epi,
+                       const float* aux, float* part) {
+  if (!htile_split_fits(kind, rows, cols, tokens) || !split_rows_ok(kind, w, row_bytes, cols))
     return fail(MI_ERR_SHAPE, "htile: no split-K tile for %d x %d at %d tokens", rows, cols, tokens);
-  int rc = launch_split_main(s, w, row_bytes, rows, cols, xq, hx, tokens, nullptr, part);
+  int rc = launch_split_main(s, kind, w, row_bytes, rows, cols, xq, hx, tokens, nullptr, part);
   if (rc) return rc;
   hipLaunchKernelGGL(htile_split_reduce_kernel, dim3((tokens * rows + 255) / 256), dim3(256), 0, s, part,
-                     htile_nsplit(cols), tokens, rows, y, ldy, epi, aux);
+                     htile_nsplit(kind, cols), tokens, rows, y, ldy, epi, aux);
   return hip_check(hipGetLastError(), "htile split reduce");
 }
 
-bool htile_split_norm_fits(int32_t rows, int32_t cols, int32_t tokens) {
-  const int n = htile_nsplit(cols);
+bool htile_split_norm_fits(int kind, int32_t rows, int32_t cols, int32_t tokens) {
+  const int n = htile_nsplit(kind, cols);
   // launch_split_add_norm takes rows of up to 16 * 256 values
-  return htile_split_fits(rows, cols, tokens) && n <= kMaxNormSplit && rows % 32 == 0 && rows <= 4096 &&
+  return htile_split_fits(kind, rows, cols, tokens) && n <= kMaxNormSplit && rows % 32 == 0 && rows <= 4096 &&
          (int64_t)std::min((rows + 15) / 16, std::max(1, cu_count() / n)) * n * (cols / n / 256 / kSBW) * 64 >=
              (int64_t)tokens * rows;
 }
 
-int launch_htile_split_norm(hipStream_t s, const void* w, int64_t row_bytes, int32_t rows, int32_t cols,
+int launch_htile_split_norm(hipStream_t s, int kind, const void* w, int64_t row_bytes, int32_t rows, int32_t cols,
                             const void* xq, const void* hx, int32_t tokens, float* resid, const float* gain,
                             float eps, float* part, void* xq_out, void* hx_out) {
-  if (!htile_split_norm_fits(rows, cols, tokens) || row_bytes != (int64_t)(cols / 256) * HGeo<MI_Q4_K>::SB ||
-      ((uintptr_t)w & 7))
+  if (!htile_split_norm_fits(kind, rows, cols, tokens) || !split_rows_ok(kind, w, row_bytes, cols))
     return fail(MI_ERR_SHAPE, "htile: no split-K tile with a norm for %d x %d at %d tokens", rows, cols, tokens);
-  int rc = launch_split_main(s, w, row_bytes, rows, cols, xq, hx, tokens, resid, part);
+  int rc = launch_split_main(s, kind, w, row_bytes, rows, cols, xq, hx, tokens, resid, part);
   if (rc) return rc;
-  return launch_split_add_norm(s, part, htile_nsplit(cols), resid, gain, rows, tokens, eps, xq_out, hx_out);
+  return launch_split_add_norm(s, part, htile_nsplit(kind, cols), resid, gain, rows, tokens, eps, xq_out, hx_out);
 }
 
 bool htile_qkv_rope_fits(const RowSegs& sg, int32_t cols, int32_t tokens, int32_t head_dim, int32_t rope_dim) {

@@ -168,27 +168,27 @@ constexpr int kEpiHx = 1 << 16;
 int cu_count();
 
 bool htile_fits(int kind, int32_t rows, int32_t cols, int32_t tokens);
-// Q4_K rows longer than 4096 columns on the f16 tile: K split over column
+// Q4_K or Q6_K rows longer than 4096 columns on the f16 tile: K split over column
 // parts (part: htile_split_bytes of scratch), then one reduce launch that adds
 // the parts in order and applies the epilogue.
-bool htile_split_fits(int32_t rows, int32_t cols, int32_t tokens);
+bool htile_split_fits(int kind, int32_t rows, int32_t cols, int32_t tokens);
 // q|k|v (whole 16-row segments) with the rope and the f16 cache store in the
 // epilogue, as launch_q4k_tile_qkv_rope.
 bool htile_qkv_rope_fits(const RowSegs& sg, int32_t cols, int32_t tokens, int32_t head_dim, int32_t rope_dim);
 int launch_htile_qkv_rope(hipStream_t s, const RowSegs& sg, int32_t cols, const void* xq, const void* hx,
                           int32_t tokens, float* q, int64_t ldq, const QkvRope& rp);
 size_t htile_split_bytes(int32_t rows, int32_t cols, int32_t tokens);
-int launch_htile_split(hipStream_t s, const void* w, int64_t row_bytes, int32_t rows, int32_t cols, const void* xq,
-                       const void* hx, int32_t tokens, float* y, int64_t ldy, int32_t epi, const float* aux,
-                       float* part);
+int launch_htile_split(hipStream_t s, int kind, const void* w, int64_t row_bytes, int32_t rows, int32_t cols,
+                       const void* xq, const void* hx, int32_t tokens, float* y, int64_t ldy, int32_t epi,
+                       const float* aux, float* part);
 // The same split with the residual add and the next RMSNorm after it in
 // one launch: resid += the parts (added in order, as the reduce above with
 // MI_EPI_ADD), then gain's norm of the new rows written in matvec form into
 // xq_out and in the hx form into hx_out.  Up to kMaxNormSplit parts and
 // 4096 rows.
 constexpr int kMaxNormSplit = 4;
-bool htile_split_norm_fits(int32_t rows, int32_t cols, int32_t tokens);
-int launch_htile_split_norm(hipStream_t s, const void* w, int64_t row_bytes, int32_t rows, int32_t cols,
+bool htile_split_norm_fits(int kind, int32_t rows, int32_t cols, int32_t tokens);
+int launch_htile_split_norm(hipStream_t s, int kind, const void* w, int64_t row_bytes, int32_t rows, int32_t cols,
                             const void* xq, const void* hx, int32_t tokens, float* resid, const float* gain,
                             float eps, float* part, void* xq_out, void* hx_out);
 // part[k][t][r] for k < nsplit, and the old residual in slot nsplit:

@@ -154,21 +154,25 @@ static void* hx_of(const void* xq, int32_t cols, int32_t tokens) {
 }
 
 // 2..8 tokens: the activation forms, then (256-aligned) room for the parts
-// of a Q4_K matvec split over K (launch_htile_split, launch_q4k_tile_split).
+// of a Q4_K or Q6_K matvec split over K (launch_htile_split,
+// launch_q4k_tile_split).
 static size_t batch_act_bytes(int32_t cols, int32_t tokens) {
   return (mi_matvec_workspace(cols, tokens) + 255) & ~(size_t)255;
 }
-static size_t batch_split_bytes(int32_t rows, int32_t cols, int32_t tokens) {
+static size_t batch_split_bytes(int kind, int32_t rows, int32_t cols, int32_t tokens) {
   size_t b = 0;
-  if (htile_split_fits(rows, cols, tokens)) b = htile_split_bytes(rows, cols, tokens);
-  if (q4k_tile_split_fits(rows, cols, tokens)) b = std::max(b, q4k_tile_split_bytes(rows, tokens));
+  if ((kind == MI_Q4_K || kind == MI_Q6_K) && htile_split_fits(kind, rows, cols, tokens))
+    b = htile_split_bytes(rows, cols, tokens);
+  if (kind == MI_Q4_K && q4k_tile_split_fits(rows, cols, tokens)) b = std::max(b, q4k_tile_split_bytes(rows, tokens));
   return b;
 }
 
 size_t mi_matmul_workspace(int32_t rows, int32_t cols, int32_t tokens) {
   if (rows <= 0 || cols <= 0 || tokens <= 0 || tokens > kMaxPrefill) return 0;
   if (tokens > kMaxTokens) return prefill_workspace(rows, cols, tokens);
-  const size_t split = tokens > 1 ? batch_split_bytes(rows, cols, tokens) : 0;
+  const size_t split = tokens > 1 ? std::max(batch_split_bytes(MI_Q4_K, rows, cols, tokens),
+                                             batch_split_bytes(MI_Q6_K, rows, cols, tokens))
+                                  : 0;
   return split ? batch_act_bytes(cols, tokens) + split : mi_matvec_workspace(cols, tokens);
 }
 
@@ -237,12 +241,12 @@ int mi_matvec(mi_stream stream, int kind, const void* w, int64_t row_bytes, int3
   if (work_bytes < mi_matvec_workspace(cols, tokens))
     return fail(MI_ERR_WORKSPACE, "matvec: workspace of %zu bytes, %zu needed", work_bytes,
                 mi_matvec_workspace(cols, tokens));
-  // 2..8 tokens of a Q4_K matrix with too few 16-row tiles for its long K,
-  // given room for the parts (mi_matmul_workspace): split over K, on the f16
-  // tile where it fits, else the int8 tile
+  // 2..8 tokens of a Q4_K or Q6_K matrix with too few 16-row tiles for its
+  // long K, given room for the parts (mi_matmul_workspace): split over K, on
+  // the f16 tile where it fits, else (Q4_K) the int8 tile
   const size_t act = batch_act_bytes(cols, tokens);
-  const bool split = tokens > 1 && kind == MI_Q4_K && batch_split_bytes(rows, cols, tokens) &&
-                     work_bytes >= act + batch_split_bytes(rows, cols, tokens);
+  const size_t sb = tokens > 1 ? batch_split_bytes(kind, rows, cols, tokens) : 0;
+  const bool split = sb && work_bytes >= act + sb;
   if (!split) {
     if ((rc = mi_quantize(stream, x, cols, tokens, work))) return rc;
     return mi_matvec_xq(stream, kind, w, row_bytes, rows, cols, work, tokens, y, epi, aux);
@@ -252,10 +256,12 @@ int mi_matvec(mi_stream stream, int kind, const void* w, int64_t row_bytes, int3
   if ((rc = mi_quantize(stream, x, cols, tokens, work))) return rc;
   hipStream_t s = (hipStream_t)stream;
   float* part = (float*)((char*)work + act);
-  if (htile_split_fits(rows, cols, tokens) && row_bytes == (int64_t)(cols / 256) * 144 && !((uintptr_t)w & 7))
-    return launch_htile_split(s, w, row_bytes, rows, cols, work, hx_of(work, cols, tokens), tokens, y, rows, epi,
-                              aux, part);
-  if (q4k_tile_split_fits(rows, cols, tokens))
+  const int sbb = kind == MI_Q6_K ? 210 : 144;
+  if (htile_split_fits(kind, rows, cols, tokens) && row_bytes == (int64_t)(cols / 256) * sbb &&
+      !((uintptr_t)w & (kind == MI_Q6_K ? 3 : 7)))
+    return launch_htile_split(s, kind, w, row_bytes, rows, cols, work, hx_of(work, cols, tokens), tokens, y, rows,
+                              epi, aux, part);
+  if (kind == MI_Q4_K && q4k_tile_split_fits(rows, cols, tokens))
     return launch_q4k_tile_split(s, w, row_bytes, rows, cols, work, tokens, y, rows, epi, aux, part);
   return launch_matvec(s, kind, w, row_bytes, rows, cols, work, tokens, y, rows, epi, aux, hx_of(work, cols, tokens));
 }

@@ -197,6 +197,8 @@ def test_matmul_tokens_epilogues(ctx, kind, tokens):
     (oracle.Q8_0, 1000, 4096, 3),
     # Q6_K rows longer than 4096 at one token: four, three and two waves a row
     (oracle.Q6_K, 4096, 14336, 1),      # a Q4_K_M file's ffn_down
+    (oracle.Q6_K, 4096, 14336, 4),      # ... at 4 and 8 tokens: the f16 tile split over K
+    (oracle.Q6_K, 4096, 14336, 8),
     (oracle.Q6_K, 333, 12288, 1),
     (oracle.Q6_K, 70, 5120, 1),
 ])

@@ -153,6 +153,39 @@ def test_layer_matches_oracle(dims, pos, tokens, factors):
         assert np.allclose(got_v[t, pos], vr[pos], rtol=2e-3, atol=1e-3)
 
 
+@pytest.mark.parametrize("tokens", [1, 4, 8])
+def test_layer_q4_k_m_kinds_match_oracle(tokens):
+    """The kinds of a Q4_K_M file: attn_v and ffn_down in Q6_K (the f16
+    tile's split over K takes the Q6_K down at 4 and 8 tokens)."""
+    from molla_amd import block, gpu
+    ctx = gpu.DeviceContext(0)
+    spec = spec_of(1024, 14336, 8, 2, 128)
+    host = make_layer_weights(spec, 9, {"wv": oracle.Q6_K, "down": oracle.Q6_K})
+    bs, layer = device_layer_from(host, spec)
+    kvw = bs.kv_width()
+    pos = 120
+    count = pos + 1
+    cache_stride = count * kvw
+    keys16 = synth.normal(tokens * cache_stride, 43).half()
+    vals16 = synth.normal(tokens * cache_stride, 44).half()
+    x = synth.normal(tokens * bs.width, 45).numpy()
+    kd, vd = keys16.clone().cuda(), vals16.clone().cuda()
+    xd = torch.from_numpy(x.copy()).cuda()
+    posd = torch.full((tokens,), pos, dtype=torch.int32, device="cuda")
+    block.device_layer(ctx, layer, xd, kd, vd, cache_stride, posd, count, tokens)
+    ctx.synchronize()
+    got_x = xd.cpu().numpy().reshape(tokens, -1)
+    keep = []
+    L = oracle.make_layer(spec, host, keep)
+    for t in range(tokens):
+        xr = x.reshape(tokens, -1)[t].copy()
+        kr = keys16.float().numpy().reshape(tokens, -1)[t].copy()
+        vr = vals16.float().numpy().reshape(tokens, -1)[t].copy()
+        bound = layer_gate(spec, host, xr, kr, vr, pos)
+        oracle.layer_step(L, xr, kr, vr, pos, pos, f16_store=True, threads=8)
+        assert_layer_close(got_x[t], xr, bound, f"seq {t}:")
+
+
 def test_layer_unaligned_residual_runs_separate_norms():
     """A residual row that is not 16-byte aligned makes the batch-1 layer run
     both norms as launches of their own (the kernels with the norm folded in
