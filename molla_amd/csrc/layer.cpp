@@ -500,6 +500,42 @@ static int llama_layer(hipStream_t s, const mi_layer_desc* d, float* resid, uint
         return rc;
       if ((rc = launch_q4k_qkv_rope(s, sg, d->width, xq, qkv, rp))) return rc;
     }
+  } else if (tokens == 1 && !kv_index && !d->neox && !q8 && d->wq.kind == MI_Q4_K && d->wk.kind == MI_Q4_K &&
+             d->wv.kind == MI_Q6_K && q4k_rows_fits(d->width) &&
+             q4k_qkv_rope_fits(d->width, d->head_dim, d->rope_dim)) {
+    // a Q4_K_M file's layer at one token (Q6_K v): the norm with this
+    // position's rope table, q|k with the rope and k's cache store in the
+    // row kernel's epilogue, then v and its store
+    float* trig = (float*)(base + c.trig);
+    RowSegs qk{};
+    qk.w[0] = (const uint8_t*)d->wq.data;
+    qk.w[1] = qk.w[2] = (const uint8_t*)d->wk.data;
+    qk.rb[0] = d->wq.row_bytes;
+    qk.rb[1] = qk.rb[2] = d->wk.row_bytes;
+    qk.end[0] = qw;
+    qk.end[1] = qk.end[2] = qw + (int32_t)kvw;
+    qk.nseg = 2;
+    QkvRope rp{};
+    rp.qw = qw;
+    rp.kvw = (int)kvw;
+    rp.head_dim = d->head_dim;
+    rp.rope_dim = d->rope_dim;
+    rp.trig = (const float2*)trig;
+    rp.pos = pos;
+    rp.k_cache = (__half*)k_cache;
+    rp.v_cache = (__half*)v_cache;
+    rp.steps = d->rope_steps;
+    rp.factors = d->rope_factors;
+    if ((rc = launch_rms_norm_trig(s, resid, d->attn_norm, d->width, d->eps, xq, pos, d->rope_steps,
+                                   d->rope_factors, d->rope_dim / 2, trig)))
+      return rc;
+    if ((rc = launch_q4k_qkv_rope(s, qk, d->width, xq, qkv, rp))) return rc;
+    float* vrow = qkv + qw + kvw;
+    if ((rc = launch_matvec(s, d->wv.kind, d->wv.data, d->wv.row_bytes, (int32_t)kvw, d->width, xq, 1, vrow,
+                            (int32_t)kvw, MI_EPI_NONE, nullptr)))
+      return rc;
+    if ((rc = launch_store_kv(s, nullptr, vrow, (int32_t)kvw, k_cache, v_cache, pos, 0, 1, qkv_stride, 0)))
+      return rc;
   } else {
     // at 2..8 tokens the norm also writes the hx form (the f16 tile's input)
     void* hxn = tokens > 1 ? (uint8_t*)xq + (size_t)xq_token_bytes(d->width) * tokens : nullptr;

@@ -259,7 +259,8 @@ __global__ void store_kv_kernel(const float* __restrict__ k, const float* __rest
   const int slot = slot_dev ? slot_dev[t] : slot_host;
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= kvw) return;
-  kc[(int64_t)t * cache_stride + (int64_t)slot * kvw + i] = __float2half_rn(k[(int64_t)t * src_stride + i]);
+  // k null: the values only (the keys were stored, rotated, elsewhere)
+  if (k) kc[(int64_t)t * cache_stride + (int64_t)slot * kvw + i] = __float2half_rn(k[(int64_t)t * src_stride + i]);
   vc[(int64_t)t * cache_stride + (int64_t)slot * kvw + i] = __float2half_rn(v[(int64_t)t * src_stride + i]);
 }
 
