@@ -153,6 +153,7 @@ def main():
         line["batched"] = _batched(L, h, kind, ws, copies, rb, stream)
         line["kinds"] = _kinds(L, h, stream)
         line["head"] = _head(L, h, stream)
+        line["layer_kinds"] = _layer_kinds(L, h, stream)
     peak = _stream_peak(stream)
     line["roofline"]["stream_peak"] = peak
     line["roofline"]["frac_of_stream_33MB"] = round(achieved / peak["read_33MB"]["GB_s"], 4)
@@ -310,6 +311,62 @@ def _head(L, h, stream, reps=20):
         gbs = rows * rb / us / 1e3
         out[f"tokens_{tokens}"] = {"logits_us": round(us, 2), "GB_s": round(gbs, 1),
                                    "frac_hbm_peak": round(gbs / PEAK_GBS, 4), "argmax_us": round(am, 2)}
+    return out
+
+
+def _layer_kinds(L, h, stream, reps=30):
+    """One 8B-shaped decoder layer (config 4's shape) at context 2049, at 1
+    and 4 tokens, with every projection Q4_K and with a Q4_K_M file's kinds
+    (Q6_K attn_v and ffn_down): microseconds a layer call, eager."""
+    import ctypes
+
+    import torch
+
+    from molla_amd import block, gpu, synth
+    from molla_amd._lib import check
+
+    spec = block.BlockSpec()
+    qw, kvw = spec.q_width(), spec.kv_width()
+    shapes = {"wq": (qw, spec.width), "wk": (kvw, spec.width), "wv": (kvw, spec.width), "wo": (spec.width, qw),
+              "gate": (spec.hidden, spec.width), "up": (spec.hidden, spec.width), "down": (spec.width, spec.hidden)}
+    steps = torch.from_numpy(gpu.rope_steps(spec.rope_dim, spec.rope_base)).cuda()
+    ctx = gpu.DeviceContext(0, stream=stream)
+    out = {}
+    for name, q6 in (("all_q4_k", ()), ("q4_k_m", ("wv", "down"))):
+        ws = {}
+        for i, (n, (r, c)) in enumerate(shapes.items()):
+            kind = gpu.Q_Q6_K if n in q6 else gpu.Q_Q4_K
+            ws[n] = gpu.Tensor.from_bytes(synth.quant_tensor(kind, r, c, 500 + i, device="cuda"), kind, c, r)
+        an = synth.normal(spec.width, 510, device="cuda", mean=1.0, std=0.1)
+        fn = synth.normal(spec.width, 511, device="cuda", mean=1.0, std=0.1)
+        layer = block.DeviceLayer(spec, an, fn, ws, steps)
+        for tokens in (1, 4):
+            count = 2049
+            stride = count * kvw
+            k = synth.normal(tokens * stride, 40, device="cuda").half()
+            v = synth.normal(tokens * stride, 41, device="cuda").half()
+            x = synth.normal(tokens * spec.width, 42, device="cuda")
+            pos = torch.full((tokens,), count - 1, dtype=torch.int32, device="cuda")
+            need = block.layer_workspace(layer, count, tokens)
+            work = torch.empty(need + 256, dtype=torch.uint8, device="cuda")
+            d = layer.desc
+
+            def call():
+                check(L.mi_decoder_layer(ctx.handle, ctypes.byref(d), x.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                         stride, pos.data_ptr(), count, tokens, work.data_ptr(), work.numel()))
+            with torch.cuda.stream(stream):
+                for _ in range(3):
+                    call()
+                torch.cuda.synchronize()
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record(stream)
+                for _ in range(reps):
+                    call()
+                e1.record(stream)
+                torch.cuda.synchronize()
+            out[f"{name}_tokens_{tokens}_us"] = round(e0.elapsed_time(e1) * 1e3 / reps, 2)
+        del ws, layer
+        torch.cuda.empty_cache()
     return out
 
 
