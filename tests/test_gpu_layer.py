@@ -432,7 +432,7 @@ def paged_from_contiguous(caches, count, row, tokens, extra, seed):
 
 @pytest.mark.parametrize("form", ["f16", "q8"])
 @pytest.mark.parametrize("dims,pos,tokens", [((256, 512, 4, 2, 64), 77, 1), ((512, 1024, 8, 2, 64), 300, 3)])
-def test_layer_paged_matches_contiguous(form, dims, pos, tokens):
+def test_layer_paged_matches_contiguous(form, dims, pos, tokens, kinds=None):
     """The paged layer (cells scattered over a shared pool, gpu.mojo:571
     DevicePaging) gives the contiguous layer's residual and new cache rows
     bit for bit: only the addressing differs."""
@@ -441,7 +441,7 @@ def test_layer_paged_matches_contiguous(form, dims, pos, tokens):
     ctx = gpu.DeviceContext(0)
     f = gpu.CACHE_Q8 if form == "q8" else gpu.CACHE_F16
     spec = spec_of(*dims)
-    bs, layer = device_layer_from(make_layer_weights(spec, 11), spec)
+    bs, layer = device_layer_from(make_layer_weights(spec, 11, kinds), spec)
     kvw = bs.kv_width()
     row = gpu.cache_row(f, kvw)
     count = pos + 1
@@ -475,6 +475,45 @@ def test_layer_paged_matches_contiguous(form, dims, pos, tokens):
             c = cells[t, j]
             assert np.array_equal(kc[t, j * row:(j + 1) * row], kpool[c * row:(c + 1) * row])
             assert np.array_equal(vc[t, j * row:(j + 1) * row], vpool[c * row:(c + 1) * row])
+
+
+@pytest.mark.parametrize("tokens", [3, 4])
+def test_layer_paged_matches_contiguous_q4_k_m_kinds(tokens):
+    """The same with a Q6_K attn_v and ffn_down: the batched q|k and v
+    launches store k and v through the cell index too."""
+    test_layer_paged_matches_contiguous("f16", (512, 1024, 8, 2, 64), 300, tokens,
+                                        {"wv": oracle.Q6_K, "down": oracle.Q6_K})
+
+
+@pytest.mark.parametrize("kinds,tokens", [
+    ({}, 1), ({}, 4), ({}, 8),
+    ({"wv": oracle.Q6_K, "down": oracle.Q6_K}, 1),
+    ({"wv": oracle.Q6_K, "down": oracle.Q6_K}, 3),
+    ({"wv": oracle.Q6_K, "down": oracle.Q6_K}, 4),
+])
+def test_layer_ignores_prior_workspace_contents(kinds, tokens):
+    """The layer reads nothing of its workspace it has not written in the
+    same call: runs over workspaces filled with different bytes agree bit
+    for bit."""
+    from molla_amd import block, gpu
+    ctx = gpu.DeviceContext(0)
+    spec = spec_of(512, 1024, 8, 2, 64)
+    bs, layer = device_layer_from(make_layer_weights(spec, 11, kinds), spec)
+    kvw, pos = bs.kv_width(), 300
+    count = pos + 1
+    need = block.layer_workspace(layer, count, tokens)
+    outs = []
+    for fill in (0, 0x7F, 0x3C, 0xFF):
+        k = synth.normal(tokens * count * kvw, 60).half().cuda()
+        v = synth.normal(tokens * count * kvw, 61).half().cuda()
+        x = synth.normal(tokens * bs.width, 62).cuda()
+        posd = torch.full((tokens,), pos, dtype=torch.int32, device="cuda")
+        work = torch.full((need + 256,), fill, dtype=torch.uint8, device="cuda")
+        block.device_layer(ctx, layer, x, k, v, count * kvw, posd, count, tokens, work=work)
+        ctx.synchronize()
+        outs.append((x.cpu(), k.cpu(), v.cpu()))
+    for o in outs[1:]:
+        assert all(torch.equal(a, b) for a, b in zip(outs[0], o))
 
 
 def test_layer_paged_skips_positions_it_does_not_hold():
