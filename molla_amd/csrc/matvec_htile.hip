@@ -588,9 +588,12 @@ __global__ void htile_split_reduce_kernel(const float* __restrict__ part, int ns
 
 }  // namespace
 
+// A tile is copied in 8-byte words, row by row, so a row must be whole
+// words: any number of 144-byte Q4_K superblocks, a multiple of four 210-byte
+// Q6_K ones (a Q6_K row of 2, 6, 10 or 14 superblocks would straddle words).
 bool htile_fits(int kind, int32_t rows, int32_t cols, int32_t tokens) {
-  return (kind == MI_Q4_K || kind == MI_Q6_K) && tokens >= 2 && tokens <= kMaxTokens &&
-         cols % (256 * kSBW) == 0 && cols / (256 * kSBW) <= kMaxHWaves && rows > 0;
+  return (kind == MI_Q4_K || (kind == MI_Q6_K && (cols / 256) % 4 == 0)) && tokens >= 2 &&
+         tokens <= kMaxTokens && cols % (256 * kSBW) == 0 && cols / (256 * kSBW) <= kMaxHWaves && rows > 0;
 }
 
 int launch_htile(hipStream_t s, int kind, const RowSegs& sg, int32_t rows, int32_t cols, const void* xq,

@@ -201,6 +201,10 @@ def test_matmul_tokens_epilogues(ctx, kind, tokens):
     (oracle.Q6_K, 4096, 14336, 8),
     (oracle.Q6_K, 333, 12288, 1),
     (oracle.Q6_K, 70, 5120, 1),
+    # Q6_K rows of 2 and 6 superblocks at a batch: not whole 8-byte words,
+    # so not the f16 tile
+    (oracle.Q6_K, 200, 512, 4),
+    (oracle.Q6_K, 200, 1536, 3),
 ])
 def test_matvec_config_shapes(ctx, kind, rows, cols, tokens):
     from molla_amd import gpu
