@@ -544,9 +544,47 @@ static int llama_layer(hipStream_t s, const mi_layer_desc* d, float* resid, uint
     bool roped = false;
     const bool tile_qkv = tokens > 1 && d->wq.kind == MI_Q4_K && d->wk.kind == MI_Q4_K &&
                           d->wv.kind == MI_Q4_K && q4k_tile_fits(d->width, tokens);
+    // a Q4_K_M file's layer: Q4_K q and k, Q6_K v
+    RowSegs qk{}, vs{};
+    bool mixed_qkv = tokens > 1 && !d->neox && !q8 && d->wq.kind == MI_Q4_K && d->wk.kind == MI_Q4_K &&
+                     d->wv.kind == MI_Q6_K;
+    if (mixed_qkv) {
+      qk.w[0] = (const uint8_t*)d->wq.data;
+      qk.w[1] = qk.w[2] = (const uint8_t*)d->wk.data;
+      qk.rb[0] = d->wq.row_bytes;
+      qk.rb[1] = qk.rb[2] = d->wk.row_bytes;
+      qk.end[0] = qw;
+      qk.end[1] = qk.end[2] = qw + (int32_t)kvw;
+      qk.nseg = 2;
+      vs = rows::one_matrix(d->wv.data, d->wv.row_bytes, (int32_t)kvw);
+      mixed_qkv = htile_qkv_rope_fits(qk, d->width, tokens, d->head_dim, d->rope_dim) &&
+                  htile_qkv_rope_fits(vs, d->width, tokens, d->head_dim, d->rope_dim, MI_Q6_K);
+    }
     if (fused_qkv) {
       // q, k and v in one launch, straight into the fused row
       if ((rc = launch_q4k_rows_segs(s, sg, d->width, xq, qkv))) return rc;
+    } else if (mixed_qkv) {
+      // q|k with the rope and k's cache store on the Q4_K f16 tile, then v
+      // on the Q6_K one, every row of which the same epilogue stores into
+      // the v cache (as rows qw + kvw .. of a q|k|v launch: qw = -kvw)
+      QkvRope rp{};
+      rp.qw = qw;
+      rp.kvw = (int)kvw;
+      rp.head_dim = d->head_dim;
+      rp.rope_dim = d->rope_dim;
+      rp.pos = pos;
+      rp.k_cache = (__half*)k_cache;
+      rp.v_cache = (__half*)v_cache;
+      rp.kv_index = kv_index;
+      rp.steps = d->rope_steps;
+      rp.factors = d->rope_factors;
+      rp.cache_stride = cache_stride;
+      rp.index_stride = index_stride;
+      if ((rc = launch_htile_qkv_rope(s, qk, d->width, xq, hxn, tokens, qkv, qkv_stride, rp))) return rc;
+      QkvRope rv = rp;
+      rv.qw = -(int)kvw;
+      if ((rc = launch_htile_qkv_rope(s, vs, d->width, xq, hxn, tokens, qkv, qkv_stride, rv, MI_Q6_K))) return rc;
+      roped = true;
     } else if (tile_qkv) {
       // the same for a batch, on the matrix-core tile
       RowSegs tg{};

@@ -718,28 +718,35 @@ int launch_htile_split_norm(hipStream_t s, int kind, const void* w, int64_t row_
   return launch_split_add_norm(s, part, htile_nsplit(kind, cols), resid, gain, rows, tokens, eps, xq_out, hx_out);
 }
 
-bool htile_qkv_rope_fits(const RowSegs& sg, int32_t cols, int32_t tokens, int32_t head_dim, int32_t rope_dim) {
+bool htile_qkv_rope_fits(const RowSegs& sg, int32_t cols, int32_t tokens, int32_t head_dim, int32_t rope_dim,
+                         int kind) {
   const int rows = sg.end[sg.nseg - 1];
-  if (!htile_fits(MI_Q4_K, rows, cols, tokens) || head_dim % 2 || rope_dim % 2 || rope_dim > 2 * kMaxRopePairs)
+  const int sbb = kind == MI_Q6_K ? HGeo<MI_Q6_K>::SB : HGeo<MI_Q4_K>::SB;
+  if ((kind != MI_Q4_K && kind != MI_Q6_K) || !htile_fits(kind, rows, cols, tokens) || head_dim % 2 ||
+      rope_dim % 2 || rope_dim > 2 * kMaxRopePairs)
     return false;
   for (int i = 0; i < sg.nseg; i++)
-    if (sg.end[i] % 16 || sg.rb[i] != (int64_t)(cols / 256) * HGeo<MI_Q4_K>::SB || ((uintptr_t)sg.w[i] & 7))
-      return false;
+    if (sg.end[i] % 16 || sg.rb[i] != (int64_t)(cols / 256) * sbb || ((uintptr_t)sg.w[i] & 7)) return false;
   return true;
 }
 
 int launch_htile_qkv_rope(hipStream_t s, const RowSegs& sg, int32_t cols, const void* xq, const void* hx,
-                          int32_t tokens, float* q, int64_t ldq, const QkvRope& rp) {
-  if (!htile_qkv_rope_fits(sg, cols, tokens, rp.head_dim, rp.rope_dim))
+                          int32_t tokens, float* q, int64_t ldq, const QkvRope& rp, int kind) {
+  if (!htile_qkv_rope_fits(sg, cols, tokens, rp.head_dim, rp.rope_dim, kind))
     return fail(MI_ERR_SHAPE, "htile: no rope tile for %d columns at %d tokens", cols, tokens);
   const int rows = sg.end[sg.nseg - 1];
   const int waves = cols / (256 * kSBW);
   const int grid = std::min((rows + 15) / 16, cu_count());
 #define MI_HR(T)                                                                                              \
   case T:                                                                                                     \
-    hipLaunchKernelGGL((htile_kernel<T, MI_Q4_K, false, true>), dim3(grid), dim3(waves * 64), 0, s, sg, cols, \
-                       (const uint8_t*)xq, (const uint8_t*)hx, q, ldq, MI_EPI_NONE, nullptr, nullptr,         \
-                       cols / 32, 0, rp);                                                                     \
+    if (kind == MI_Q6_K)                                                                                      \
+      hipLaunchKernelGGL((htile_kernel<T, MI_Q6_K, false, true>), dim3(grid), dim3(waves * 64), 0, s, sg, cols, \
+                         (const uint8_t*)xq, (const uint8_t*)hx, q, ldq, MI_EPI_NONE, nullptr, nullptr,       \
+                         cols / 32, 0, rp);                                                                   \
+    else                                                                                                      \
+      hipLaunchKernelGGL((htile_kernel<T, MI_Q4_K, false, true>), dim3(grid), dim3(waves * 64), 0, s, sg, cols, \
+                         (const uint8_t*)xq, (const uint8_t*)hx, q, ldq, MI_EPI_NONE, nullptr, nullptr,       \
+                         cols / 32, 0, rp);                                                                   \
     break;
   switch (tokens) {
     MI_HR(2) MI_HR(3) MI_HR(4) MI_HR(5) MI_HR(6) MI_HR(7) MI_HR(8)

@@ -174,9 +174,11 @@ bool htile_fits(int kind, int32_t rows, int32_t cols, int32_t tokens);
 bool htile_split_fits(int kind, int32_t rows, int32_t cols, int32_t tokens);
 // q|k|v (whole 16-row segments) with the rope and the f16 cache store in the
 // epilogue, as launch_q4k_tile_qkv_rope.
-bool htile_qkv_rope_fits(const RowSegs& sg, int32_t cols, int32_t tokens, int32_t head_dim, int32_t rope_dim);
+// kind MI_Q6_K: a Q6_K segment (a Q4_K_M file's attn_v) in its own launch.
+bool htile_qkv_rope_fits(const RowSegs& sg, int32_t cols, int32_t tokens, int32_t head_dim, int32_t rope_dim,
+                         int kind = MI_Q4_K);
 int launch_htile_qkv_rope(hipStream_t s, const RowSegs& sg, int32_t cols, const void* xq, const void* hx,
-                          int32_t tokens, float* q, int64_t ldq, const QkvRope& rp);
+                          int32_t tokens, float* q, int64_t ldq, const QkvRope& rp, int kind = MI_Q4_K);
 size_t htile_split_bytes(int32_t rows, int32_t cols, int32_t tokens);
 int launch_htile_split(hipStream_t s, int kind, const void* w, int64_t row_bytes, int32_t rows, int32_t cols,
                        const void* xq, const void* hx, int32_t tokens, float* y, int64_t ldy, int32_t epi,

@@ -481,23 +481,27 @@ def test_layer_paged_matches_contiguous(form, dims, pos, tokens, kinds=None):
 def test_layer_paged_matches_contiguous_q4_k_m_kinds(tokens):
     """The same with a Q6_K attn_v and ffn_down: the batched q|k and v
     launches store k and v through the cell index too."""
-    test_layer_paged_matches_contiguous("f16", (512, 1024, 8, 2, 64), 300, tokens,
+    test_layer_paged_matches_contiguous("f16", (1024, 1024, 8, 2, 64), 300, tokens,
                                         {"wv": oracle.Q6_K, "down": oracle.Q6_K})
 
 
-@pytest.mark.parametrize("kinds,tokens", [
-    ({}, 1), ({}, 4), ({}, 8),
-    ({"wv": oracle.Q6_K, "down": oracle.Q6_K}, 1),
-    ({"wv": oracle.Q6_K, "down": oracle.Q6_K}, 3),
-    ({"wv": oracle.Q6_K, "down": oracle.Q6_K}, 4),
+@pytest.mark.parametrize("kinds,tokens,width", [
+    ({}, 1, 512), ({}, 4, 512), ({}, 8, 512),
+    ({"wv": oracle.Q6_K, "down": oracle.Q6_K}, 1, 512),
+    ({"wv": oracle.Q6_K, "down": oracle.Q6_K}, 3, 512),
+    ({"wv": oracle.Q6_K, "down": oracle.Q6_K}, 4, 512),
+    # width 1024 (Q6_K rows of four superblocks): the batched q|k and v
+    # launches of a Q6_K attn_v
+    ({"wv": oracle.Q6_K, "down": oracle.Q6_K}, 4, 1024),
+    ({"wv": oracle.Q6_K}, 8, 1024),
 ])
-def test_layer_ignores_prior_workspace_contents(kinds, tokens):
+def test_layer_ignores_prior_workspace_contents(kinds, tokens, width):
     """The layer reads nothing of its workspace it has not written in the
     same call: runs over workspaces filled with different bytes agree bit
     for bit."""
     from molla_amd import block, gpu
     ctx = gpu.DeviceContext(0)
-    spec = spec_of(512, 1024, 8, 2, 64)
+    spec = spec_of(width, 1024, 8, 2, 64)
     bs, layer = device_layer_from(make_layer_weights(spec, 11, kinds), spec)
     kvw, pos = bs.kv_width(), 300
     count = pos + 1
