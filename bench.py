@@ -539,48 +539,56 @@ def _cpu_baseline(w_dev, kind, rb, x_dev, model=None):
 
 
 def _stream_peak(stream, reps=200):
-    """The read ceiling measured on this box: a plain streaming read
-    (libmolla_probe.so probe_read) of a 33,030,144-byte buffer rotated over
-    2 GiB so every launch reads cold HBM, timed like the roofline (K
+    """The read ceiling measured on this box: plain streaming reads
+    (libmolla_probe.so probe_read, every loaded byte folded into the result)
+    of buffers the size of the decode step's matrices (wo 9.4 MB, q|k|v
+    14.2 MB, one 33 MB Q4_K matrix, gate+up 66 MB), each rotated over 2 GiB
+    so every launch reads cold HBM and timed like the roofline (K
     back-to-back launches between HIP events), and of a 1 GiB buffer; the
-    best over four grid sizes."""
+    best over two access shapes (grid-stride, contiguous chunk per wave with
+    8 or 16 loads in flight) and four grid sizes."""
     import ctypes
 
     import torch
 
     plib = ctypes.CDLL(os.path.join(ROOT, "molla_amd", "libmolla_probe.so"))
     plib.probe_read.restype = ctypes.c_int
-    plib.probe_read.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_void_p]
+    plib.probe_read.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_void_p,
+                                ctypes.c_int32]
     size = ROWS * (COLS // 256) * 144
-    slot = (size + 4095) // 4096 * 4096
-    n = (2 << 30) // slot
-    big = torch.empty(n * slot + (1 << 30), dtype=torch.uint8, device="cuda")
+    sizes = (("read_9MB", 9437184, reps), ("read_14MB", 14155776, reps), ("read_33MB", size, reps),
+             ("read_66MB", 2 * size, reps // 2), ("read_1GiB", 1 << 30, 10))
+    span = 2 << 30
+    big = torch.empty(span + (1 << 30), dtype=torch.uint8, device="cuda")
     big.view(torch.float32).zero_()
     sink = torch.zeros(1, device="cuda")
     h = stream.cuda_stream
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
 
-    def run(nbytes, count, blocks, rotate):
+    def run(nbytes, count, blocks, variant):
+        slot = (nbytes + 4095) // 4096 * 4096
+        n = max(1, span // slot) if nbytes < span else 1
         for i in range(count):
-            off = (i % n) * slot if rotate else 0
-            if plib.probe_read(h, big.data_ptr() + off, nbytes, blocks, sink.data_ptr()) != 0:
+            off = (i % n) * slot
+            if plib.probe_read(h, big.data_ptr() + off, nbytes, blocks, sink.data_ptr(), variant) != 0:
                 raise RuntimeError("probe_read launch failed")
 
     out = {}
-    for name, nbytes, count in (("read_33MB", size, reps), ("read_1GiB", 1 << 30, 10)):
+    for name, nbytes, count in sizes:
         best = None
-        for blocks in (1024, 2048, 4096, 8192):
-            run(nbytes, 5, blocks, name == "read_33MB")
-            torch.cuda.synchronize()
-            e0.record(stream)
-            run(nbytes, count, blocks, name == "read_33MB")
-            e1.record(stream)
-            torch.cuda.synchronize()
-            us = e0.elapsed_time(e1) * 1e3 / count
-            if best is None or us < best[0]:
-                best = (us, blocks)
+        for variant in (0, 1, 2):
+            for blocks in (1024, 2048, 4096, 8192):
+                run(nbytes, 5, blocks, variant)
+                torch.cuda.synchronize()
+                e0.record(stream)
+                run(nbytes, count, blocks, variant)
+                e1.record(stream)
+                torch.cuda.synchronize()
+                us = e0.elapsed_time(e1) * 1e3 / count
+                if best is None or us < best[0]:
+                    best = (us, blocks, variant)
         out[name] = {"bytes": nbytes, "us": round(best[0], 3), "GB_s": round(nbytes / best[0] / 1e3, 1),
-                     "blocks": best[1]}
+                     "blocks": best[1], "shape": ("grid-stride", "chunk x8", "chunk x16")[best[2]]}
     del big
     torch.cuda.empty_cache()
     return out

@@ -173,7 +173,9 @@ __global__ __launch_bounds__(256) void q6k_rows_kernel(const uint8_t* __restrict
       // part alternates between two buffers: a row's buffer is written
       // again two rows later, after every wave has passed the next row's
       // barrier, which wave 0 reaches only once it has read this one
-      if (lane == 0) part[it & 1][ks] = v;
+      // a block always holds four waves; with KS < 4 the spare ones own no
+      // units and must not write (their slot would be the other buffer's)
+      if (lane == 0 && ks < KS) part[it & 1][ks] = v;
       __syncthreads();
       if (ks == 0 && lane == 0) {
         float t = part[it & 1][0];

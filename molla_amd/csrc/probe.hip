@@ -1,34 +1,83 @@
 // probe.hip -- measurement helper for bench.py, not part of the decode path:
-// a plain streaming read, so the bench line can report the read ceiling it
+// plain streaming reads, so the bench line can report the read ceiling it
 // measured on the same box next to the matvec's roofline fraction.
 //
-// probe_read: every thread of `blocks` x 256 reads float4s of the buffer
-// in a grid-stride loop, four loads in flight per step, and folds them into
-// a sum that is stored only if it hits an impossible value (so the loads
-// are not dropped).  Built as its own library, libmolla_probe.so.
+// Every byte that is loaded is folded into the result (xor of all four
+// dwords of every 16-byte load), and the result is stored only if it hits a
+// value no input here produces, so the compiler can neither drop a load nor
+// narrow a 16-byte load to the part it uses.
+//
+// Two access shapes, both 16 bytes a lane per load:
+//   variant 0, grid-stride: thread i reads vectors i, i + S, i + 2S, ...
+//     (S = all threads of the grid), four loads in flight per step;
+//   variant 1, chunks: wave w reads one contiguous run of the buffer,
+//     `unroll` loads of 1 KB each in flight (the matvec's shape: a wave's
+//     loads issued straight-line before any is consumed).
+// Built as its own library, libmolla_probe.so.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
 namespace {
 
-__global__ __launch_bounds__(256) void read_kernel(const float4* __restrict__ p, int64_t n4,
-                                                   float* __restrict__ sink) {
+__device__ __forceinline__ uint32_t fold(const uint4& v) { return v.x ^ v.y ^ v.z ^ v.w; }
+
+__global__ __launch_bounds__(256) void read_stride_kernel(const uint4* __restrict__ p, int64_t n16,
+                                                          uint32_t* __restrict__ sink) {
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  float a = 0.0f;
-  for (; i + 3 * stride < n4; i += 4 * stride) {
-    const float4 v0 = p[i], v1 = p[i + stride], v2 = p[i + 2 * stride], v3 = p[i + 3 * stride];
-    a += (v0.x + v1.y) + (v2.z + v3.w);
+  uint32_t a = 0;
+  for (; i + 3 * stride < n16; i += 4 * stride) {
+    const uint4 v0 = p[i], v1 = p[i + stride], v2 = p[i + 2 * stride], v3 = p[i + 3 * stride];
+    a ^= fold(v0) ^ fold(v1) ^ fold(v2) ^ fold(v3);
   }
-  for (; i < n4; i += stride) a += p[i].x;
-  if (a == -1.2345e-30f) sink[0] = a;
+  for (; i < n16; i += stride) a ^= fold(p[i]);
+  if (a == 0x9E3779B9u) sink[0] = a;
+}
+
+// Wave w of the grid owns vectors [w * per, (w + 1) * per) (per a multiple of
+// 64 * U); it walks them U loads of 64 lanes at a time.
+template <int U>
+__global__ __launch_bounds__(256) void read_chunk_kernel(const uint4* __restrict__ p, int64_t n16, int64_t per,
+                                                         uint32_t* __restrict__ sink) {
+  const int lane = threadIdx.x & 63;
+  const int64_t wave = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+  const int64_t beg = wave * per, end = beg + per < n16 ? beg + per : n16;
+  uint32_t a = 0;
+  for (int64_t i = beg + lane; i < end; i += 64 * U) {
+    uint4 v[U];
+#pragma unroll
+    for (int k = 0; k < U; k++) {
+      const int64_t j = i + 64 * k;
+      v[k] = j < end ? p[j] : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int k = 0; k < U; k++) a ^= fold(v[k]);
+  }
+  if (a == 0x9E3779B9u) sink[0] = a;
 }
 
 }  // namespace
 
-extern "C" int probe_read(void* stream, const void* p, int64_t bytes, int32_t blocks, float* sink) {
-  if (!p || bytes < 16 || blocks <= 0 || ((uintptr_t)p & 15)) return -1;
-  hipLaunchKernelGGL(read_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream, (const float4*)p, bytes / 16,
-                     sink);
+// variant 0: grid-stride with `blocks` x 256 threads; variant 1: chunks, each
+// of the `blocks` x 4 waves reading one contiguous share, 8 loads a lane in
+// flight; variant 2: the same with 16.
+extern "C" int probe_read(void* stream, const void* p, int64_t bytes, int32_t blocks, void* sink, int32_t variant) {
+  if (!p || bytes < 16 || blocks <= 0 || ((uintptr_t)p & 15) || variant < 0 || variant > 2) return -1;
+  const int64_t n16 = bytes / 16;
+  hipStream_t s = (hipStream_t)stream;
+  if (variant == 0) {
+    hipLaunchKernelGGL(read_stride_kernel, dim3(blocks), dim3(256), 0, s, (const uint4*)p, n16, (uint32_t*)sink);
+  } else {
+    const int U = variant == 1 ? 8 : 16;
+    const int64_t waves = (int64_t)blocks * 4;
+    int64_t per = (n16 + waves - 1) / waves;
+    per = (per + 64 * U - 1) / (64 * U) * (64 * U);
+    if (U == 8)
+      hipLaunchKernelGGL(read_chunk_kernel<8>, dim3(blocks), dim3(256), 0, s, (const uint4*)p, n16, per,
+                         (uint32_t*)sink);
+    else
+      hipLaunchKernelGGL(read_chunk_kernel<16>, dim3(blocks), dim3(256), 0, s, (const uint4*)p, n16, per,
+                         (uint32_t*)sink);
+  }
   return hipGetLastError() == hipSuccess ? 0 : -2;
 }

@@ -201,6 +201,11 @@ def test_matmul_tokens_epilogues(ctx, kind, tokens):
     (oracle.Q6_K, 4096, 14336, 8),
     (oracle.Q6_K, 333, 12288, 1),
     (oracle.Q6_K, 70, 5120, 1),
+    # more rows than blocks (1024), so a block takes several rows in turn
+    # with two and three waves a row
+    (oracle.Q6_K, 2048, 5120, 1),
+    (oracle.Q6_K, 2048, 8192, 1),
+    (oracle.Q6_K, 4096, 11008, 1),
     # Q6_K rows of 2 and 6 superblocks at a batch: not whole 8-byte words,
     # so not the f16 tile
     (oracle.Q6_K, 200, 512, 4),
