@@ -788,52 +788,55 @@ __global__ __launch_bounds__(256) void store_kv_q8_kernel(const float* __restric
 }
 
 // One block per (query head, token); thread d owns output dimension d (the
-// block has max(64, head_dim) threads).  Thread d issues its loads of up to
-// 32 slices' partial values before anything else, so they overlap the
-// (max, sum) staging: the merge costs one memory latency per 32 slices.
-// Every wave reduces the (max, sum) pairs identically; the weights
-// exp(m_c - M) are computed once per slice into LDS (zero past the last
-// slice) and the values are folded in slice order.
+// block has max(64, head_dim) threads).  The first 64 slices' partial values
+// and (max, sum) pairs are loaded before the position is known (slots past
+// the live slices are read and then ignored), so the merge costs one memory
+// latency, not a position load followed by one.  Each wave holds slice c's
+// (max, sum) in lane c, derives the weights exp(m_c - M) there, and every
+// thread takes the weights lane by lane (readlane) while it folds the values
+// in slice order: no LDS and no barrier.  Slices past the first 64 come in
+// further rounds of 64.
 constexpr int kMergeBatch = 64;
 __global__ void attend_merge_kernel(const float* __restrict__ part_acc, const float* __restrict__ part_ml,
                                     int heads, int head_dim, const int32_t* __restrict__ pos_dev,
                                     int count_host, int max_chunks, float* __restrict__ out,
                                     uint8_t* __restrict__ xq, uint8_t* __restrict__ hx) {
-  extern __shared__ float mls[];  // [max_chunks][2], then the weights [ceil32(max_chunks)]
   const int h = blockIdx.x, t = blockIdx.y;
-  const int count = pos_dev ? pos_dev[t] + 1 : count_host;  // a position p attends over p + 1 slots
-  const int kk = attn_slice(head_dim);
-  const int chunks = (count + kk - 1) / kk;
-  const int padded = (chunks + kMergeBatch - 1) / kMergeBatch * kMergeBatch;
-  float* wts = mls + 2 * max_chunks;
   const int64_t slot = ((int64_t)t * heads + h) * max_chunks;
-  const int d = threadIdx.x;
+  const int d = threadIdx.x, lane = d & 63;
   const bool live = d < head_dim;
   const float* pa = part_acc + slot * head_dim + min(d, head_dim - 1);
+  const float2* pml = (const float2*)part_ml + slot;
   float a[kMergeBatch];
 #pragma unroll
-  for (int k = 0; k < kMergeBatch; k++) a[k] = pa[(int64_t)min(k, chunks - 1) * head_dim];
-  for (int c = threadIdx.x; c < chunks; c += blockDim.x)
-    *(float2*)(mls + 2 * c) = *(const float2*)(part_ml + (slot + c) * 2);
-  __syncthreads();
-  const int lane = threadIdx.x & 63;
-  float M = -INFINITY;
-  for (int c = lane; c < chunks; c += kWave) M = fmaxf(M, mls[2 * c]);
+  for (int k = 0; k < kMergeBatch; k++) a[k] = pa[(int64_t)min(k, max_chunks - 1) * head_dim];
+  float2 ml = pml[min(lane, max_chunks - 1)];
+  const int count = pos_dev ? pos_dev[t] + 1 : count_host;  // a position p attends over p + 1 slots
+  const int kk = attn_slice(head_dim);
+  const int chunks = min((count + kk - 1) / kk, max_chunks);
+  // the largest slice max over every round
+  float M = lane < chunks ? ml.x : -INFINITY;
+  for (int c0 = kMergeBatch; c0 < chunks; c0 += kMergeBatch) {
+    const int c = c0 + lane;
+    if (c < chunks) M = fmaxf(M, pml[c].x);
+  }
   M = lanes::reduce<64>(M, lanes::Max{});
-  for (int c = threadIdx.x; c < padded; c += blockDim.x) wts[c] = c < chunks ? expf(mls[2 * c] - M) : 0.0f;
-  __syncthreads();
-  float L = 0.0f;
-  for (int c = lane; c < chunks; c += kWave) L += mls[2 * c + 1] * wts[c];
-  L = lanes::reduce<64>(L, lanes::Add{});
-  float o = 0.0f;
+  float o = 0.0f, L = 0.0f;
   for (int c0 = 0; c0 < chunks; c0 += kMergeBatch) {
     if (c0 > 0) {
 #pragma unroll
       for (int k = 0; k < kMergeBatch; k++) a[k] = pa[(int64_t)min(c0 + k, chunks - 1) * head_dim];
+      ml = pml[min(c0 + lane, chunks - 1)];
     }
+    const int n = min(chunks - c0, kMergeBatch);
+    const float w = lane < n ? expf(ml.x - M) : 0.0f;
+    L += lane < n ? ml.y * w : 0.0f;
 #pragma unroll
-    for (int k = 0; k < kMergeBatch; k++) o = fmaf(a[k], wts[c0 + k], o);
+    for (int k = 0; k < kMergeBatch; k++) {
+      if (k < n) o = fmaf(a[k], __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), k)), o);
+    }
   }
+  L = lanes::reduce<64>(L, lanes::Add{});
   o *= 1.0f / L;
   const int width = heads * head_dim;
   if (live && out) out[(int64_t)t * width + (int64_t)h * head_dim + d] = o;
@@ -1374,8 +1377,6 @@ int launch_attend(hipStream_t s, const float* q, int64_t q_stride, const uint16_
   const size_t acc_bytes = ((size_t)slots * head_dim * sizeof(float) + 255) & ~(size_t)255;
   float* part_ml = (float*)((char*)work + acc_bytes);
   const int group = heads / kv_heads;
-  const size_t merge_lds =
-      ((size_t)chunks * 2 + (chunks + kMergeBatch - 1) / kMergeBatch * kMergeBatch) * sizeof(float);
   // decode (at most 8 tokens, one each per sequence, f16 cache): the
   // 1024-thread slice kernel
   if (tokens <= kMaxTokens && (head_dim == 64 || head_dim == 128) &&
@@ -1412,7 +1413,7 @@ int launch_attend(hipStream_t s, const float* q, int64_t q_stride, const uint16_
 #undef MI_WIDE
     int rc = hip_check(hipGetLastError(), "attend_wide launch");
     if (rc) return rc;
-    hipLaunchKernelGGL(attend_merge_kernel, dim3(heads, tokens), dim3(head_dim < 64 ? 64 : head_dim), merge_lds, s,
+    hipLaunchKernelGGL(attend_merge_kernel, dim3(heads, tokens), dim3(head_dim < 64 ? 64 : head_dim), 0, s,
                        part_acc, part_ml, heads, head_dim, pos_dev, count_host, chunks, out, (uint8_t*)xq_out,
                        (uint8_t*)hx_out);
     return hip_check(hipGetLastError(), "attend_merge launch");
@@ -1449,8 +1450,7 @@ int launch_attend(hipStream_t s, const float* q, int64_t q_stride, const uint16_
 #undef MI_CHUNK
     int rc = hip_check(hipGetLastError(), "attend_chunk launch");
     if (rc) return rc;
-    const size_t mlds = ((size_t)chunks * 2 + (chunks + kMergeBatch - 1) / kMergeBatch * kMergeBatch) * sizeof(float);
-    hipLaunchKernelGGL(attend_merge_kernel, dim3(heads, tokens), dim3(head_dim < 64 ? 64 : head_dim), mlds, s,
+    hipLaunchKernelGGL(attend_merge_kernel, dim3(heads, tokens), dim3(head_dim < 64 ? 64 : head_dim), 0, s,
                        part_acc, part_ml, heads, head_dim, pos_dev, count_host, chunks, out, (uint8_t*)xq_out,
                        (uint8_t*)hx_out);
     return hip_check(hipGetLastError(), "attend_merge launch");
@@ -1481,7 +1481,7 @@ int launch_attend(hipStream_t s, const float* q, int64_t q_stride, const uint16_
 #undef MI_ATTEND
   int rc = hip_check(hipGetLastError(), "attend_split launch");
   if (rc) return rc;
-  hipLaunchKernelGGL(attend_merge_kernel, dim3(heads, tokens), dim3(head_dim < 64 ? 64 : head_dim), merge_lds, s,
+  hipLaunchKernelGGL(attend_merge_kernel, dim3(heads, tokens), dim3(head_dim < 64 ? 64 : head_dim), 0, s,
                      part_acc, part_ml, heads, head_dim, pos_dev,
                      count_host, chunks, out, (uint8_t*)xq_out, (uint8_t*)hx_out);
   return hip_check(hipGetLastError(), "attend_merge launch");
