@@ -136,6 +136,15 @@ __global__ __launch_bounds__(GQ ? 32 / RPW * 64 : KS * 64) void rows_kernel(
   constexpr bool kL23 = KIND == MI_Q4_0 || KIND == MI_Q5_0;  // kinds with a fixed offset
   XUnitRegs<kL23> xr;
   typename UnitOf<KIND, 1>::type un[NR];
+  // the epilogue's operand (plain rows): loaded first, so the store at the
+  // end waits for nothing queued behind the weights
+  // (branch-free: a load under a branch makes the compiler wait for every
+  // load in flight at the join)
+  float pre = 0.0f;
+  if constexpr (!GLU && !ROPE) {
+    const float* src = (epi & (MI_EPI_BIAS | MI_EPI_GLU)) ? aux : y;
+    pre = src[min(row0 + (lane & (RPW - 1)), rows - 1)];
+  }
   load_x(xr, XAcc{xq, 4 * (int64_t)cols, (int64_t)(cols >> 5) * 16}, u);
 #pragma unroll
   for (int r = 0; r < NR; r++) {
@@ -204,7 +213,7 @@ __global__ __launch_bounds__(GQ ? 32 / RPW * 64 : KS * 64) void rows_kernel(
       if (wib == 0) quantize_group32(grp[lane & 31], lane & 31, blockIdx.x, rows >> 5, xq_out, lane < 32);
     }
   } else {
-    if (lane < RPW && row0 + lane < rows) epilogue(y, aux, epi, row0 + lane, row0 + lane, v);
+    if (lane < RPW && row0 + lane < rows) epilogue_with(y, epi, row0 + lane, pre, v);
   }
 }
 

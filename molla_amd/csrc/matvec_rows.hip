@@ -25,13 +25,14 @@ using namespace mv;
 // launch
 // and is computed once per CU, not once per group.  After each group, wave 0
 // writes its act(gate) * up in matvec form for the down projection.
+constexpr int kGluIts = 8;  // groups a block of glu_norm_kernel takes at most (one per wave)
 template <int PRE>
 __global__ __launch_bounds__(8 * 64) void glu_norm_kernel(const RowSegs sg, int cols, float* __restrict__ y,
                                                           int epi, const NormIn nm, uint8_t* __restrict__ xq_out) {
   constexpr int RPW = 4, NR = 2 * RPW, kNT = 8 * 64;
   __shared__ __align__(16) uint8_t xs[4 * 4096];
   __shared__ double red[kNT / 64];
-  __shared__ float grp[2][32];
+  __shared__ float grp[kGluIts][32];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const int rows = sg.end[0];
@@ -65,15 +66,15 @@ __global__ __launch_bounds__(8 * 64) void glu_norm_kernel(const RowSegs sg, int 
     const int row = (g * 8 + wave) * RPW + r % RPW;
     un[r].load(sg.w[r / RPW] + (int64_t)row * sg.rb[r / RPW], 0, 0, 0, u);
   }
-  for (int it = 0;; it++) {
-    float acc[NR];
-#pragma unroll
-    for (int r = 0; r < NR; r++) {
-      float a[1][1] = {{0.0f}};
-      un[r].template compute<1>(xr, u, a);
-      acc[r] = act ? a[0][0] : 0.0f;
-      __builtin_amdgcn_sched_barrier(0);
-    }
+  // No barrier inside the loop: each wave sends for its next group's weights
+  // as soon as it has used this group's, and leaves its act(gate) * up in
+  // LDS; the quantize of every group (wave k takes the block's k-th group)
+  // waits for one barrier after the last group.  A barrier per group held
+  // every wave of the block, and the next group's loads, until the slowest
+  // wave's weights had arrived.  The launcher keeps a block to at most
+  // kGluIts groups.
+  // this group's sums, store and act(gate) * up into LDS
+  auto finish = [&](float (&acc)[NR], int it) __attribute__((always_inline)) {
 #pragma unroll
     for (int r = 0; r < NR; r++) acc[r] = wave_sum(acc[r]);
     float v = acc[0];
@@ -86,20 +87,38 @@ __global__ __launch_bounds__(8 * 64) void glu_norm_kernel(const RowSegs sg, int 
     if (lane < RPW) {
       if (epi & MI_EPI_ADD) y[row0 + lane] += o;
       else y[row0 + lane] = o;
-      grp[it & 1][wave * RPW + lane] = o;
+      grp[it][wave * RPW + lane] = o;
     }
-    // grp alternates between two buffers: a group's buffer is written again
-    // two groups later, after every wave has passed the next group's barrier,
-    // which wave 0 reaches only once it has read this one.
-    __syncthreads();
-    if (wave == 0) quantize_group32(grp[it & 1][lane & 31], lane & 31, g, groups, xq_out, lane < 32);
-    g += gridDim.x;
-    if (g >= groups) break;
+  };
+  int it = 0;
+  for (;; it++) {
+    float acc[NR];
 #pragma unroll
     for (int r = 0; r < NR; r++) {
-      const int row = (g * 8 + wave) * RPW + r % RPW;
+      float a[1][1] = {{0.0f}};
+      un[r].template compute<1>(xr, u, a);
+      acc[r] = act ? a[0][0] : 0.0f;
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    const int gn = g + gridDim.x;
+    // the exit and the next loads on one branch: with the loads under a
+    // branch of their own, the old weights stayed live across it (spills)
+    if (gn >= groups) {
+      finish(acc, it);
+      break;
+    }
+#pragma unroll
+    for (int r = 0; r < NR; r++) {
+      const int row = (gn * 8 + wave) * RPW + r % RPW;
       un[r].load(sg.w[r / RPW] + (int64_t)row * sg.rb[r / RPW], 0, 0, 0, u);
     }
+    finish(acc, it);
+    g = gn;
+  }
+  __syncthreads();
+  if (wave <= it) {
+    const int gq = blockIdx.x + wave * gridDim.x;
+    quantize_group32(grp[wave][lane & 31], lane & 31, gq, groups, xq_out, lane < 32);
   }
 }
 
@@ -318,7 +337,9 @@ int launch_q4k_glu_norm(hipStream_t s, const void* gate, const void* up, int64_t
   sg.rb[0] = sg.rb[1] = sg.rb[2] = row_bytes;
   sg.end[0] = sg.end[1] = sg.end[2] = rows;
   sg.nseg = 2;
-  hipLaunchKernelGGL(glu_norm_kernel<4>, dim3(std::min(rows / 32, cu_count())), dim3(8 * 64), 0, s, sg, cols, y,
+  const int groups = rows / 32;
+  const int grid = std::max(std::min(groups, cu_count()), (groups + kGluIts - 1) / kGluIts);
+  hipLaunchKernelGGL(glu_norm_kernel<4>, dim3(grid), dim3(8 * 64), 0, s, sg, cols, y,
                      MI_EPI_NONE, NormIn{x, gain, eps}, (uint8_t*)xq_out);
   return hip_check(hipGetLastError(), "matvec launch");
 }

@@ -642,5 +642,15 @@ __device__ __forceinline__ void epilogue(float* __restrict__ y, const float* __r
   else y[at] = v;
 }
 
+// The same epilogue with its one memory operand (y for ADD, aux for BIAS or
+// GLU) loaded ahead by the caller (pre = aux[at] or y[at]), so the store does
+// not wait for a load issued behind the weights.
+__device__ __forceinline__ void epilogue_with(float* __restrict__ y, int epi, int64_t at, float pre, float v) {
+  if (epi & MI_EPI_BIAS) v += pre;
+  else if (epi & MI_EPI_GLU) v = ((epi & MI_ACT_GELU) ? gelu(v) : silu(v)) * pre;
+  if (epi & MI_EPI_ADD) y[at] = (epi & (MI_EPI_BIAS | MI_EPI_GLU)) ? y[at] + v : pre + v;
+  else y[at] = v;
+}
+
 }  // namespace mv
 }  // namespace mi
