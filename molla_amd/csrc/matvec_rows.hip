@@ -183,6 +183,21 @@ __global__ __launch_bounds__((Q8 ? 16 : 12) * 64) void qkv_norm_kernel(const Row
 #pragma unroll
   for (int r = 0; r < PRE; r++) un[r].load(rows::seg_row(sg, min(pr.row0 + r, rows - 1)), 0, 0, 0, u);
   __builtin_amdgcn_sched_barrier(0);
+  // rope_theta's arithmetic on the step and factor (scalar loads): done
+  // while the row's loads are in flight, not after the norm
+  float c = 1.0f, sn = 0.0f;
+  auto angle = [&]() __attribute__((always_inline)) {
+    c = 1.0f;
+    sn = 0.0f;
+    if (pr.rot) {
+      float theta = (float)pos * step;
+      if (rp.factors) theta = theta / factor;
+      c = (float)cos((double)theta);
+      sn = (float)sin((double)theta);
+    }
+  };
+  angle();
+  __builtin_amdgcn_sched_barrier(0);
   norm_row_to_lds<kNT>(nr, cols, nm.eps, xs, red);
   rows::load_x(xr, XLds{xs, 0, (cols >> 5) * 16}, u);
   __builtin_amdgcn_sched_barrier(0);
@@ -195,14 +210,7 @@ __global__ __launch_bounds__((Q8 ? 16 : 12) * 64) void qkv_norm_kernel(const Row
   // wave has passed the next group's barrier, which wave 0 reaches once it
   // has read the buffer
   for (int it = 0;; it++) {
-    // rope_theta's arithmetic on the preloaded step and factor
-    float c = 1.0f, sn = 0.0f;
-    if (pr.rot) {
-      float theta = (float)pos * step;
-      if (rp.factors) theta = theta / factor;
-      c = (float)cos((double)theta);
-      sn = (float)sin((double)theta);
-    }
+    if (it > 0) angle();
     float acc[RPW];
 #pragma unroll
     for (int r = 0; r < RPW; r++) {
