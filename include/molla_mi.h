@@ -199,6 +199,18 @@ int mi_attend_form(mi_stream stream, int32_t form, const float* q, const uint16_
  * index (kernel.mojo:571 argmax, gpu_ops.mojo:408). out: device int32[tokens]. */
 int mi_argmax(mi_stream stream, const float* x, int32_t n, int32_t tokens, int32_t* out);
 
+/* The same argmax spread over the chip: each row in 64 parts, the parts'
+ * winners left in `work` (mi_argmax_workspace(n, tokens) bytes, 8-byte
+ * aligned) and folded in part order, ties to the lower index as above.
+ * The single-block form (the reference's, gpu_ops.mojo:408) is bound by one
+ * compute unit's bandwidth on a vocabulary-sized row.  Optionally the
+ * decode loop's bookkeeping in the same launch (engine/device.mojo:917 pick
+ * and the advance after it): next_ids[t] = out[t] and next_pos[t] += 1 when
+ * those pointers are not NULL. */
+size_t mi_argmax_workspace(int32_t n, int32_t tokens);
+int mi_argmax_ws(mi_stream stream, const float* x, int32_t n, int32_t tokens, int32_t* out, void* work,
+                 size_t work_bytes, int32_t* next_ids, int32_t* next_pos);
+
 /* out[t] = row ids[t] of an f32 embedding (model.mojo:102 embed). */
 int mi_embed(mi_stream stream, const float* embedding, int32_t vocab, int32_t width,
              const int32_t* ids, int32_t tokens, float* out);

@@ -224,11 +224,14 @@ class DeviceSession:
         need = max(layer_workspace(l, context, batch) for l in model.layers)
         need = max(need, lib().mi_matvec_workspace(s.width, batch))
         self.work = torch.empty(need + 256, dtype=torch.uint8, device=dev)
+        self.amax_work = torch.empty(lib().mi_argmax_workspace(model.vocab, batch), dtype=torch.uint8, device=dev)
 
-    def step(self) -> None:
+    def step(self, advance: bool = False) -> None:
         """One token for every sequence: embed ids, every layer at pos, final
         norm, head, argmax into picks (engine/device.mojo:859 step + :917 pick).
-        Queued, not synchronized; reads ids and pos from device memory."""
+        advance=True also does advance()'s ids <- picks, pos += 1 inside the
+        argmax launch.  Queued, not synchronized; reads ids and pos from
+        device memory."""
         m, s, c = self.model, self.model.spec, self.ctx
         L = lib()
         check(L.mi_embed(c.handle, m.embedding.data_ptr(), m.embedding.shape[0], s.width, self.ids.data_ptr(),
@@ -242,7 +245,12 @@ class DeviceSession:
                             None, xq))
         check(L.mi_matvec_xq(c.handle, m.output.kind, m.output.address, m.output.row_bytes(), m.output.rows,
                              m.output.cols, xq, self.batch, self.logits.data_ptr(), gpu.EPI_NONE, None))
-        check(L.mi_argmax(c.handle, self.logits.data_ptr(), m.vocab, self.batch, self.picks.data_ptr()))
+        self._pick(self.ids.data_ptr() if advance else None, self.pos.data_ptr() if advance else None)
+
+    def _pick(self, next_ids, next_pos) -> None:
+        check(lib().mi_argmax_ws(self.ctx.handle, self.logits.data_ptr(), self.model.vocab, self.batch,
+                                 self.picks.data_ptr(), self.amax_work.data_ptr(), self.amax_work.numel(),
+                                 next_ids, next_pos))
 
     def prefill(self, ids: torch.Tensor, seq: int = 0, start: int = 0, chunk: int = 256) -> None:
         """Feed a prompt to sequence `seq` from position `start` in chunks of
@@ -293,7 +301,7 @@ class DeviceSession:
                             None, xq))
         check(L.mi_matvec_xq(c.handle, m.output.kind, m.output.address, m.output.row_bytes(), m.output.rows,
                              m.output.cols, xq, self.batch, self.logits.data_ptr(), gpu.EPI_NONE, None))
-        check(L.mi_argmax(c.handle, self.logits.data_ptr(), m.vocab, self.batch, self.picks.data_ptr()))
+        self._pick(None, None)
 
     def advance(self) -> None:
         """Greedy decode bookkeeping on the device: next ids = picks, pos += 1."""
@@ -314,9 +322,9 @@ class DeviceSession:
             raise RuntimeError("capture: the session's DeviceContext needs its own stream")
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g, stream=self.ctx.stream):
-            self.step()
             if advance:
-                self.advance()
+                self.step(advance=True)
             else:
+                self.step()
                 self.pos.add_(1)
         return g

@@ -251,6 +251,9 @@ int launch_attend(hipStream_t s, const float* q, int64_t q_stride, const uint16_
                   int32_t form = MI_CACHE_F16, const int32_t* kv_index = nullptr, int64_t index_stride = 0,
                   void* hx_out = nullptr);
 int launch_argmax(hipStream_t s, const float* x, int32_t n, int32_t tokens, int32_t* out);
+size_t argmax_workspace(int32_t n, int32_t tokens);
+int launch_argmax_ws(hipStream_t s, const float* x, int32_t n, int32_t tokens, int32_t* out, void* work,
+                     int32_t* next_ids, int32_t* next_pos);
 // The optional layer parts (ops.hip): per-head RMS norm of `heads` runs of n
 // in each of `tokens` rows row_stride apart, in place; resid[t] +=
 // rms_norm(y[t]) * gain; x = act(x) (silu, or gelu with MI_ACT_GELU).

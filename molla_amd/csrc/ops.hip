@@ -1248,6 +1248,92 @@ __global__ __launch_bounds__(1024) void argmax4_kernel(const float* __restrict__
   argmax_finish(bv, bi, n, out + t);
 }
 
+// Multi-block form (mi_argmax_ws): a row of n is cut into kArgParts chunks
+// of whole float4s, one 256-thread block each, every thread issuing all of
+// its loads before comparing; each block leaves its (value, index) in the
+// workspace and argmax_pick_kernel folds the parts of a row in part order
+// with the same tie rule.  One block streaming a 128256-logit row was bound
+// by a single CU's bandwidth (about 16 us); the parts spread it over the chip.
+constexpr int kArgParts = 64, kArgThreads = 256, kArgPer = 4;
+__global__ __launch_bounds__(kArgThreads) void argmax_part_kernel(const float* __restrict__ x, int n, int chunk4,
+                                                                  float2* __restrict__ part) {
+  const int b = blockIdx.x, t = blockIdx.y;
+  const float* xr = x + (int64_t)t * n;
+  const int n4 = n >> 2, j0 = b * chunk4, j1 = min(j0 + chunk4, n4);
+  float bv = -INFINITY;
+  int bi = n;
+  const bool vec = ((n & 3) == 0) && (((uintptr_t)xr & 15) == 0);
+  if (vec) {
+    const float4* xr4 = (const float4*)xr;
+    for (int j = j0 + threadIdx.x; j < j1; j += kArgThreads * kArgPer) {
+      float4 v[kArgPer];
+#pragma unroll
+      for (int k = 0; k < kArgPer; k++) {
+        const int jj = j + k * kArgThreads;
+        v[k] = jj < j1 ? xr4[jj] : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+      }
+#pragma unroll
+      for (int k = 0; k < kArgPer; k++) {
+        const int i = 4 * (j + k * kArgThreads);
+        if (j + k * kArgThreads < j1) {
+          better(bv, bi, v[k].x, i);
+          better(bv, bi, v[k].y, i + 1);
+          better(bv, bi, v[k].z, i + 2);
+          better(bv, bi, v[k].w, i + 3);
+        }
+      }
+    }
+  } else {
+    // scalar chunks of 4 * chunk4 values (the last part also takes the tail)
+    const int i1 = b == (int)gridDim.x - 1 ? n : min(4 * j1, n);
+    for (int i = 4 * j0 + threadIdx.x; i < i1; i += kArgThreads) better(bv, bi, xr[i], i);
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    const float ov = __shfl_xor(bv, o);
+    const int oi = __shfl_xor(bi, o);
+    better(bv, bi, ov, oi);
+  }
+  __shared__ float sv[kArgThreads / 64];
+  __shared__ int si[kArgThreads / 64];
+  if ((threadIdx.x & 63) == 0) {
+    sv[threadIdx.x >> 6] = bv;
+    si[threadIdx.x >> 6] = bi;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < kArgThreads / 64; w++) better(bv, bi, sv[w], si[w]);
+    part[(int64_t)t * gridDim.x + b] = make_float2(bv, __int_as_float(bi));
+  }
+}
+
+// One wave per row: lane b holds part b; the winner goes to out[t], and
+// optionally to next_ids[t] with next_pos[t] += 1 (the decode loop's
+// bookkeeping, so it costs no launches of its own).
+__global__ __launch_bounds__(64) void argmax_pick_kernel(const float2* __restrict__ part, int parts, int n,
+                                                         int32_t* __restrict__ out, int32_t* __restrict__ next_ids,
+                                                         int32_t* __restrict__ next_pos) {
+  const int t = blockIdx.x, lane = threadIdx.x;
+  float bv = -INFINITY;
+  int bi = n;
+  for (int b = lane; b < parts; b += 64) {
+    const float2 p = part[(int64_t)t * parts + b];
+    better(bv, bi, p.x, __float_as_int(p.y));
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    const float ov = __shfl_xor(bv, o);
+    const int oi = __shfl_xor(bi, o);
+    better(bv, bi, ov, oi);
+  }
+  if (lane == 0) {
+    const int pick = bi < n ? bi : 0;
+    out[t] = pick;
+    if (next_ids) next_ids[t] = pick;
+    if (next_pos) next_pos[t] += 1;
+  }
+}
+
 // ---- embedding -------------------------------------------------------------
 // model.mojo:102 embed for an f32 table: one row copy per token.
 __global__ void embed_kernel(const float* __restrict__ emb, int vocab, int width,
@@ -1500,6 +1586,24 @@ int launch_argmax(hipStream_t s, const float* x, int32_t n, int32_t tokens, int3
     return hip_check(hipGetLastError(), "argmax launch");
   }
   hipLaunchKernelGGL(argmax_kernel, dim3(tokens), dim3(1024), 0, s, x, n, out);
+  return hip_check(hipGetLastError(), "argmax launch");
+}
+
+size_t argmax_workspace(int32_t n, int32_t tokens) {
+  (void)n;
+  return (size_t)tokens * kArgParts * sizeof(float2);
+}
+
+int launch_argmax_ws(hipStream_t s, const float* x, int32_t n, int32_t tokens, int32_t* out, void* work,
+                     int32_t* next_ids, int32_t* next_pos) {
+  const int n4 = n >> 2;
+  const int parts = n4 < kArgParts ? 1 : kArgParts;
+  const int chunk4 = (n4 + parts - 1) / parts;
+  hipLaunchKernelGGL(argmax_part_kernel, dim3(parts, tokens), dim3(kArgThreads), 0, s, x, n, chunk4, (float2*)work);
+  int rc = hip_check(hipGetLastError(), "argmax launch");
+  if (rc) return rc;
+  hipLaunchKernelGGL(argmax_pick_kernel, dim3(tokens), dim3(64), 0, s, (const float2*)work, parts, n, out, next_ids,
+                     next_pos);
   return hip_check(hipGetLastError(), "argmax launch");
 }
 

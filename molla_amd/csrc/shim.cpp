@@ -361,6 +361,22 @@ int mi_argmax(mi_stream stream, const float* x, int32_t n, int32_t tokens, int32
   return launch_argmax((hipStream_t)stream, x, n, tokens, out);
 }
 
+size_t mi_argmax_workspace(int32_t n, int32_t tokens) {
+  if (n <= 0 || tokens <= 0) return 0;
+  return argmax_workspace(n, tokens);
+}
+
+int mi_argmax_ws(mi_stream stream, const float* x, int32_t n, int32_t tokens, int32_t* out, void* work,
+                 size_t work_bytes, int32_t* next_ids, int32_t* next_pos) {
+  if (!x || !out) return fail(MI_ERR_ARG, "argmax: null pointer");
+  if (n <= 0 || tokens <= 0) return fail(MI_ERR_SHAPE, "argmax: empty row");
+  if (!work || work_bytes < argmax_workspace(n, tokens))
+    return fail(MI_ERR_WORKSPACE, "argmax: workspace of %zu bytes, %zu needed", work_bytes,
+                argmax_workspace(n, tokens));
+  if ((uintptr_t)work & 7) return fail(MI_ERR_ALIGN, "argmax: the workspace must be 8-byte aligned");
+  return launch_argmax_ws((hipStream_t)stream, x, n, tokens, out, work, next_ids, next_pos);
+}
+
 int mi_embed(mi_stream stream, const float* embedding, int32_t vocab, int32_t width, const int32_t* ids,
              int32_t tokens, float* out) {
   if (!embedding || !ids || !out) return fail(MI_ERR_ARG, "embed: null pointer");

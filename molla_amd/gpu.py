@@ -245,6 +245,19 @@ def device_argmax(ctx: DeviceContext, x: torch.Tensor, n: int, tokens: int = 1) 
     return out
 
 
+def device_argmax_ws(ctx: DeviceContext, x: torch.Tensor, n: int, tokens: int = 1, next_ids=None,
+                     next_pos=None) -> torch.Tensor:
+    """device_argmax spread over 64 parts a row (mi_argmax_ws); next_ids /
+    next_pos (device int32[tokens]) get the pick and pos + 1 when given."""
+    L = lib()
+    out = torch.empty(tokens, dtype=torch.int32, device=ctx.device)
+    work = torch.empty(L.mi_argmax_workspace(n, tokens), dtype=torch.uint8, device=ctx.device)
+    check(L.mi_argmax_ws(ctx.handle, x.data_ptr(), n, tokens, out.data_ptr(), work.data_ptr(), work.numel(),
+                         None if next_ids is None else next_ids.data_ptr(),
+                         None if next_pos is None else next_pos.data_ptr()))
+    return out
+
+
 def device_embed(ctx: DeviceContext, embedding: torch.Tensor, ids: torch.Tensor, out: torch.Tensor) -> None:
     """model.mojo:102 embed for an f32 table, one row per token id (device int32)."""
     vocab, width = embedding.shape

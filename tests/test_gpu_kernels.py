@@ -235,7 +235,9 @@ def test_q6k_head_and_argmax(ctx, tokens):
     out = torch.zeros(tokens * rows, device="cuda")
     gpu.device_matmul_into(ctx, w, torch.from_numpy(x).cuda(), out, tokens)
     picks = gpu.device_argmax(ctx, out, rows, tokens).cpu().numpy()
+    picks_ws = gpu.device_argmax_ws(ctx, out, rows, tokens).cpu().numpy()
     ctx.synchronize()
+    assert (picks_ws == picks).all()
     got = out.cpu().numpy().reshape(tokens, rows)
     err = np.abs(got.astype(np.float64) - want)
     assert err.max() <= 1e-5 * np.abs(want).max()
@@ -255,6 +257,39 @@ def test_argmax_ties_go_low(ctx):
     x[[17, 4000, 9999]] = 3.0
     picks = gpu.device_argmax(ctx, torch.from_numpy(x).cuda(), 10000).cpu().numpy()
     assert picks[0] == 17 == oracle.argmax(x)
+
+
+def test_argmax_ws_ties_go_low(ctx):
+    """The multi-part argmax: equal maxima in different parts (17 in part 0,
+    4000 in part 25, 9999 in the last) and in one part go to the lowest."""
+    from molla_amd import gpu
+    x = np.zeros(10000, np.float32)
+    x[[17, 4000, 9999]] = 3.0
+    assert gpu.device_argmax_ws(ctx, torch.from_numpy(x).cuda(), 10000).cpu().numpy()[0] == 17
+    x[17] = 0.0
+    assert gpu.device_argmax_ws(ctx, torch.from_numpy(x).cuda(), 10000).cpu().numpy()[0] == 4000
+    x[4001] = 3.0
+    assert gpu.device_argmax_ws(ctx, torch.from_numpy(x).cuda(), 10000).cpu().numpy()[0] == 4000
+
+
+@pytest.mark.parametrize("n", [1, 3, 5, 255, 256, 10001, 128256, 128259])
+@pytest.mark.parametrize("tokens", [1, 3])
+def test_argmax_ws_matches_oracle(ctx, n, tokens):
+    """Random rows (quantized to few values, so ties are frequent), aligned
+    and ragged lengths, every token against oracle.argmax; the optional
+    bookkeeping writes the picks to next_ids and adds one to next_pos."""
+    from molla_amd import gpu
+    rng = np.random.default_rng(n + tokens)
+    x = np.round(rng.standard_normal(n * tokens) * 2).astype(np.float32)
+    ids = torch.full((tokens,), -5, dtype=torch.int32, device="cuda")
+    pos = torch.arange(tokens, dtype=torch.int32, device="cuda") * 7
+    picks = gpu.device_argmax_ws(ctx, torch.from_numpy(x).cuda(), n, tokens, next_ids=ids, next_pos=pos)
+    ctx.synchronize()
+    picks = picks.cpu().numpy()
+    for t in range(tokens):
+        assert picks[t] == oracle.argmax(x[t * n:(t + 1) * n]), t
+    assert (ids.cpu().numpy() == picks).all()
+    assert (pos.cpu().numpy() == np.arange(tokens) * 7 + 1).all()
 
 
 # ---- norm / rope / attention ---------------------------------------------------
