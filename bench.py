@@ -154,6 +154,8 @@ def main():
         line["kinds"] = _kinds(L, h, stream)
         line["head"] = _head(L, h, stream)
         line["layer_kinds"] = _layer_kinds(L, h, stream)
+    line["config1"] = _config1(L, h, stream, cpu=not args.no_cpu)
+    line["config4"] = _config4(L)
     peak = _stream_peak(stream)
     line["roofline"]["stream_peak"] = peak
     line["roofline"]["frac_of_stream_33MB"] = round(achieved / peak["read_33MB"]["GB_s"], 4)
@@ -307,10 +309,14 @@ def _head(L, h, stream, reps=20):
 
         us = timed(lambda: check(L.mi_matvec_xq(h, kind, w.data_ptr(), rb, rows, cols, xq.data_ptr(), tokens,
                                                 y.data_ptr(), 0, None)))
-        am = timed(lambda: check(L.mi_argmax(h, y.data_ptr(), rows, tokens, picks.data_ptr())))
+        am1 = timed(lambda: check(L.mi_argmax(h, y.data_ptr(), rows, tokens, picks.data_ptr())))
+        aw = torch.empty(L.mi_argmax_workspace(rows, tokens), dtype=torch.uint8, device="cuda")
+        am = timed(lambda: check(L.mi_argmax_ws(h, y.data_ptr(), rows, tokens, picks.data_ptr(), aw.data_ptr(),
+                                                aw.numel(), None, None)))
         gbs = rows * rb / us / 1e3
         out[f"tokens_{tokens}"] = {"logits_us": round(us, 2), "GB_s": round(gbs, 1),
-                                   "frac_hbm_peak": round(gbs / PEAK_GBS, 4), "argmax_us": round(am, 2)}
+                                   "frac_hbm_peak": round(gbs / PEAK_GBS, 4), "argmax_us": round(am, 2),
+                                   "argmax_one_block_us": round(am1, 2)}
     return out
 
 
@@ -368,6 +374,134 @@ def _layer_kinds(L, h, stream, reps=30):
         del ws, layer
         torch.cuda.empty_cache()
     return out
+
+
+def _config1(L, h, stream, cpu=True, reps=400):
+    """one Q8_0 4864x896 matvec at batch 1 (the
+    reference's CPU-path config).  GPU: mi_matvec_xq on weights rotated over
+    copies worth 1 GiB (cold), K back-to-back launches between HIP events;
+    the activation's quantize is one more launch per call and is timed with
+    it as `step_us`.  CPU: the oracle's matvec (kernel.mojo:316) on the same
+    bytes, one thread and every usable one."""
+    import numpy as np
+    import torch
+
+    import oracle
+    from molla_amd import gpu, synth
+    from molla_amd._lib import check
+
+    rows, cols, kind = 4864, 896, gpu.Q_Q8_0
+    rb = gpu.row_bytes(kind, cols)
+    wbytes = rows * rb
+    n = max(2, (1 << 30) // wbytes + 1)
+    base = synth.quant_tensor(kind, rows, cols, 4864, device="cuda")
+    ws = base.repeat(n)
+    x = synth.normal(cols, 896, device="cuda")
+    xq = torch.empty(L.mi_matvec_workspace(cols, 1), dtype=torch.uint8, device="cuda")
+    y = torch.empty(rows, dtype=torch.float32, device="cuda")
+    algo = _algo_bytes(rows, cols, 1, wbytes)
+
+    def run(count, with_quant):
+        for i in range(count):
+            if with_quant:
+                check(L.mi_quantize(h, x.data_ptr(), cols, 1, xq.data_ptr()))
+            check(L.mi_matvec_xq(h, kind, ws.data_ptr() + (i % n) * wbytes, rb, rows, cols, xq.data_ptr(), 1,
+                                 y.data_ptr(), 0, None))
+    out = {"workload": "Q8_0 matvec 4864x896, batch 1 (BASELINE configs[0])", "weight_bytes": wbytes,
+           "algorithmic_bytes": algo}
+    check(L.mi_quantize(h, x.data_ptr(), cols, 1, xq.data_ptr()))
+    for with_quant, key in ((False, "kernel_us"), (True, "step_us")):
+        run(10, with_quant)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        run(reps, with_quant)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        out[key] = round(e0.elapsed_time(e1) * 1e3 / reps, 3)
+    out["GB_s"] = round(algo / out["kernel_us"] / 1e3, 1)
+    out["frac_hbm_peak"] = round(algo / out["kernel_us"] / 1e3 / PEAK_GBS, 4)
+    if cpu:
+        blob = base.cpu().numpy()
+        xh = x.cpu().numpy()
+        threads = max(1, min(16, _host_facts()["usable_cpus"] or 1))
+        t1, r1 = _timed(lambda: oracle.matvec(kind, blob, rows, cols, xh, threads=1), 2.0, 2000)
+        tn, rn = _timed(lambda: oracle.matvec(kind, blob, rows, cols, xh, threads=threads), 1.0, 2000)
+        out["cpu"] = {"us_1_thread": round(t1 * 1e6, 1), "GB_s_1_thread": round(algo / t1 / 1e9, 3), "reps_1": r1,
+                      "threads": threads, f"us_{threads}_threads": round(tn * 1e6, 1),
+                      f"GB_s_{threads}_threads": round(algo / tn / 1e9, 3), f"reps_{threads}": rn}
+    del ws, base
+    torch.cuda.empty_cache()
+    return out
+
+
+def _config4(L, copies=16, reps=8):
+    """one 8B Llama layer (4096 wide, 32 query / 8 key
+    heads of 128, MLP 14336, Q4_K, RMSNorm gains N(1, 0.1)) at batch 1 over an
+    f16 cache pre-filled with N(0, 1) to 4096 positions, the token at
+    position 4096.  `copies` distinct layers, each with its own cache
+    (2.2 GB in all, past the 256 MB Infinity Cache), run in turn from one
+    captured HIP graph, so each call streams cold weights and a cold cache;
+    us per layer = graph time / copies.  The roofline is the layer's
+    algorithmic bytes (weights + the 4097 cached keys and values) at 8 TB/s."""
+    import ctypes
+
+    import torch
+
+    from molla_amd import block, gpu, synth
+    from molla_amd._lib import check
+
+    spec = block.BlockSpec()
+    qw, kvw = spec.q_width(), spec.kv_width()
+    shapes = {"wq": (qw, spec.width), "wk": (kvw, spec.width), "wv": (kvw, spec.width), "wo": (spec.width, qw),
+              "gate": (spec.hidden, spec.width), "up": (spec.hidden, spec.width), "down": (spec.width, spec.hidden)}
+    steps = torch.from_numpy(gpu.rope_steps(spec.rope_dim, spec.rope_base)).cuda()
+    stream = torch.cuda.Stream()  # graphs are captured on a created stream
+    ctx = gpu.DeviceContext(0, stream=stream)
+    pos_v, count = 4096, 4097
+    stride = count * kvw
+    layers, caches = [], []
+    for c in range(copies):
+        ws = {n: gpu.Tensor.from_bytes(synth.quant_tensor(gpu.Q_Q4_K, r, cc, 700 + 10 * c + i, device="cuda"),
+                                       gpu.Q_Q4_K, cc, r) for i, (n, (r, cc)) in enumerate(shapes.items())}
+        an = synth.normal(spec.width, 780 + c, device="cuda", mean=1.0, std=0.1)
+        fn = synth.normal(spec.width, 880 + c, device="cuda", mean=1.0, std=0.1)
+        layers.append(block.DeviceLayer(spec, an, fn, ws, steps))
+        caches.append((synth.normal(stride, 40 + c, device="cuda").half(),
+                       synth.normal(stride, 140 + c, device="cuda").half()))
+    x = synth.normal(spec.width, 42, device="cuda")
+    pos = torch.full((1,), pos_v, dtype=torch.int32, device="cuda")
+    need = block.layer_workspace(layers[0], count, 1)
+    work = torch.empty(need + 256, dtype=torch.uint8, device="cuda")
+    descs = [l.desc for l in layers]
+
+    def all_layers():
+        for d, (k, v) in zip(descs, caches):
+            check(L.mi_decoder_layer(ctx.handle, ctypes.byref(d), x.data_ptr(), k.data_ptr(), v.data_ptr(), stride,
+                                     pos.data_ptr(), count, 1, work.data_ptr(), work.numel()))
+    with torch.cuda.stream(stream):
+        all_layers()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            all_layers()
+        g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            g.replay()
+        e1.record(stream)
+        torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / (reps * copies)
+    wbytes = layers[0].weight_bytes()
+    algo = wbytes + 2 * 2 * count * kvw
+    del g, layers, caches, work
+    torch.cuda.empty_cache()
+    return {"workload": "8B Llama layer, Q4_K, batch 1, token at position 4096 over an f16 cache (BASELINE configs[3])",
+            "us_per_layer": round(us, 2), "weight_bytes": wbytes, "algorithmic_bytes": algo,
+            "GB_s": round(algo / us / 1e3, 1), "frac_hbm_peak": round(algo / us / 1e3 / PEAK_GBS, 4),
+            "roofline_us": round(algo / PEAK_GBS / 1e3, 2), "copies": copies}
 
 
 def _kinds(L, h, stream, reps=100):
