@@ -215,6 +215,26 @@ int mi_argmax_ws(mi_stream stream, const float* x, int32_t n, int32_t tokens, in
 int mi_embed(mi_stream stream, const float* embedding, int32_t vocab, int32_t width,
              const int32_t* ids, int32_t tokens, float* out);
 
+/* Which kernel mi_matvec runs for a shape (no reference counterpart: an
+ * introspection hook for tests and tools).  Assumes the weight rows are
+ * cols / block_elements whole blocks at a 256-byte aligned address and a
+ * workspace of work_bytes.  Returns one of MI_ROUTE_*, with
+ * MI_ROUTE_SPLIT_BIT set when the matrix is split over K (the parts added
+ * by a second launch), or a negative MI_ERR_* code; *part_cols (may be NULL)
+ * gets the columns of one part (cols when not split). */
+enum {
+  MI_ROUTE_ROWS = 1,      /* batch-1 row kernel, Q4_K Q4_0 Q4_1 Q5_0 Q5_1 Q5_K Q8_0 */
+  MI_ROUTE_Q6K_ROWS = 2,  /* batch-1 Q6_K row kernel */
+  MI_ROUTE_HTILE = 3,     /* 2..8 tokens, f16 matrix-core tile, Q4_K / Q6_K */
+  MI_ROUTE_Q4K_TILE = 4,  /* 2..8 tokens, int8 matrix-core tile, Q4_K */
+  MI_ROUTE_B32_TILE = 5,  /* 2..8 tokens, int8 matrix-core tile, Q4_0 / Q8_0 */
+  MI_ROUTE_Q6K_TILE = 6,  /* 2..8 tokens, int8 matrix-core tile, Q6_K */
+  MI_ROUTE_GENERAL = 7,   /* the general kernel, any kind */
+  MI_ROUTE_PREFILL = 8,   /* above 8 tokens, the prefill matmul */
+  MI_ROUTE_SPLIT_BIT = 16
+};
+int mi_matvec_route(int kind, int32_t rows, int32_t cols, int32_t tokens, size_t work_bytes, int32_t* part_cols);
+
 /* ---- decoder layer (src/molla/nn/gpu_block.mojo:899 device_layer) -------- */
 
 typedef struct {

@@ -57,6 +57,7 @@ SIGNATURES = {
     "mi_attend_form": (ctypes.c_int, [P, I32, P, P, P, I32, I32, I32, F, I32, P, P, SZ]),
     "mi_argmax": (ctypes.c_int, [P, P, I32, I32, P]),
     "mi_argmax_workspace": (SZ, [I32, I32]),
+    "mi_matvec_route": (ctypes.c_int, [ctypes.c_int, I32, I32, I32, SZ, P]),
     "mi_argmax_ws": (ctypes.c_int, [P, P, I32, I32, P, P, SZ, P, P]),
     "mi_embed": (ctypes.c_int, [P, P, I32, I32, P, I32, P]),
     "mi_layer_workspace": (SZ, [ctypes.POINTER(MiLayerDesc), I32, I32]),

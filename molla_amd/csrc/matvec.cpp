@@ -27,21 +27,33 @@ int launch_matvec_q51(hipStream_t, const void*, int64_t, int32_t, int32_t, const
 int launch_matvec_q5k(hipStream_t, const void*, int64_t, int32_t, int32_t, const void*, int32_t, float*, int64_t,
                       int32_t, const float*);
 
+int matvec_route(int kind, const void* w, int64_t row_bytes, int32_t rows, int32_t cols, int32_t tokens,
+                 bool hx) {
+  if (tokens == 1 && rows_fits(kind, cols)) return MI_ROUTE_ROWS;
+  if (hx && htile_fits(kind, rows, cols, tokens) && ((uintptr_t)w & 7) == 0) return MI_ROUTE_HTILE;
+  if (kind == MI_Q4_K && q4k_tile_fits(cols, tokens)) return MI_ROUTE_Q4K_TILE;
+  if (b32_tile_fits(kind, cols, row_bytes, tokens) && ((uintptr_t)w & 15) == 0) return MI_ROUTE_B32_TILE;
+  if (kind == MI_Q6_K && q6k_tile_fits(cols, row_bytes, tokens) && ((uintptr_t)w & 1) == 0)
+    return MI_ROUTE_Q6K_TILE;
+  if (tokens == 1 && kind == MI_Q6_K && q6k_rows_fits(cols, row_bytes) && ((uintptr_t)w & 3) == 0)
+    return MI_ROUTE_Q6K_ROWS;
+  return MI_ROUTE_GENERAL;
+}
+
 int launch_matvec(hipStream_t s, int kind, const void* w, int64_t row_bytes, int32_t rows,
                   int32_t cols, const void* xq, int32_t tokens, float* y, int64_t ldy, int32_t epi,
                   const float* aux, const void* hx) {
-  if (tokens == 1 && rows_fits(kind, cols))
-    return launch_rows(s, kind, w, row_bytes, rows, cols, xq, y, epi, aux);
-  if (hx && htile_fits(kind, rows, cols, tokens) && ((uintptr_t)w & 7) == 0)
-    return launch_htile(s, kind, rows::one_matrix(w, row_bytes, rows), rows, cols, xq, hx, tokens, y, ldy, epi, aux);
-  if (kind == MI_Q4_K && q4k_tile_fits(cols, tokens))
-    return launch_q4k_tile(s, w, row_bytes, rows, cols, xq, tokens, y, ldy, epi, aux);
-  if (b32_tile_fits(kind, cols, row_bytes, tokens) && ((uintptr_t)w & 15) == 0)
-    return launch_b32_tile(s, kind, w, row_bytes, rows, cols, xq, tokens, y, ldy, epi, aux);
-  if (kind == MI_Q6_K && q6k_tile_fits(cols, row_bytes, tokens) && ((uintptr_t)w & 1) == 0)
-    return launch_q6k_tile(s, w, row_bytes, rows, cols, xq, tokens, y, ldy, epi, aux);
-  if (tokens == 1 && kind == MI_Q6_K && q6k_rows_fits(cols, row_bytes) && ((uintptr_t)w & 3) == 0)
-    return launch_q6k_rows(s, w, row_bytes, rows, cols, xq, y, epi, aux);
+  switch (matvec_route(kind, w, row_bytes, rows, cols, tokens, hx != nullptr)) {
+    case MI_ROUTE_ROWS: return launch_rows(s, kind, w, row_bytes, rows, cols, xq, y, epi, aux);
+    case MI_ROUTE_HTILE:
+      return launch_htile(s, kind, rows::one_matrix(w, row_bytes, rows), rows, cols, xq, hx, tokens, y, ldy, epi,
+                          aux);
+    case MI_ROUTE_Q4K_TILE: return launch_q4k_tile(s, w, row_bytes, rows, cols, xq, tokens, y, ldy, epi, aux);
+    case MI_ROUTE_B32_TILE: return launch_b32_tile(s, kind, w, row_bytes, rows, cols, xq, tokens, y, ldy, epi, aux);
+    case MI_ROUTE_Q6K_TILE: return launch_q6k_tile(s, w, row_bytes, rows, cols, xq, tokens, y, ldy, epi, aux);
+    case MI_ROUTE_Q6K_ROWS: return launch_q6k_rows(s, w, row_bytes, rows, cols, xq, y, epi, aux);
+    default: break;
+  }
   switch (kind) {
     case MI_Q4_K: return launch_matvec_q4k(s, w, row_bytes, rows, cols, xq, tokens, y, ldy, epi, aux);
     case MI_Q6_K: return launch_matvec_q6k(s, w, row_bytes, rows, cols, xq, tokens, y, ldy, epi, aux);

@@ -626,7 +626,7 @@ int launch_htile(hipStream_t s, int kind, const RowSegs& sg, int32_t rows, int32
 // A part's row bytes must be whole 8-byte words (a tile is copied in 8-byte
 // words, row by row): any number of 144-byte Q4_K superblocks, a multiple of
 // four 210-byte Q6_K ones (14336 columns: seven parts of 2048).
-static int htile_nsplit(int kind, int32_t cols) {
+int htile_nsplit(int kind, int32_t cols) {
   for (int n = (cols + 4095) / 4096; n <= 8; n++)
     if (cols % (n * 256 * kSBW) == 0 && (kind != MI_Q6_K || (cols / n / 256) % 4 == 0)) return n;
   return 0;

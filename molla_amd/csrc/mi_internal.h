@@ -153,7 +153,10 @@ int matmul_tokens(hipStream_t s, int kind, const void* w, int64_t row_bytes, int
                   const float* x, int32_t tokens, float* y, int64_t ldy, int32_t epi, const float* aux, void* work,
                   size_t work_bytes);
 // Every kind and batch: routes to the kernels above or the general
-// matvec_kernel.h.
+// matvec_kernel.h.  matvec_route names the kernel launch_matvec takes for a
+// shape (MI_ROUTE_*, the codes mi_matvec_route reports); the split-K forms
+// are chosen by mi_matvec itself (shim.cpp).
+int matvec_route(int kind, const void* w, int64_t row_bytes, int32_t rows, int32_t cols, int32_t tokens, bool hx);
 int launch_matvec(hipStream_t s, int kind, const void* w, int64_t row_bytes, int32_t rows,
                   int32_t cols, const void* xq, int32_t tokens, float* y, int64_t ldy, int32_t epi,
                   const float* aux, const void* hx = nullptr);
@@ -172,6 +175,8 @@ bool htile_fits(int kind, int32_t rows, int32_t cols, int32_t tokens);
 // parts (part: htile_split_bytes of scratch), then one reduce launch that adds
 // the parts in order and applies the epilogue.
 bool htile_split_fits(int kind, int32_t rows, int32_t cols, int32_t tokens);
+// The parts a split f16 tile cuts cols into (0: none fits).
+int htile_nsplit(int kind, int32_t cols);
 // q|k|v (whole 16-row segments) with the rope and the f16 cache store in the
 // epilogue, as launch_q4k_tile_qkv_rope.
 // kind MI_Q6_K: a Q6_K segment (a Q4_K_M file's attn_v) in its own launch.

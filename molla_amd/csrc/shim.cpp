@@ -266,6 +266,27 @@ int mi_matvec(mi_stream stream, int kind, const void* w, int64_t row_bytes, int3
   return launch_matvec(s, kind, w, row_bytes, rows, cols, work, tokens, y, rows, epi, aux, hx_of(work, cols, tokens));
 }
 
+int mi_matvec_route(int kind, int32_t rows, int32_t cols, int32_t tokens, size_t work_bytes, int32_t* part_cols) {
+  if (mi_block_elements(kind) <= 0) return fail(MI_ERR_KIND, "route: ggml type %d has no device kernel", kind);
+  if (rows <= 0 || cols <= 0 || cols % mi_block_elements(kind) || tokens <= 0 || tokens > kMaxPrefill)
+    return fail(MI_ERR_SHAPE, "route: bad shape");
+  if (part_cols) *part_cols = cols;
+  if (tokens > kMaxTokens) return MI_ROUTE_PREFILL;
+  const int64_t rb = mi_row_bytes(kind, cols);
+  const void* w = (const void*)(uintptr_t)256;  // an aligned address, never dereferenced
+  const size_t act = batch_act_bytes(cols, tokens);
+  const size_t sb = tokens > 1 ? batch_split_bytes(kind, rows, cols, tokens) : 0;
+  if (sb && work_bytes >= act + sb) {
+    const int sbb = kind == MI_Q6_K ? 210 : 144;
+    if (htile_split_fits(kind, rows, cols, tokens) && rb == (int64_t)(cols / 256) * sbb) {
+      if (part_cols) *part_cols = cols / htile_nsplit(kind, cols);
+      return MI_ROUTE_HTILE | MI_ROUTE_SPLIT_BIT;
+    }
+    if (kind == MI_Q4_K && q4k_tile_split_fits(rows, cols, tokens)) return MI_ROUTE_Q4K_TILE | MI_ROUTE_SPLIT_BIT;
+  }
+  return matvec_route(kind, w, rb, rows, cols, tokens, tokens > 1);
+}
+
 int mi_rms_norm(mi_stream stream, const float* x, const float* gain, int32_t n, int32_t tokens, float eps,
                 float* out, void* xq) {
   if (!x || !gain || (!out && !xq)) return fail(MI_ERR_ARG, "rms_norm: null pointer");

@@ -40,7 +40,7 @@ def rms64(x, gain, eps):
     return x / np.sqrt(np.mean(x * x) + eps) * gain
 
 
-def attend64(q, keys, values, count, heads, kv_heads, head_dim, scale, interleave=False):
+def attend64(q, keys, values, count, heads, kv_heads, head_dim, scale, interleave=False, pmax=None):
     group = heads // kv_heads
     K = keys.reshape(-1, kv_heads * head_dim)[:count].reshape(count, kv_heads, head_dim)
     V = values.reshape(-1, kv_heads * head_dim)[:count].reshape(count, kv_heads, head_dim)
@@ -50,6 +50,8 @@ def attend64(q, keys, values, count, heads, kv_heads, head_dim, scale, interleav
         s = K[:, kh, :] @ q[h * head_dim:(h + 1) * head_dim] * scale
         p = np.exp(s - s.max())
         out[h] = (p / p.sum()) @ V[:, kh, :]
+        if pmax is not None:
+            pmax.append(float(p.max() / p.sum()))
     return out.reshape(-1)
 
 
@@ -95,8 +97,9 @@ def layer64(spec, weights, x, keys, values, slot, pos, interleave=False, parts=F
         keys[slot] = np.concatenate([rms64(h, opt["k_norm"], eps) for h in keys[slot].reshape(KV, HD)])
     q = rope64(q, H, HD, spec["rope_dim"], spec["rope_base"], spec["neox"], pos, fac)
     keys[slot] = rope64(keys[slot], KV, HD, spec["rope_dim"], spec["rope_base"], spec["neox"], pos, fac)
+    pmax = []
     heads_out = attend64(q, keys.reshape(-1), values.reshape(-1), slot + 1, H, KV, HD, spec["attn_scale"],
-                         interleave)
+                         interleave, pmax)
     proj = W["wo"] @ heads_out
     post = {}
     if opt["attn_post_norm"] is not None:
@@ -116,7 +119,7 @@ def layer64(spec, weights, x, keys, values, slot, pos, interleave=False, parts=F
         proj = rms64(proj, opt["ffn_post_norm"], eps)
     out = x + proj
     if parts:
-        return out, {"W": W, "attn": heads_out, "act": act, "post": post, "eps": eps}
+        return out, {"W": W, "attn": heads_out, "act": act, "post": post, "eps": eps, "pmax": pmax}
     return out
 
 

@@ -62,13 +62,16 @@ def spec_of(width, hidden, heads, kv_heads, head_dim, base=500000.0):
                 neox=0, eps=1e-5, rope_base=base, attn_scale=float(np.float32(1 / math.sqrt(head_dim))))
 
 
-def layer_gate(spec, host, x, keys16, values16, pos):
+def layer_gate(spec, host, x, keys16, values16, pos, stats=None):
     """Per-element tolerance of one layer's output for sequence input x over
     a cache of f16 values (keys16/values16: [pos + 1, kv_width] float32
-    holding halves): tests/layer64.py layer_bound."""
+    holding halves): tests/layer64.py layer_bound.  stats (a dict): gets the
+    largest softmax weight of each head ("pmax")."""
     k = np.asarray(keys16, np.float64).reshape(pos + 1, -1).copy()
     v = np.asarray(values16, np.float64).reshape(pos + 1, -1).copy()
     _, parts = l64.layer64(spec, host, x, k, v, pos, pos, parts=True)
+    if stats is not None:
+        stats["pmax"] = parts["pmax"]
     return l64.layer_bound(parts)
 
 
@@ -113,12 +116,28 @@ def llama31_factors(pairs):
     ((4096, 1024, 32, 32, 128), 50, 1, True),
 ])
 def test_layer_matches_oracle(dims, pos, tokens, factors):
+    _layer_vs_oracle(dims, pos, tokens, factors)
+
+
+@pytest.mark.parametrize("tokens", [4, 8])
+def test_batched_config_layer_spread_softmax(tokens):
+    """Config 4's shape at 4 and 8 tokens with the attention norm's gain
+    scaled by 0.05: q and k elements of a few units, scores of order one, so
+    the batched attention (the 512-thread slice kernel) and the q|k|v tile's
+    rope epilogue are checked where the softmax spreads over many keys (with
+    N(1, 0.1) gains the scores reach thousands and one key takes all)."""
+    _layer_vs_oracle((4096, 14336, 32, 8, 128), 300, tokens, False, attn_gain=0.05)
+
+
+def _layer_vs_oracle(dims, pos, tokens, factors, attn_gain=1.0):
     from molla_amd import block, gpu
     ctx = gpu.DeviceContext(0)
     spec = spec_of(*dims)
     host = make_layer_weights(spec, 7)
     if factors:
         host["rope_factors"] = llama31_factors(spec["rope_dim"] // 2)
+    if attn_gain != 1.0:
+        host["attn_norm"] = (host["attn_norm"] * attn_gain).astype(np.float32)
     bs, layer = device_layer_from(host, spec)
     kvw = bs.kv_width()
     count = pos + 1
@@ -142,7 +161,14 @@ def test_layer_matches_oracle(dims, pos, tokens, factors):
         xr = x.reshape(tokens, -1)[t].copy()
         kr = keys16.float().numpy().reshape(tokens, -1)[t].copy()
         vr = vals16.float().numpy().reshape(tokens, -1)[t].copy()
-        bound = layer_gate(spec, host, xr, kr, vr, pos)
+        stats = {}
+        bound = layer_gate(spec, host, xr, kr, vr, pos, stats)
+        pm = np.array(stats["pmax"])
+        print(f"seq {t}: largest softmax weight per head: median {np.median(pm):.3e}, max {pm.max():.3e}",
+              flush=True)
+        if attn_gain != 1.0:
+            # the point of the case: no head's softmax is one key
+            assert pm.max() < 0.5
         oracle.layer_step(L, xr, kr, vr, pos, pos, f16_store=True, threads=8)
         assert_layer_close(got_x[t], xr, bound, f"seq {t}:")
         # earlier slots untouched, new slot within one f16 ulp of the oracle's rounding
