@@ -34,6 +34,7 @@ def test_dispatch_grid(ctx, kind):
     rows = 48
     routes = set()
     for cols in COLS:
+        print(f"kind {kind} cols {cols}", flush=True)
         blob = synth.quant_tensor(kind, rows, cols, 900 + cols // 256 + kind).numpy()
         x = synth.normal(8 * cols, 901 + cols // 256).numpy()
         want_all = oracle.matvec(kind, blob, rows, cols, x.reshape(8, cols), threads=8).reshape(8, rows)
