@@ -120,7 +120,11 @@ int mi_matvec(mi_stream stream, int kind, const void* w, int64_t row_bytes,
  * resolved once per device on first use; the call itself allocates nothing.
  * Shapes whose mi_matvec_workspace(cols, tokens) is larger are refused
  * (MI_ERR_WORKSPACE).  Every call on one GPU shares that array: calls that
- * overlap on one GPU race. */
+ * overlap on one GPU race.  The array is reserved on every GPU the library is
+ * loaded on, 32 MiB each, whether or not this entry point is called.  The
+ * first call on a device resolves the array's address (hipGetSymbolAddress,
+ * which may load the code object): make that first call outside graph
+ * capture; later calls may be captured. */
 #define MI_MATVEC_NOALLOC_BYTES (32u << 20)
 int mi_matvec_noalloc(mi_stream stream, int kind, const void* w, int64_t row_bytes,
                       int32_t rows, int32_t cols, const float* x, int32_t tokens,

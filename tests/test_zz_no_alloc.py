@@ -72,3 +72,37 @@ def test_noalloc_refuses_beyond_its_scratch():
     with pytest.raises(MiError, match="static"):
         check(L.mi_matvec_noalloc(ctx.handle, gpu.Q_Q4_K, blob.data_ptr(), gpu.row_bytes(gpu.Q_Q4_K, cols), 256,
                                   cols, x.data_ptr(), tokens, y.data_ptr(), 0, None))
+
+
+@pytest.mark.parametrize("kind,rows,cols,tokens", [(gpu.Q_Q4_K, 4096, 4096, 1), (gpu.Q_Q4_K, 4096, 4096, 4)])
+def test_noalloc_under_graph_capture(kind, rows, cols, tokens):
+    """The use the entry point is for: after a first eager call on the device
+    (which resolves the scratch address), calls captured in a HIP graph;
+    every replay, with eager work and synchronizations between them, equals
+    the eager result bit for bit."""
+    L = lib()
+    ctx = gpu.DeviceContext(0)
+    blob = synth.quant_tensor(kind, rows, cols, 77, device="cuda")
+    rb = gpu.row_bytes(kind, cols)
+    x = synth.normal(tokens * cols, 78, device="cuda")
+    want = torch.empty(tokens * rows, device="cuda")
+    check(L.mi_matvec_noalloc(ctx.handle, kind, blob.data_ptr(), rb, rows, cols, x.data_ptr(), tokens,
+                              want.data_ptr(), 0, None))
+    ctx.synchronize()
+    stream = torch.cuda.Stream()
+    sctx = gpu.DeviceContext(0, stream=stream)
+    got = torch.full((tokens * rows,), 7.0, device="cuda")
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        check(L.mi_matvec_noalloc(sctx.handle, kind, blob.data_ptr(), rb, rows, cols, x.data_ptr(), tokens,
+                                  got.data_ptr(), 0, None))
+    for r in range(3):
+        got.fill_(7.0)
+        # eager work on the same scratch between replays
+        other = torch.empty(tokens * rows, device="cuda")
+        check(L.mi_matvec_noalloc(ctx.handle, kind, blob.data_ptr(), rb, rows, cols, x.data_ptr(), tokens,
+                                  other.data_ptr(), 0, None))
+        ctx.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(got.view(torch.int32), want.view(torch.int32)), r
