@@ -65,6 +65,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-batched", action="store_true", help="skip the batch-4/8 matrix-core tile lines")
     ap.add_argument("--no-prefill", action="store_true", help="skip the 256-token prefill matmul lines")
+    ap.add_argument("--no-configs", action="store_true", help="skip the BASELINE configs[0] and configs[3] lines")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}).",
@@ -154,8 +155,9 @@ def main():
         line["kinds"] = _kinds(L, h, stream)
         line["head"] = _head(L, h, stream)
         line["layer_kinds"] = _layer_kinds(L, h, stream)
-    line["config1"] = _config1(L, h, stream, cpu=not args.no_cpu)
-    line["config4"] = _config4(L)
+    if not args.no_configs:
+        line["config1"] = _config1(L, h, stream, cpu=not args.no_cpu)
+        line["config4"] = _config4(L)
     peak = _stream_peak(stream)
     line["roofline"]["stream_peak"] = peak
     line["roofline"]["frac_of_stream_33MB"] = round(achieved / peak["read_33MB"]["GB_s"], 4)
