@@ -62,8 +62,9 @@ Carve carve(const mi_layer_desc* d, int32_t max_count, int32_t tokens) {
   c.xq2 = at;  // down's input; at 2..8 tokens followed by its hx form
   at += up256((size_t)xq_token_bytes(d->hidden) * tokens * (tokens > 1 ? 2 : 1));
   c.part = at;  // split-K partial sums of the down projection (batch 2..8)
-  at += tokens > 1 ? up256(std::max(q4k_tile_split_bytes(d->width, tokens),
-                                    htile_split_bytes(d->width, d->hidden, tokens)))
+  at += tokens > 1 ? up256(std::max({q4k_tile_split_bytes(d->width, tokens),
+                                     htile_split_bytes(d->width, d->hidden, tokens),
+                                     htile_split_bytes(d->width, d->heads * d->head_dim, tokens, 2)}))
                    : 0;
   c.total = at;
   return c;
@@ -367,6 +368,17 @@ static bool down_htile(const mi_layer_desc* d, int32_t tokens) {
          !((uintptr_t)d->down.data & (k == MI_Q6_K ? 3 : 7));
 }
 
+// wo at 4..8 tokens split over K in two (its 4096 columns otherwise fill
+// 128 tiles of one launch), the residual add and the ffn norm (with the hx
+// form for the GLU tile) in the reduce launch after the parts.
+static bool wo_split_norm(const mi_layer_desc* d, int32_t qw, int32_t tokens) {
+  const int k = d->wo.kind;
+  return tokens >= 4 && (k == MI_Q4_K || k == MI_Q6_K) &&
+         htile_split_norm_fits(k, d->width, qw, tokens, 2) &&
+         d->wo.row_bytes == (int64_t)(qw / 256) * (k == MI_Q6_K ? 210 : 144) &&
+         !((uintptr_t)d->wo.data & (k == MI_Q6_K ? 3 : 7));
+}
+
 static int down_batch(hipStream_t s, const mi_layer_desc* d, const void* xq2, int32_t tokens, float* resid,
                       void* part, NextNorm* nn, void* xq) {
   const void* hx2 = (const uint8_t*)xq2 + (size_t)xq_token_bytes(d->hidden) * tokens;
@@ -652,8 +664,11 @@ static int llama_layer(hipStream_t s, const mi_layer_desc* d, float* resid, uint
                           d->head_dim, d->attn_scale, pos, -1, max_count, tokens, nullptr, xq, attn,
                           d->cache_form, kv_index, index_stride, hx)))
     return rc;
-  if ((rc = launch_matvec(s, d->wo.kind, d->wo.data, d->wo.row_bytes, d->width, qw, xq, tokens, resid,
-                          d->width, MI_EPI_ADD, nullptr, hx)))
+  const bool glu_tile = tokens >= 4 && d->gate.kind == MI_Q4_K && d->up.kind == MI_Q4_K &&
+                        d->gate.row_bytes == d->up.row_bytes && htile_glu_fits(d->hidden, d->width, tokens);
+  const bool wo_split = glu_tile && wo_split_norm(d, qw, tokens);
+  if (!wo_split && (rc = launch_matvec(s, d->wo.kind, d->wo.data, d->wo.row_bytes, d->width, qw, xq, tokens, resid,
+                                       d->width, MI_EPI_ADD, nullptr, hx)))
     return rc;
 
   // mlp_layer (block.mojo:429), gated silu
@@ -667,15 +682,20 @@ static int llama_layer(hipStream_t s, const mi_layer_desc* d, float* resid, uint
     return launch_matvec(s, d->down.kind, d->down.data, d->down.row_bytes, d->width, d->hidden, xq2, tokens,
                          resid, d->width, MI_EPI_ADD, nullptr);
   }
-  if (tokens >= 4 && d->gate.kind == MI_Q4_K && d->up.kind == MI_Q4_K && d->gate.row_bytes == d->up.row_bytes &&
-      htile_glu_fits(d->hidden, d->width, tokens)) {
+  if (glu_tile) {
     // a batch of 4..8: the norm (with the hx form), then gate and up on the
     // f16 matrix-core tile, which writes act(gate) * up straight into down's
     // xq and hx forms (at 4 tokens 3.084 against 3.115 ms a decode step with
     // the int8 GLU tile below, at 8 tokens 3.86 against 4.50 ms)
     void* hx2 = (uint8_t*)xq + (size_t)xq_token_bytes(d->width) * tokens;
     void* xq2 = base + c.xq2;
-    if ((rc = launch_rms_norm(s, resid, d->ffn_norm, d->width, tokens, d->eps, nullptr, xq, hx2))) return rc;
+    if (wo_split) {
+      if ((rc = launch_htile_split_norm(s, d->wo.kind, d->wo.data, d->wo.row_bytes, d->width, qw, xq, hx, tokens,
+                                        resid, d->ffn_norm, d->eps, (float*)(base + c.part), xq, hx2, 2)))
+        return rc;
+    } else if ((rc = launch_rms_norm(s, resid, d->ffn_norm, d->width, tokens, d->eps, nullptr, xq, hx2))) {
+      return rc;
+    }
     if ((rc = launch_htile_glu(s, d->gate.data, d->up.data, d->gate.row_bytes, d->hidden, d->width, xq, hx2, tokens,
                                MI_EPI_NONE, xq2, down_htile(d, tokens))))
       return rc;

@@ -626,14 +626,14 @@ int launch_htile(hipStream_t s, int kind, const RowSegs& sg, int32_t rows, int32
 // A part's row bytes must be whole 8-byte words (a tile is copied in 8-byte
 // words, row by row): any number of 144-byte Q4_K superblocks, a multiple of
 // four 210-byte Q6_K ones (14336 columns: seven parts of 2048).
-int htile_nsplit(int kind, int32_t cols) {
-  for (int n = (cols + 4095) / 4096; n <= 8; n++)
+int htile_nsplit(int kind, int32_t cols, int nmin) {
+  for (int n = std::max(nmin, (cols + 4095) / 4096); n <= 8; n++)
     if (cols % (n * 256 * kSBW) == 0 && (kind != MI_Q6_K || (cols / n / 256) % 4 == 0)) return n;
   return 0;
 }
 
-bool htile_split_fits(int kind, int32_t rows, int32_t cols, int32_t tokens) {
-  const int n = htile_nsplit(kind, cols);
+bool htile_split_fits(int kind, int32_t rows, int32_t cols, int32_t tokens, int nmin) {
+  const int n = htile_nsplit(kind, cols, nmin);
   return n > 1 && htile_fits(kind, rows, cols / n, tokens);
 }
 
@@ -647,15 +647,16 @@ static bool split_rows_ok(int kind, const void* w, int64_t row_bytes, int32_t co
 }
 
 // the parts, and one more slot for launch_htile_split_norm's residual copy
-size_t htile_split_bytes(int32_t rows, int32_t cols, int32_t tokens) {
+size_t htile_split_bytes(int32_t rows, int32_t cols, int32_t tokens, int nmin) {
   // room for either kind's parts
-  const int n = std::max(htile_nsplit(MI_Q4_K, cols), htile_nsplit(MI_Q6_K, cols));
+  const int n = std::max(htile_nsplit(MI_Q4_K, cols, nmin), htile_nsplit(MI_Q6_K, cols, nmin));
   return sizeof(float) * (size_t)(n + 1) * rows * tokens;
 }
 
 static int launch_split_main(hipStream_t s, int kind, const void* w, int64_t row_bytes, int32_t rows, int32_t cols,
-                             const void* xq, const void* hx, int32_t tokens, const float* resid, float* part) {
-  const int n = htile_nsplit(kind, cols), pc = cols / n;
+                             const void* xq, const void* hx, int32_t tokens, const float* resid, float* part,
+                             int nmin = 1) {
+  const int n = htile_nsplit(kind, cols, nmin), pc = cols / n;
   const RowSegs sg = rows::one_matrix(w, row_bytes, rows);
   const int waves = pc / (256 * kSBW);
   const int grid = std::min((rows + 15) / 16, std::max(1, cu_count() / n));
@@ -700,22 +701,23 @@ int launch_htile_split(hipStream_t s, int kind, const void* w, int64_t row_bytes
   return hip_check(hipGetLastError(), "htile split reduce");
 }
 
-bool htile_split_norm_fits(int kind, int32_t rows, int32_t cols, int32_t tokens) {
-  const int n = htile_nsplit(kind, cols);
+bool htile_split_norm_fits(int kind, int32_t rows, int32_t cols, int32_t tokens, int nmin) {
+  const int n = htile_nsplit(kind, cols, nmin);
   // launch_split_add_norm takes rows of up to 16 * 256 values
-  return htile_split_fits(kind, rows, cols, tokens) && n <= kMaxNormSplit && rows % 32 == 0 && rows <= 4096 &&
+  return htile_split_fits(kind, rows, cols, tokens, nmin) && n <= kMaxNormSplit && rows % 32 == 0 && rows <= 4096 &&
          (int64_t)std::min((rows + 15) / 16, std::max(1, cu_count() / n)) * n * (cols / n / 256 / kSBW) * 64 >=
              (int64_t)tokens * rows;
 }
 
 int launch_htile_split_norm(hipStream_t s, int kind, const void* w, int64_t row_bytes, int32_t rows, int32_t cols,
                             const void* xq, const void* hx, int32_t tokens, float* resid, const float* gain,
-                            float eps, float* part, void* xq_out, void* hx_out) {
-  if (!htile_split_norm_fits(kind, rows, cols, tokens) || !split_rows_ok(kind, w, row_bytes, cols))
+                            float eps, float* part, void* xq_out, void* hx_out, int nmin) {
+  if (!htile_split_norm_fits(kind, rows, cols, tokens, nmin) || !split_rows_ok(kind, w, row_bytes, cols))
     return fail(MI_ERR_SHAPE, "htile: no split-K tile with a norm for %d x %d at %d tokens", rows, cols, tokens);
-  int rc = launch_split_main(s, kind, w, row_bytes, rows, cols, xq, hx, tokens, resid, part);
+  int rc = launch_split_main(s, kind, w, row_bytes, rows, cols, xq, hx, tokens, resid, part, nmin);
   if (rc) return rc;
-  return launch_split_add_norm(s, part, htile_nsplit(kind, cols), resid, gain, rows, tokens, eps, xq_out, hx_out);
+  return launch_split_add_norm(s, part, htile_nsplit(kind, cols, nmin), resid, gain, rows, tokens, eps, xq_out,
+                               hx_out);
 }
 
 bool htile_qkv_rope_fits(const RowSegs& sg, int32_t cols, int32_t tokens, int32_t head_dim, int32_t rope_dim,

@@ -174,9 +174,9 @@ bool htile_fits(int kind, int32_t rows, int32_t cols, int32_t tokens);
 // Q4_K or Q6_K rows longer than 4096 columns on the f16 tile: K split over column
 // parts (part: htile_split_bytes of scratch), then one reduce launch that adds
 // the parts in order and applies the epilogue.
-bool htile_split_fits(int kind, int32_t rows, int32_t cols, int32_t tokens);
+bool htile_split_fits(int kind, int32_t rows, int32_t cols, int32_t tokens, int nmin = 1);
 // The parts a split f16 tile cuts cols into (0: none fits).
-int htile_nsplit(int kind, int32_t cols);
+int htile_nsplit(int kind, int32_t cols, int nmin = 1);
 // q|k|v (whole 16-row segments) with the rope and the f16 cache store in the
 // epilogue, as launch_q4k_tile_qkv_rope.
 // kind MI_Q6_K: a Q6_K segment (a Q4_K_M file's attn_v) in its own launch.
@@ -184,7 +184,7 @@ bool htile_qkv_rope_fits(const RowSegs& sg, int32_t cols, int32_t tokens, int32_
                          int kind = MI_Q4_K);
 int launch_htile_qkv_rope(hipStream_t s, const RowSegs& sg, int32_t cols, const void* xq, const void* hx,
                           int32_t tokens, float* q, int64_t ldq, const QkvRope& rp, int kind = MI_Q4_K);
-size_t htile_split_bytes(int32_t rows, int32_t cols, int32_t tokens);
+size_t htile_split_bytes(int32_t rows, int32_t cols, int32_t tokens, int nmin = 1);
 int launch_htile_split(hipStream_t s, int kind, const void* w, int64_t row_bytes, int32_t rows, int32_t cols,
                        const void* xq, const void* hx, int32_t tokens, float* y, int64_t ldy, int32_t epi,
                        const float* aux, float* part);
@@ -194,10 +194,10 @@ int launch_htile_split(hipStream_t s, int kind, const void* w, int64_t row_bytes
 // xq_out and in the hx form into hx_out.  Up to kMaxNormSplit parts and
 // 4096 rows.
 constexpr int kMaxNormSplit = 4;
-bool htile_split_norm_fits(int kind, int32_t rows, int32_t cols, int32_t tokens);
+bool htile_split_norm_fits(int kind, int32_t rows, int32_t cols, int32_t tokens, int nmin = 1);
 int launch_htile_split_norm(hipStream_t s, int kind, const void* w, int64_t row_bytes, int32_t rows, int32_t cols,
                             const void* xq, const void* hx, int32_t tokens, float* resid, const float* gain,
-                            float eps, float* part, void* xq_out, void* hx_out);
+                            float eps, float* part, void* xq_out, void* hx_out, int nmin = 1);
 // part[k][t][r] for k < nsplit, and the old residual in slot nsplit:
 // resid[t][r] = old + (part 0 + ... + part nsplit-1), then its RMSNorm by
 // gain (rms_norm_kernel's arithmetic) into xq and hx.

@@ -9,8 +9,8 @@
 
 A decode step starts at an embed_kernel dispatch (DeviceSession.step), so
 --steps N keeps the dispatches from the N-th last embed_kernel on and reports
-per-step counts and times, the wall span per step and the kernel-busy time
-per step.  Used for the tables under profiles/.
+per-step counts and times, the wall span per step, the median embed-to-embed
+step and the kernel-busy time per step.  Used for the tables under profiles/.
 """
 
 from __future__ import annotations
@@ -69,8 +69,10 @@ def main() -> None:
         x[1] += (e - s) / 1e3
     busy = sum(v[1] for v in agg.values())
     if a.steps:
+        gaps = sorted((b - a_) / 1e3 for a_, b in zip(emb[-a.steps:], emb[-a.steps + 1:]))
+        med = gaps[len(gaps) // 2] if gaps else span
         print(f"last {n} steps: {len(rows)} dispatches, span {span / n:.1f} us/step, "
-              f"kernel-busy {busy / n:.1f} us/step")
+              f"kernel-busy {busy / n:.1f} us/step, median step {med:.1f} us")
     unit = "per step" if a.steps else "calls"
     print(f"| kernel | {unit} | avg us | us{'/step' if a.steps else ' total'} | share |")
     print("|---|---|---|---|---|")
