@@ -3,6 +3,8 @@
 
     python -m molla_amd.trace_summary DB            # every kernel of the run
     python -m molla_amd.trace_summary DB --steps N  # the last N decode steps
+    python -m molla_amd.trace_summary DB --steps N --cycle 'KERNEL=wo,down'
+        # the same, the dispatches of KERNEL in each step labelled in turn
     python -m molla_amd.trace_summary DB --calls prefill_x_kernel --per 23
         # calls that start at each dispatch of the named kernel, in runs of
         # 23 calls (one bench shape each): median duration per kernel
@@ -33,7 +35,13 @@ def main() -> None:
     ap.add_argument("--top", type=int, default=20)
     ap.add_argument("--calls", default="")
     ap.add_argument("--per", type=int, default=1)
+    ap.add_argument("--cycle", action="append", default=[],
+                    help="NAME=a,b: label the dispatches of kernel NAME in each step a, b, a, b, ... in order")
     a = ap.parse_args()
+    cycles = {}
+    for c in a.cycle:
+        name, labels = c.split("=", 1)
+        cycles[name] = labels.split(",")
     rows = sqlite3.connect(a.db).execute("select name, start, end from kernels order by start").fetchall()
     if a.calls:
         calls = []
@@ -63,8 +71,16 @@ def main() -> None:
         n = a.steps
         span = (max(r[2] for r in rows) - t0) / 1e3
     agg = collections.defaultdict(lambda: [0, 0.0])
+    seen = collections.Counter()
     for name, s, e in rows:
-        x = agg[short(name)]
+        kn = short(name)
+        if "embed_kernel" in name:
+            seen.clear()
+        if kn in cycles:
+            labels = cycles[kn]
+            seen[kn] += 1
+            kn = f"{kn} [{labels[(seen[kn] - 1) % len(labels)]}]"
+        x = agg[kn]
         x[0] += 1
         x[1] += (e - s) / 1e3
     busy = sum(v[1] for v in agg.values())
