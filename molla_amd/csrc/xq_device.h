@@ -88,14 +88,15 @@ __device__ __forceinline__ void quantize_group32(float v, int lane32, int g, int
 // then does norm_row_to_lds wait for the row.  Vector-memory loads of a wave
 // complete in issue order, so the row's loads must go out first.
 //
-// norm_row_to_lds: the NT threads normalise the row with rms_norm_kernel's
-// arithmetic (float64 sum of squares, scale = f32(1/sqrt(sum/n + eps)), x *
-// scale * gain) and write it in matvec form into the LDS `xs` (4 n bytes,
-// the planes of an xq token), byte for byte what quantize_group32 writes.
-// Thread t holds values 8t..8t+7, so a 32-value group is 4 lanes and its
-// reductions are two shuffles.  Every block sums in the same order, so every
-// block derives the same scale.  `red` is NT / 64 doubles of LDS; the step
-// ends with a barrier.
+// norm_row_to_lds: the NT threads take rms_norm_kernel's scale (float64 sum
+// of squares, scale = f32(1/sqrt(sum/n + eps))) and write the row in matvec
+// form into the LDS `xs` (4 n bytes, the planes of an xq token): x * scale *
+// gain, byte for byte what quantize_group32 writes for it, or (DEFER, below)
+// x * gain with the scale left to the caller.  Thread t holds values
+// 8t..8t+7, so a 32-value group is 4 lanes and its reductions are two
+// shuffles.  Every block sums in the same order, so every block derives the
+// same scale.  `red` is NT / 64 doubles of LDS; the step ends with a
+// barrier.
 struct NormRow {
   float4 x0, x1, g0, g1;
 };
@@ -169,8 +170,16 @@ __device__ __forceinline__ void quantize8_to_lds(const float (&v)[8], bool live,
   }
 }
 
-template <int NT>
-__device__ __forceinline__ void norm_row_to_lds(const NormRow& nr, int n, float eps, uint8_t* xs, double* red) {
+//
+// DEFER: the row goes into LDS as x * gain, without the norm's scale, and
+// the scale is returned for the caller to apply to each matvec result
+// (W (s x g) = s (W (x g)); the matvec form's per-group power-of-two scale
+// gives x g the same relative precision as s x g).  The sum of squares then
+// runs beside the quantize instead of ahead of it, and the step has one
+// barrier.  Without DEFER the scale is applied first, as rms_norm_kernel
+// does, and 1 is returned.
+template <int NT, bool DEFER = false>
+__device__ __forceinline__ float norm_row_to_lds(const NormRow& nr, int n, float eps, uint8_t* xs, double* red) {
 #pragma clang fp contract(off)
   const int t = threadIdx.x;
   const int i0 = t * 8;
@@ -183,15 +192,22 @@ __device__ __forceinline__ void norm_row_to_lds(const NormRow& nr, int n, float 
   for (int k = 0; k < 8; k++) acc += live ? (double)v[k] * (double)v[k] : 0.0;
   acc = lanes::reduce_sum<64>(acc);
   if ((t & 63) == 0) red[t >> 6] = acc;
+  if constexpr (DEFER) {
+#pragma unroll
+    for (int k = 0; k < 8; k++) v[k] = v[k] * g[k];
+    quantize8_to_lds(v, live, t, n, xs);
+  }
   __syncthreads();
   double sum = 0.0;
 #pragma unroll
   for (int i = 0; i < NT / 64; i++) sum += red[i];
   const float scale = (float)(1.0 / sqrt(sum / (double)n + (double)eps));
+  if constexpr (DEFER) return scale;
 #pragma unroll
   for (int k = 0; k < 8; k++) v[k] = v[k] * scale * g[k];
   quantize8_to_lds(v, live, t, n, xs);
   __syncthreads();
+  return 1.0f;
 }
 
 // rope.mojo:253 angle with scale 1 and no YaRN mix: f32(pos) * step / freq,

@@ -217,8 +217,10 @@ def test_layer_q4_k_m_kinds_match_oracle(tokens):
 def test_layer_unaligned_residual_runs_separate_norms():
     """A residual row that is not 16-byte aligned makes the batch-1 layer run
     both norms as launches of their own (the kernels with the norm folded in
-    load the row as float4): the same result as the aligned call, and the
-    oracle's."""
+    load the row as float4): both calls within the oracle's per-element
+    bound, and within it of each other (the folded kernels scale each row's
+    sum by the norm's scale rather than the activation, so the two round
+    differently)."""
     from molla_amd import block, gpu
     ctx = gpu.DeviceContext(0)
     spec = spec_of(512, 1024, 8, 2, 64)
@@ -246,11 +248,10 @@ def test_layer_unaligned_residual_runs_separate_norms():
     keep = []
     bound = layer_gate(spec, host, xr, kr, vr, pos)
     oracle.layer_step(oracle.make_layer(spec, host, keep), xr, kr, vr, pos, pos, f16_store=True, threads=8)
-    peak = np.abs(xr).max()
     for got_x, got_k, got_v in outs:
         assert_layer_close(got_x, xr, bound)
         assert np.allclose(got_k, kr, rtol=2e-3, atol=1e-3) and np.allclose(got_v, vr, rtol=2e-3, atol=1e-3)
-    assert np.abs(outs[0][0] - outs[1][0]).max() <= 1e-5 * peak
+    assert_layer_close(outs[0][0], outs[1][0], bound)
 
 
 def test_small_model_greedy_decode_matches_oracle():
