@@ -42,6 +42,8 @@
 //
 // Replaces the batched planar_matmul_kernel (src/molla/nn/gpu.mojo:1809) for
 // Q4_K and Q6_K; output y[t * ldy + r] and epilogues as gpu.mojo:1005.
+#include <type_traits>
+
 #include "matvec_rows.h"
 
 namespace mi {
@@ -438,10 +440,9 @@ __global__ __launch_bounds__(kMaxHWaves * 64) void htile_kernel(const RowSegs sg
   }
 
   // (row r, token u) sums of tile kk over the waves, in wave order, hi + lo,
-  // and the epilogue; the 16 * TN sums are dealt round the waves, so that
-  // no wave comes late to the next barrier.  GLU: a gate tile's sums wait in
-  // gsum for the up tile of the same rows (the same thread takes the same
-  // (row, token) every tile), whose act(gate) * up go to hbuf.
+  // and the epilogue.  GLU: a gate tile's sums wait in gsum for the up tile
+  // of the same rows, whose act(gate) * up go to hbuf (another wave may
+  // finish that tile: a barrier lies between the two finishes).
   __shared__ float gsum[GLU ? 2 : 1][16][TN], hbuf[GLU ? 32 : 1][TN];
   // ROPE: (cos, sin) of every (token, pair), once per block, read by the
   // finish of every tile (computed as rope_theta then float64 trig)
@@ -456,8 +457,21 @@ __global__ __launch_bounds__(kMaxHWaves * 64) void htile_kernel(const RowSegs sg
     }
   }
   auto finish = [&](int kk, int buf) __attribute__((always_inline)) {
+    // The (row, token) sums of a tile are dealt to as few waves as hold them
+    // (F of 64 sums each), a different wave for each tile: the finish's
+    // instructions cost a wave that runs them however few of its lanes are
+    // live, so spreading a few sums over every wave costs all of them.
+    constexpr int F = (16 * TN + 63) / 64;
+    int f0 = 0;  // this wave's first share
+    if constexpr (F == 1) {
+      if (wave != kk % nw) return;
+    } else {
+      f0 = wave - (kk * F) % nw;
+      if (f0 < 0) f0 += nw;
+      if (f0 >= F) return;
+    }
     const int tl = tile_of(kk);
-    for (int ix = lane * nw + wave; ix < 16 * TN; ix += 64 * nw) {
+    for (int ix = f0 * 64 + lane; ix < 16 * TN; ix += (F == 1 ? 64 : 64 * nw)) {
       const int rr = ix & 15, u = ix >> 4;
       // every wave's pair is read unconditionally (a wave past nw reads
       // the last one again and adds nothing), so the reads go out together
@@ -539,30 +553,34 @@ __global__ __launch_bounds__(kMaxHWaves * 64) void htile_kernel(const RowSegs sg
   int k = 0;
   store_tile(ra, 0);
   if (valid(2)) load_tile(ra, tile_of(2));
-  auto step_tile = [&](uint2 (&rn)[kLoads]) __attribute__((always_inline)) {
+  // P = k & 1, the buffer tile k is computed from: step_tile(rb_) always
+  // runs at even k and step_tile(ra) at odd k, so it is a constant of each
+  // call and the buffers' LDS addresses fold into the instructions' offsets.
+  auto step_tile = [&](uint2 (&rn)[kLoads], auto par) __attribute__((always_inline)) {
+    constexpr int P = decltype(par)::value;
     __syncthreads();
     if (GLU && k >= 2 && ((k - 2) & 3) == 3) quantize_group(k - 2);
-    if (k > 0) finish(k - 1, (k - 1) & 1);
+    if (k > 0) finish(k - 1, 1 - P);
     ff4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int s = 0; s < kSBW; s++) {
       if constexpr (KIND == MI_Q4_K) {
-        sb_product(wl[k & 1], wave * kSBW + s, b[s], bm[s], esc[s], lm, kq, acc);
+        sb_product(wl[P], wave * kSBW + s, b[s], bm[s], esc[s], lm, kq, acc);
       } else if (s == 0) {
-        sb_product_q6k<0>(wl[k & 1], wave * kSBW, b[0], esc[0], lm, kq, acc);
+        sb_product_q6k<0>(wl[P], wave * kSBW, b[0], esc[0], lm, kq, acc);
       } else {
-        sb_product_q6k<1>(wl[k & 1], wave * kSBW + 1, b[1], esc[1], lm, kq, acc);
+        sb_product_q6k<1>(wl[P], wave * kSBW + 1, b[1], esc[1], lm, kq, acc);
       }
     }
 #pragma unroll
-    for (int i = 0; i < 4; i++) part[k & 1][wave][4 * kq + i][lm] = acc[i];
+    for (int i = 0; i < 4; i++) part[P][wave][4 * kq + i][lm] = acc[i];
     if (!valid(k + 1)) return false;
-    store_tile(rn, (k + 1) & 1);  // tile k + 1
+    store_tile(rn, 1 - P);  // tile k + 1
     if (valid(k + 3)) load_tile(rn, tile_of(k + 3));
     k++;
     return true;
   };
-  while (step_tile(rb_) && step_tile(ra)) {
+  while (step_tile(rb_, std::integral_constant<int, 0>{}) && step_tile(ra, std::integral_constant<int, 1>{})) {
   }
   __syncthreads();
   finish(k, k & 1);
