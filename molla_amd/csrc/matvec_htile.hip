@@ -138,12 +138,18 @@ __device__ __forceinline__ void sb_product(const uint8_t* lrows, int sb, const h
   uint32_t sc_lo, sc_hi, m_lo, m_hi;
   kscales(h.y, h.z, h.w, sc_lo, sc_hi, m_lo, m_hi);
   const hh2 k1024 = {(_Float16)-1024.0f, (_Float16)-1024.0f};
-  // the 8 scales as pairs (sc 2i, sc 2i + 1) and their negated 1024 multiples;
-  // a group takes one half of its pair to both halves
+  // the 8 scales as pairs (sc 2i, sc 2i + 1 / 16) and their negated 1024
+  // multiples; a group takes one half of its pair to both halves.  An odd
+  // group's codes are the high nibbles left in place (16 u, one AND instead
+  // of a shift and an AND), so its scale is a sixteenth: 0x54 above the
+  // byte is the exponent of 64, whose half step is 1/16, and (1024 + 16 u)
+  // sc / 16 - 64 sc = u sc is one exact rounding, as for the even groups.
+  const hh2 kOff = {(_Float16)-1024.0f, (_Float16)-64.0f};
+  constexpr uint32_t kScSel01 = 0x07010400u, kScSel23 = 0x07030402u;
   hh2 scp[4], nscp[4];
 #pragma unroll
   for (int i = 0; i < 4; i++) {
-    scp[i] = as_hh2(magic2(i < 2 ? sc_lo : sc_hi, (i & 1) ? kSel23 : kSel01)) + k1024;
+    scp[i] = as_hh2(__builtin_amdgcn_perm(0x54646464u, i < 2 ? sc_lo : sc_hi, (i & 1) ? kScSel23 : kScSel01)) + kOff;
     nscp[i] = scp[i] * k1024;
   }
   ff4 c = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -154,8 +160,8 @@ __device__ __forceinline__ void sb_product(const uint8_t* lrows, int sb, const h
     const hh2 nsc = (j & 1) ? __builtin_shufflevector(nscp[j >> 1], nscp[j >> 1], 1, 1)
                             : __builtin_shufflevector(nscp[j >> 1], nscp[j >> 1], 0, 0);
     const uint32_t t0 = q[j >> 1].x, t1 = q[j >> 1].y;
-    const uint32_t u0 = (j & 1) ? (t0 >> 4) & 0x0F0F0F0Fu : t0 & 0x0F0F0F0Fu;
-    const uint32_t u1 = (j & 1) ? (t1 >> 4) & 0x0F0F0F0Fu : t1 & 0x0F0F0F0Fu;
+    const uint32_t u0 = t0 & ((j & 1) ? 0xF0F0F0F0u : 0x0F0F0F0Fu);
+    const uint32_t u1 = t1 & ((j & 1) ? 0xF0F0F0F0u : 0x0F0F0F0Fu);
     c = mfma16(codes8(u0, u1, sc, nsc), b[j], c);
   }
   // the mins of groups 0..7 as this lane's A fragment: k 0..7 and 8..15
