@@ -3,6 +3,7 @@
 
     python -m molla_amd.trace_summary DB            # every kernel of the run
     python -m molla_amd.trace_summary DB --steps N  # the last N decode steps
+    python -m molla_amd.trace_summary DB --first N  # each kernel's first N dispatches
     python -m molla_amd.trace_summary DB --steps N --cycle 'KERNEL=wo,down'
         # the same, the dispatches of KERNEL in each step labelled in turn
     python -m molla_amd.trace_summary DB --calls prefill_x_kernel --per 23
@@ -35,6 +36,8 @@ def main() -> None:
     ap.add_argument("--top", type=int, default=20)
     ap.add_argument("--calls", default="")
     ap.add_argument("--per", type=int, default=1)
+    ap.add_argument("--first", type=int, default=0,
+                    help="each kernel's first N dispatches only, with their median duration")
     ap.add_argument("--cycle", action="append", default=[],
                     help="NAME=a,b: label the dispatches of kernel NAME in each step a, b, a, b, ... in order")
     a = ap.parse_args()
@@ -62,6 +65,16 @@ def main() -> None:
                         per[n].append(d)
             cells = "; ".join(f"`{n}` {sorted(per[n])[len(per[n]) // 2]:.1f}" for n in names)
             print(f"| run {r0 // a.per} | {cells} |")
+        return
+    if a.first:
+        per = collections.defaultdict(list)
+        for name, st, en in rows:
+            if len(per[short(name)]) < a.first:
+                per[short(name)].append((en - st) / 1e3)
+        print("| kernel | calls | avg us | median us |")
+        print("|---|---|---|---|")
+        for k, d in sorted(per.items(), key=lambda kv: -sum(kv[1]))[: a.top]:
+            print(f"| `{k}` | {len(d)} | {sum(d) / len(d):.2f} | {sorted(d)[len(d) // 2]:.2f} |")
         return
     n = 1
     if a.steps:
