@@ -165,17 +165,18 @@ __device__ __forceinline__ void sb_product(const uint8_t* lrows, int sb, const h
     c = mfma16(codes8(u0, u1, sc, nsc), b[j], c);
   }
   // the mins of groups 0..7 as this lane's A fragment: k 0..7 and 8..15
-  // (the hi and lo group sums) both take m0..m7; k 16..31 are zero
+  // (the hi and lo group sums) both take m0..m7
   const uint4 am = make_uint4(magic2(m_lo, kSel01), magic2(m_lo, kSel23), magic2(m_hi, kSel01),
                               magic2(m_hi, kSel23));
   const _Float16 n = (_Float16)-1024.0f;
-  hh8 a_m = as_hh8(am) + hh8{n, n, n, n, n, n, n, n};
-  if (kq >= 2) a_m = hh8{0, 0, 0, 0, 0, 0, 0, 0};
+  // (lanes kq >= 2 hold k 16..31, where bm is zero: their finite mins add
+  // nothing, so they are not cleared)
+  const hh8 a_m = as_hh8(am) + hh8{n, n, n, n, n, n, n, n};
   const ff4 cm = mfma16(a_m, bm, ff4{0.0f, 0.0f, 0.0f, 0.0f});
 #pragma unroll
   for (int i = 0; i < 4; i++) {
     const float di = half_bits_to_float(dd[i]), mi_ = half_bits_to_float(dd[i] >> 16);
-    acc[i] = fmaf(esc, fmaf(di, c[i], -256.0f * mi_ * cm[i]), acc[i]);
+    acc[i] = fmaf(esc, fmaf(mi_, cm[i] * -256.0f, di * c[i]), acc[i]);
   }
 }
 
