@@ -989,6 +989,176 @@ __global__ __launch_bounds__(NT) void attend_wide_kernel(
     *(float2*)(part_acc + (slot0 + (int64_t)g * max_chunks + c) * D + 2 * e) = make_float2(a0, a1);
 }
 
+// attend_mfma_kernel: the same slice as attend_wide_kernel (one 64-key
+// slice x one key head x one token, f16 cache, GROUP <= 4 query heads of
+// head_dim D), with both products on the matrix cores
+// (v_mfma_f32_16x16x32_f16), as attend_chunk_kernel computes them for a
+// prefill chunk.  At 4 and 8 sequences the VALU dot loops of the wide
+// kernel bound its time; here a block of 256 threads does
+//   * S = K Q^T: wave w takes keys 16w..16w+15 as the A rows, read straight
+//     from the cache into fragments; the N columns are the GROUP queries as
+//     three halves each (q1 = f16(q), q2 = f16(q - q1), q3 = f16(q - q1 -
+//     q2): every bit of the f32 query), staged once in LDS, so a score is
+//     the sum of three columns;
+//   * the slice softmax, one wave per query head (lane = key), as the wide
+//     kernel;
+//   * O = P V: P as two halves (rows h and GROUP + h), V staged by rows
+//     (exact halves); wave w takes D / 64 of the D / 16 column tiles.
+// MFMA fragments (16x16x32): lane l holds row / column l % 16 and values
+// 8 (l / 16) .. +8 of the 32; result element i of lane l is row 4 (l / 16)
+// + i, column l % 16.  The partial sums land where attend_wide_kernel
+// writes them.
+template <int GROUP, int D>
+__global__ __launch_bounds__(256) void attend_mfma_kernel(
+    const float* __restrict__ q, int64_t q_stride, const __half* __restrict__ kc, const __half* __restrict__ vc,
+    int64_t cache_stride, int heads, int kv_heads, float scale, const int32_t* __restrict__ pos_dev,
+    int count_host, int max_chunks, float* __restrict__ part_acc, float* __restrict__ part_ml,
+    const int32_t* __restrict__ kv_index, int64_t index_stride) {
+  static_assert(GROUP == 1 || GROUP == 2 || GROUP == 4, "three halves of GROUP queries fill at most 12 columns");
+  static_assert(D == 64 || D == 128, "head_dim 64 or 128");
+  constexpr int KK = kWideKeys, QP = D + 8, KP = KK + 8;
+  constexpr int PIECES = D / 8, PER = KK * PIECES / 256;
+  __shared__ __align__(16) _Float16 Qh[3 * GROUP * QP];
+  __shared__ __align__(16) _Float16 Vr[KK * QP];
+  __shared__ __align__(16) _Float16 Ph[2 * GROUP * KP];
+  __shared__ float Ss[GROUP * KK];
+  const int c = blockIdx.x, kvh = blockIdx.y, t = blockIdx.z;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int lm = lane & 15, lk = lane >> 4;
+  const int count = pos_dev ? pos_dev[t] + 1 : count_host;
+  const int start = c * KK;
+  if (start >= count) return;
+  const int nk = min(KK, count - start);
+  const int kvw = kv_heads * D;
+  const int64_t seq = kv_index ? 0 : (int64_t)t * cache_stride;
+
+  // this wave's 16 keys as A fragments (key 16 wave + lm, values 32 ks +
+  // 8 lk .. +8), the block's share of the values, and the queries; keys past
+  // the end repeat the last live one (masked below)
+  const __half* kb = kc + seq + (int64_t)kvh * D;
+  const __half* vb = vc + seq + (int64_t)kvh * D;
+  att_h8 ka[D / 32];
+  {
+    const int cell = max(kv_cell(kv_index, index_stride, t, start + min(16 * wave + lm, nk - 1)), 0);
+#pragma unroll
+    for (int ks = 0; ks < D / 32; ks++) ka[ks] = *(const att_h8*)(kb + (int64_t)cell * kvw + 32 * ks + 8 * lk);
+  }
+  uint4 vraw[PER];
+#pragma unroll
+  for (int j = 0; j < PER; j++) {
+    const int i = tid + j * 256;
+    const int key = i / PIECES, pc = i % PIECES;
+    const int cell = max(kv_cell(kv_index, index_stride, t, start + min(key, nk - 1)), 0);
+    vraw[j] = *(const uint4*)(vb + (int64_t)cell * kvw + pc * 8);
+  }
+  constexpr int NQ4 = GROUP * D / 4;
+  const float* qg = q + (int64_t)t * q_stride + (int64_t)kvh * GROUP * D;
+  const float4 qv = ((const float4*)qg)[tid < NQ4 ? tid : 0];
+  if (tid < NQ4) {
+    // query h = tid / (D / 4), dims 4 (tid % (D / 4)) .. +4, as three halves
+    const int h = tid / (D / 4), d0 = 4 * (tid % (D / 4));
+    const float qf[4] = {qv.x, qv.y, qv.z, qv.w};
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      const _Float16 h1 = (_Float16)qf[u];
+      const float r1 = qf[u] - (float)h1;  // exact
+      const _Float16 h2 = (_Float16)r1;
+      Qh[(0 * GROUP + h) * QP + d0 + u] = h1;
+      Qh[(1 * GROUP + h) * QP + d0 + u] = h2;
+      Qh[(2 * GROUP + h) * QP + d0 + u] = (_Float16)(r1 - (float)h2);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < PER; j++) {
+    const int i = tid + j * 256;
+    const int key = i / PIECES, pc = i % PIECES;
+    *(uint4*)(Vr + key * QP + pc * 8) = vraw[j];
+  }
+  __syncthreads();
+
+  // S for keys 16 wave .. +15 against column lm = (half lm / GROUP, query
+  // lm % GROUP); columns from 3 GROUP on are zero
+  {
+    att_f4 sacc = att_f4{0.0f, 0.0f, 0.0f, 0.0f};
+    const bool qcol = lm < 3 * GROUP;
+    const int qrow = qcol ? lm : 0;
+#pragma unroll
+    for (int ks = 0; ks < D / 32; ks++) {
+      const att_h8 qb = *(const att_h8*)(Qh + qrow * QP + 32 * ks + 8 * lk);
+      sacc = att_mfma(ka[ks], qcol ? qb : att_h8{0, 0, 0, 0, 0, 0, 0, 0}, sacc);
+    }
+    // lanes lm < GROUP: the score of query lm at keys 16 wave + 4 lk + i,
+    // its three halves added in order
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const float s2 = __shfl(sacc[i], lane + GROUP), s3 = __shfl(sacc[i], lane + 2 * GROUP);
+      const float sc = (sacc[i] + s2) + s3;
+      const int key = 16 * wave + 4 * lk + i;
+      const bool live = key < nk && (!kv_index || kv_cell(kv_index, index_stride, t, start + key) >= 0);
+      if (lm < GROUP) Ss[lm * KK + key] = live ? sc * scale : -INFINITY;
+    }
+  }
+  __syncthreads();
+  const int64_t slot0 = ((int64_t)t * heads + (int64_t)kvh * GROUP) * max_chunks;
+  // slice softmax: wave g takes query g, lane = key; P as two halves
+  if (wave < GROUP) {
+    const float sc = Ss[wave * KK + lane];
+    const float m = lanes::reduce<64>(sc, lanes::Max{});
+    const float pr = sc == -INFINITY ? 0.0f : expf(sc - m);
+    const float l = lanes::reduce<64>(pr, lanes::Add{});
+    const _Float16 ph = (_Float16)pr;
+    Ph[wave * KP + lane] = ph;
+    Ph[(GROUP + wave) * KP + lane] = (_Float16)(pr - (float)ph);
+    if (lane == 0) *(float2*)(part_ml + (slot0 + (int64_t)wave * max_chunks + c) * 2) = make_float2(m, l);
+  }
+  __syncthreads();
+  // O for column tiles nt = wave, wave + 4, ...: rows (half, query) =
+  // 4 lk + i, column = dim 16 nt + lm; rows from 2 GROUP on are zero
+  {
+    const bool prow = lm < 2 * GROUP;
+    const int arow = prow ? lm : 0;
+    att_h8 pa[KK / 32];
+#pragma unroll
+    for (int ks = 0; ks < KK / 32; ks++) {
+      const att_h8 a = *(const att_h8*)(Ph + arow * KP + 32 * ks + 8 * lk);
+      pa[ks] = prow ? a : att_h8{0, 0, 0, 0, 0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int nt = wave; nt < D / 16; nt += 4) {
+      att_f4 oacc = att_f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int ks = 0; ks < KK / 32; ks++)
+      {
+        // the B fragment (dim 16 nt + lm, keys 32 ks + 8 lk .. +8) gathered
+        // from the row-major values: staging them transposed (a 2-byte
+        // store per value, 8-way bank conflicts) took the kernel from 10.5
+        // to 17.9 us at 4 sequences
+        att_h8 vb;
+#pragma unroll
+        for (int e = 0; e < 8; e++) vb[e] = Vr[(32 * ks + 8 * lk + e) * QP + 16 * nt + lm];
+        oacc = att_mfma(pa[ks], vb, oacc);
+      }
+      const int dim = 16 * nt + lm;
+      // query g's output: row g (hi) plus row GROUP + g (lo)
+      if constexpr (GROUP == 4) {
+        // rows 0..3 in lanes lk = 0, rows 4..7 in lanes lk = 1
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const float lo = __shfl(oacc[i], lane + 16);
+          if (lk == 0) part_acc[(slot0 + (int64_t)i * max_chunks + c) * D + dim] = oacc[i] + lo;
+        }
+      } else if constexpr (GROUP == 2) {
+        if (lk == 0) {
+          part_acc[(slot0 + 0 * (int64_t)max_chunks + c) * D + dim] = oacc[0] + oacc[2];
+          part_acc[(slot0 + 1 * (int64_t)max_chunks + c) * D + dim] = oacc[1] + oacc[3];
+        }
+      } else {
+        if (lk == 0) part_acc[(slot0 + c) * D + dim] = oacc[0] + oacc[1];
+      }
+    }
+  }
+}
+
 // attend_wide_q8_kernel: attend_wide_kernel over a q8_0 cache (the row's
 // quants of every key head, then its factors: cache_row), the arithmetic of
 // attend_split_q8_kernel (each key or value element float(quant) *
@@ -1463,8 +1633,9 @@ int launch_attend(hipStream_t s, const float* q, int64_t q_stride, const uint16_
   const size_t acc_bytes = ((size_t)slots * head_dim * sizeof(float) + 255) & ~(size_t)255;
   float* part_ml = (float*)((char*)work + acc_bytes);
   const int group = heads / kv_heads;
-  // decode (at most 8 tokens, one each per sequence, f16 cache): the
-  // 1024-thread slice kernel
+  // decode (at most 8 tokens, one each per sequence): the matrix-core slice
+  // kernel for an f16 cache and up to 4 query heads a key head, else the
+  // wide VALU slice kernel (1024 threads at one token, 512 for a batch)
   if (tokens <= kMaxTokens && (head_dim == 64 || head_dim == 128) &&
       (form != MI_CACHE_Q8 || wide_q8_fits(group, head_dim, tokens == 1 ? 1024 : 512))) {
     dim3 grid(chunks, kv_heads, tokens);
@@ -1478,6 +1649,10 @@ int launch_attend(hipStream_t s, const float* q, int64_t q_stride, const uint16_
     hipLaunchKernelGGL((attend_wide_q8_kernel<G, DD, 512>), grid, dim3(512), 0, s, q, q_stride,              \
                        (const __half*)k_cache, (const __half*)v_cache, cache_stride, qrow, heads, kv_heads,   \
                        scale, pos_dev, count_host, chunks, part_acc, part_ml, kv_index, index_stride);        \
+  else if (G <= 4)                                                                                           \
+    hipLaunchKernelGGL((attend_mfma_kernel<(G <= 4 ? G : 4), DD>), grid, dim3(256), 0, s, q, q_stride,        \
+                       (const __half*)k_cache, (const __half*)v_cache, cache_stride, heads, kv_heads, scale,   \
+                       pos_dev, count_host, chunks, part_acc, part_ml, kv_index, index_stride);               \
   else if (tokens == 1)                                                                                      \
     hipLaunchKernelGGL((attend_wide_kernel<G, DD, 1024>), grid, dim3(1024), 0, s, q, q_stride,               \
                        (const __half*)k_cache, (const __half*)v_cache, cache_stride, heads, kv_heads, scale,   \
