@@ -470,6 +470,10 @@ __device__ __forceinline__ att_f4 att_mfma(att_h8 a, att_h8 b, att_f4 c) {
 }
 
 constexpr int kChunkKeys = 64;
+// The matrix-core slices split P (at most 1) into two halves after lifting
+// it by 2^14, and scale the sums back: exact powers of two, which keep the
+// low halves of weights down to ~1e-8 out of the f16 subnormals.
+constexpr float kPLift = 16384.0f, kPDrop = 1.0f / 16384.0f;
 __host__ __device__ __forceinline__ int attn_chunk_pad(int d) { return d + 8; }  // halves per LDS row
 __host__ __device__ __forceinline__ size_t attn_chunk_lds_bytes(int head_dim) {
   const int dp = attn_chunk_pad(head_dim), kp = kChunkKeys + 8;
@@ -608,7 +612,7 @@ __global__ __launch_bounds__(256) void attend_chunk_kernel(
   for (int i = 0; i < 4; i++)
 #pragma unroll
     for (int nt = 0; nt < 4; nt++) {
-      const float p = pv[i][nt];
+      const float p = pv[i][nt] * kPLift;  // see kPLift
       const _Float16 h = (_Float16)p;
       ph[(4 * lk + i) * KP + 16 * nt + lm] = h;
       pl[(4 * lk + i) * KP + 16 * nt + lm] = (_Float16)(p - (float)h);
@@ -635,7 +639,7 @@ __global__ __launch_bounds__(256) void attend_chunk_kernel(
     const int r = row0 + 4 * lk + i, t = t0 + r / GROUP, h = kvh * GROUP + r % GROUP;
     const int64_t slot = ((int64_t)t * heads + h) * max_chunks + c;
 #pragma unroll
-    for (int nt = 0; nt < D / 16; nt++) part_acc[slot * D + 16 * nt + lm] = oacc[nt][i];
+    for (int nt = 0; nt < D / 16; nt++) part_acc[slot * D + 16 * nt + lm] = oacc[nt][i] * kPDrop;
     if (lm == 0) {
       part_ml[slot * 2 + 0] = mrow[i];
       part_ml[slot * 2 + 1] = lrow[i];
@@ -1106,9 +1110,12 @@ __global__ __launch_bounds__(256) void attend_mfma_kernel(
     const float m = lanes::reduce<64>(sc, lanes::Max{});
     const float pr = sc == -INFINITY ? 0.0f : expf(sc - m);
     const float l = lanes::reduce<64>(pr, lanes::Add{});
-    const _Float16 ph = (_Float16)pr;
+    // P lifted by 2^14 (exact; p <= 1 stays below the largest half) so that
+    // the low halves of small weights are not f16 subnormals
+    const float pl = pr * kPLift;
+    const _Float16 ph = (_Float16)pl;
     Ph[wave * KP + lane] = ph;
-    Ph[(GROUP + wave) * KP + lane] = (_Float16)(pr - (float)ph);
+    Ph[(GROUP + wave) * KP + lane] = (_Float16)(pl - (float)ph);
     if (lane == 0) *(float2*)(part_ml + (slot0 + (int64_t)wave * max_chunks + c) * 2) = make_float2(m, l);
   }
   __syncthreads();
@@ -1145,15 +1152,15 @@ __global__ __launch_bounds__(256) void attend_mfma_kernel(
 #pragma unroll
         for (int i = 0; i < 4; i++) {
           const float lo = __shfl(oacc[i], lane + 16);
-          if (lk == 0) part_acc[(slot0 + (int64_t)i * max_chunks + c) * D + dim] = oacc[i] + lo;
+          if (lk == 0) part_acc[(slot0 + (int64_t)i * max_chunks + c) * D + dim] = (oacc[i] + lo) * kPDrop;
         }
       } else if constexpr (GROUP == 2) {
         if (lk == 0) {
-          part_acc[(slot0 + 0 * (int64_t)max_chunks + c) * D + dim] = oacc[0] + oacc[2];
-          part_acc[(slot0 + 1 * (int64_t)max_chunks + c) * D + dim] = oacc[1] + oacc[3];
+          part_acc[(slot0 + 0 * (int64_t)max_chunks + c) * D + dim] = (oacc[0] + oacc[2]) * kPDrop;
+          part_acc[(slot0 + 1 * (int64_t)max_chunks + c) * D + dim] = (oacc[1] + oacc[3]) * kPDrop;
         }
       } else {
-        if (lk == 0) part_acc[(slot0 + c) * D + dim] = oacc[0] + oacc[1];
+        if (lk == 0) part_acc[(slot0 + c) * D + dim] = (oacc[0] + oacc[1]) * kPDrop;
       }
     }
   }

@@ -373,6 +373,31 @@ def test_attention(ctx, count):
     assert np.abs(got - want).max() <= 1e-5 * np.abs(want).max()
 
 
+@pytest.mark.parametrize("count", [5, 300, 2049])
+@pytest.mark.parametrize("heads,kv,hd,qmul", [
+    (32, 8, 128, 1.0),   # groups of 4 (the matrix-core slice kernel)
+    (32, 8, 128, 4.0),   # peaky scores: weights down to ~1e-30 in a slice
+    (8, 2, 64, 1.0),     # groups of 4, head_dim 64
+    (4, 2, 128, 4.0),    # groups of 2
+    (2, 2, 64, 1.0),     # groups of 1
+    (16, 2, 128, 1.0),   # groups of 8 (the VALU slice kernel)
+])
+def test_attention_groups(ctx, count, heads, kv, hd, qmul):
+    """f16-cache attention of one token for every query-group size and head
+    width the decode slice kernels take, against the oracle."""
+    from molla_amd import gpu
+    kvw = kv * hd
+    q = (synth.normal(heads * hd, 31).numpy() * np.float32(qmul)).astype(np.float32)
+    kh = synth.normal(count * kvw, 32).half()
+    vh = synth.normal(count * kvw, 33).half()
+    scale = float(np.float32(1 / np.sqrt(hd)))
+    want = oracle.attend(heads, kv, hd, scale, q, kh.float().numpy(), vh.float().numpy(), count)
+    out = torch.zeros(heads * hd, device="cuda")
+    gpu.device_attend(ctx, torch.from_numpy(q).cuda(), kh.cuda(), vh.cuda(), heads, kv, hd, scale, count, out)
+    got = out.cpu().numpy()
+    assert np.abs(got - want).max() <= 1e-5 * np.abs(want).max()
+
+
 def q8_rows(values, kvw):
     """Host encoding of f32 rows into q8_0 cache rows (tests/test_gpu_ops.mojo
     _quantize_q8 rule), as the uint16 halves the device cache holds."""
