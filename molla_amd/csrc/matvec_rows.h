@@ -86,6 +86,28 @@ __device__ __forceinline__ float wave_sum_rows4(float a0, float a1, float a2, fl
   return lanes::reduce<16>(z, lanes::Add{});
 }
 
+// The same for eight values: lane l ends with the sum of value
+// (g & 1) + 2 h + 4 (g >> 1), g = l / 16, h = l / 8 % 2, so value r sits 32
+// lanes below value r + 4.  After the half and row swaps, each 8-lane half
+// of a row keeps one of its two values and adds its partner half's (row
+// rotate by 8), and an 8-lane sum finishes.
+__device__ __forceinline__ float wave_sum_rows8(const float (&a)[8]) {
+  float x[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(a[i]), __float_as_uint(a[i + 4]), false, false);
+    x[i] = __uint_as_float(p[0]) + __uint_as_float(p[1]);  // lanes < 32: value i, else i + 4
+  }
+  const auto p01 = __builtin_amdgcn_permlane16_swap(__float_as_uint(x[0]), __float_as_uint(x[1]), false, false);
+  const auto p23 = __builtin_amdgcn_permlane16_swap(__float_as_uint(x[2]), __float_as_uint(x[3]), false, false);
+  const float z0 = __uint_as_float(p01[0]) + __uint_as_float(p01[1]);  // rows 0, 1, 4, 5 of 16 lanes
+  const float z1 = __uint_as_float(p23[0]) + __uint_as_float(p23[1]);  // rows 2, 3, 6, 7
+  const bool hi = (__lane_id() & 8) != 0;
+  const float keep = hi ? z1 : z0, send = hi ? z0 : z1;
+  const float w = keep + __uint_as_float(lanes::dpp<0x128>(__float_as_uint(send)));  // row_ror:8
+  return lanes::reduce<8>(w, lanes::Add{});
+}
+
 // Activation of one lane's 64-value unit (groups 2u and 2u + 1); the
 // per-half limb sums of plane 7 only for the kinds with an offset (Q4_0).
 template <bool L23>

@@ -79,21 +79,19 @@ __global__ __launch_bounds__(8 * 64) void glu_norm_kernel(const RowSegs sg, int 
   // wave's weights had arrived.  The launcher keeps a block to at most
   // kGluIts groups.
   // this group's sums, store and act(gate) * up into LDS
+  // the eight sums by a transposed reduction (wave_sum_rows8): gate row r
+  // in lanes 8 h + 16 k with r = k + 2 h, its up row 32 lanes higher
   auto finish = [&](float (&acc)[NR], int it) __attribute__((always_inline)) {
-#pragma unroll
-    for (int r = 0; r < NR; r++) acc[r] = wave_sum(acc[r]);
-    float v = acc[0];
-#pragma unroll
-    for (int r = 1; r < NR; r++)
-      if (lane == r) v = acc[r];
+    float v = rows::wave_sum_rows8(acc);
     if constexpr (kNormDefer) v *= nsc;
-    const float upv = __shfl_down(v, RPW);
+    const float upv = __shfl_down(v, 32);
     const float o = ((epi & MI_ACT_GELU) ? gelu(v) : silu(v)) * upv;
     const int row0 = (g * 8 + wave) * RPW;
-    if (lane < RPW) {
-      if (epi & MI_EPI_ADD) y[row0 + lane] += o;
-      else y[row0 + lane] = o;
-      grp[it][wave * RPW + lane] = o;
+    const int r = ((lane >> 4) & 1) + 2 * ((lane >> 3) & 1);
+    if (lane < 32 && (lane & 7) == 0) {
+      if (epi & MI_EPI_ADD) y[row0 + r] += o;
+      else y[row0 + r] = o;
+      grp[it][wave * RPW + r] = o;
     }
   };
   int it = 0;
