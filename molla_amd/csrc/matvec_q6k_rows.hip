@@ -146,10 +146,12 @@ __global__ __launch_bounds__(256) void q6k_rows_kernel(const uint8_t* __restrict
   // a unit's block address within any row: rb is a multiple of 2, rows are
   // 4-byte aligned at the base, so each (row, unit) realigns by 0 or 2 bytes
   const int64_t uoff = (int64_t)sb * 210;
+  // (pointer arithmetic, not integer casts: a pointer rebuilt from an
+  // integer loses its global address space and its loads become flat ones)
   auto blk = [&](int row, uint32_t& sh) {
-    const uintptr_t addr = (uintptr_t)(w + (int64_t)row * rb + uoff);
-    sh = (uint32_t)(addr & 3u);
-    return (const uint8_t*)(addr - sh);
+    const uint8_t* p = w + (int64_t)row * rb + uoff;
+    sh = (uint32_t)((uintptr_t)p & 3u);
+    return p - sh;
   };
 
   int row = wv;
@@ -193,17 +195,123 @@ __global__ __launch_bounds__(256) void q6k_rows_kernel(const uint8_t* __restrict
   }
 }
 
+constexpr int kQ6RowsPerWave = 128;  // rows a wave of q6k_rows2_kernel takes at most
+
+// One wave a row (4096 columns or fewer) with NP - 1 rows' loads in flight
+// behind the one being computed: NP pieces a lane in a fixed rotation (the
+// loop body takes NP rows, so no piece is copied and each compute waits
+// only for its own loads).  A row past the end is clamped to the last one
+// and its sum dropped, so no load sits under a branch; the sums wait in LDS
+// and go out at the end.  Plain rows only (no epilogue operand to load).
+// The 128256x4096 head, cold: 84.7 us for q6k_rows_kernel<1> (four waves a
+// SIMD, one row ahead), 75.2 us with NP = 3 at two waves a SIMD (NP = 4 or
+// 5 at two waves, or 4 or 6 at one wave, 76-79 us).
+template <int NP>
+__global__ __launch_bounds__(256) void q6k_rows2_kernel(const uint8_t* __restrict__ w, int64_t rb, int rows,
+                                                        int cols, const uint8_t* __restrict__ xq,
+                                                        float* __restrict__ y) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int nw = gridDim.x * 4;
+  const int units = cols >> 6;
+  const bool act = lane < units;
+  const int u = act ? lane : units - 1;
+  const int sb = u >> 2, n = (u >> 1) & 1, a = u & 1;
+  const int g0 = 8 * sb + 4 * n + a, g1 = g0 + 2;
+
+  XQ6Regs x;
+  {
+    const XAcc xa{xq, 4 * (int64_t)cols, (int64_t)(cols >> 5) * 16};
+    const int gs[2] = {g0, g1};
+#pragma unroll
+    for (int e = 0; e < 2; e++) {
+#pragma unroll
+      for (int j = 0; j < 3; j++)
+#pragma unroll
+        for (int hh = 0; hh < 2; hh++) x.l[e][j][hh] = xa.limb(0, j, hh, gs[e]);
+      const XMeta m = xa.meta(0, gs[e]);
+      const int2 l23 = xa.lsum23(0, gs[e]);
+      x.scale[e] = m.scale;
+      x.lsum1[e][0] = m.lsum1[0];
+      x.lsum1[e][1] = m.lsum1[1];
+      x.lsum23[e][0] = l23.x;
+      x.lsum23[e][1] = l23.y;
+    }
+  }
+  const int64_t uoff = (int64_t)sb * 210;
+  auto load_row = [&](Q6Piece& p, uint32_t& sh, int row) __attribute__((always_inline)) {
+    const uint8_t* q = w + (int64_t)min(row, rows - 1) * rb + uoff;
+    sh = (uint32_t)((uintptr_t)q & 3u);
+    load_piece(p, q - sh, sh, n, a);
+  };
+  int row = blockIdx.x * 4 + wave;
+  if (row >= rows) return;
+  const int row0 = row;
+  __shared__ float res[4][kQ6RowsPerWave];
+  int k = 0;
+  Q6Piece pc[NP];
+  uint32_t sh[NP];
+#pragma unroll
+  for (int j = 0; j < NP - 1; j++) load_row(pc[j], sh[j], row + j * nw);
+  // compute `use` (row r), after sending for row r + (NP - 1) nw into `refill`
+  auto step = [&](Q6Piece& use, uint32_t& su, Q6Piece& refill, uint32_t& sr) __attribute__((always_inline)) {
+    __builtin_amdgcn_sched_barrier(0);
+    load_row(refill, sr, row + (NP - 1) * nw);
+    __builtin_amdgcn_sched_barrier(0);
+    float v = piece_dot(use, su, a, x);
+    v = wave_sum(act ? v : 0.0f);
+    if (lane == 0) res[wave][k] = v;
+    __builtin_amdgcn_sched_barrier(0);
+    k++;
+    row += nw;
+    return row < rows;
+  };
+  // one pass over the ring: piece j computed, piece j - 1 refilled
+  auto ring = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < NP; j++)
+      if (!step(pc[j], sh[j], pc[(j + NP - 1) % NP], sh[(j + NP - 1) % NP])) return false;
+    return true;
+  };
+  // the first pass peeled, so the loop is entered from the state its back
+  // edge leaves (the compiler's waits at a loop head cover every path)
+  if (ring())
+    while (ring()) {}
+  // the sums go out at the end: a global store inside the loop let the
+  // compiler wait for the loads in flight before reusing its registers
+  for (int i = lane; i < k; i += 64) y[row0 + i * nw] = res[wave][i];
+}
+
 }  // namespace
 
 bool q6k_rows_fits(int32_t cols, int64_t row_bytes) {
   return cols > 0 && cols % 256 == 0 && cols / 64 <= 4 * 64 && row_bytes % 4 == 0;
 }
 
+#ifndef MI_Q6_DEEP
+#define MI_Q6_DEEP 1
+#endif
+#ifndef MI_Q6_DEEP_WAVES
+#define MI_Q6_DEEP_WAVES 2
+#endif
+constexpr bool kQ6Deep = MI_Q6_DEEP;
+constexpr int kQ6DeepWaves = MI_Q6_DEEP_WAVES;
+#ifndef MI_Q6_PIECES
+#define MI_Q6_PIECES 3
+#endif
+constexpr int kQ6Pieces = MI_Q6_PIECES;
+
 int launch_q6k_rows(hipStream_t s, const void* w, int64_t row_bytes, int32_t rows, int32_t cols, const void* xq,
                     float* y, int32_t epi, const float* aux) {
   if (((uintptr_t)w & 3) || row_bytes % 4) return fail(MI_ERR_ALIGN, "matvec: Q6_K rows must be 4-byte aligned");
   const int ks = (cols / 64 + 63) / 64;  // waves a row takes
-  if (ks == 1) {
+  const int deep_waves = std::min(rows, 256 * 4 * kQ6DeepWaves);
+  if (ks == 1 && kQ6Deep && epi == MI_EPI_NONE && rows <= (int64_t)deep_waves * kQ6RowsPerWave) {
+    // three waves per SIMD (the three-piece ring takes ~150 registers)
+    const int waves = deep_waves;
+    const int blocks = (waves + 3) / 4;
+    hipLaunchKernelGGL(q6k_rows2_kernel<kQ6Pieces>, dim3(blocks), dim3(256), 0, s, (const uint8_t*)w, row_bytes, rows, cols,
+                       (const uint8_t*)xq, y);
+  } else if (ks == 1) {
     // four waves per SIMD over the whole chip; each wave then streams rows
     const int waves = std::min(rows, 256 * 4 * 4);
     const int blocks = (waves + 3) / 4;
