@@ -1012,12 +1012,17 @@ __global__ __launch_bounds__(NT) void attend_wide_kernel(
 // 8 (l / 16) .. +8 of the 32; result element i of lane l is row 4 (l / 16)
 // + i, column l % 16.  The partial sums land where attend_wide_kernel
 // writes them.
-template <int GROUP, int D>
+// PAGED: kv_index maps positions to cache cells; without it the cell is
+// the position, and no index load sits under a branch (which would make the
+// compiler wait for every load in flight at the join: the keys before the
+// values went out).
+template <int GROUP, int D, bool PAGED>
 __global__ __launch_bounds__(256) void attend_mfma_kernel(
     const float* __restrict__ q, int64_t q_stride, const __half* __restrict__ kc, const __half* __restrict__ vc,
     int64_t cache_stride, int heads, int kv_heads, float scale, const int32_t* __restrict__ pos_dev,
     int count_host, int max_chunks, float* __restrict__ part_acc, float* __restrict__ part_ml,
-    const int32_t* __restrict__ kv_index, int64_t index_stride) {
+    const int32_t* __restrict__ kv_index_arg, int64_t index_stride) {
+  const int32_t* __restrict__ kv_index = PAGED ? kv_index_arg : nullptr;
   static_assert(GROUP == 1 || GROUP == 2 || GROUP == 4, "three halves of GROUP queries fill at most 12 columns");
   static_assert(D == 64 || D == 128, "head_dim 64 or 128");
   constexpr int KK = kWideKeys, QP = D + 8, KP = KK + 8;
@@ -1041,42 +1046,54 @@ __global__ __launch_bounds__(256) void attend_mfma_kernel(
   // the end repeat the last live one (masked below)
   const __half* kb = kc + seq + (int64_t)kvh * D;
   const __half* vb = vc + seq + (int64_t)kvh * D;
+  // the queries first, then the keys, then the values: loads complete in
+  // issue order, so the query halves wait only for the queries and the
+  // scores only for the keys, while the values are still arriving
+  constexpr int NQ4 = GROUP * D / 4;
+  const float* qg = q + (int64_t)t * q_stride + (int64_t)kvh * GROUP * D;
+  const att_f4 qv = ((const att_f4*)qg)[tid < NQ4 ? tid : 0];
+  __builtin_amdgcn_sched_barrier(0);
   att_h8 ka[D / 32];
   {
     const int cell = max(kv_cell(kv_index, index_stride, t, start + min(16 * wave + lm, nk - 1)), 0);
 #pragma unroll
     for (int ks = 0; ks < D / 32; ks++) ka[ks] = *(const att_h8*)(kb + (int64_t)cell * kvw + 32 * ks + 8 * lk);
   }
-  uint4 vraw[PER];
+  // (native vectors: an array of HIP's uint4 struct went to scratch)
+  att_h8 vraw[PER];
 #pragma unroll
   for (int j = 0; j < PER; j++) {
     const int i = tid + j * 256;
     const int key = i / PIECES, pc = i % PIECES;
     const int cell = max(kv_cell(kv_index, index_stride, t, start + min(key, nk - 1)), 0);
-    vraw[j] = *(const uint4*)(vb + (int64_t)cell * kvw + pc * 8);
+    vraw[j] = *(const att_h8*)(vb + (int64_t)cell * kvw + pc * 8);
   }
-  constexpr int NQ4 = GROUP * D / 4;
-  const float* qg = q + (int64_t)t * q_stride + (int64_t)kvh * GROUP * D;
-  const float4 qv = ((const float4*)qg)[tid < NQ4 ? tid : 0];
-  if (tid < NQ4) {
+  __builtin_amdgcn_sched_barrier(0);
+  {
     // query h = tid / (D / 4), dims 4 (tid % (D / 4)) .. +4, as three halves
-    const int h = tid / (D / 4), d0 = 4 * (tid % (D / 4));
-    const float qf[4] = {qv.x, qv.y, qv.z, qv.w};
+    // (computed by every thread, so the query load is not sunk into the
+    // branch behind the keys and values; threads past NQ4 store nothing)
+    const int h = (tid < NQ4 ? tid : 0) / (D / 4), d0 = 4 * ((tid < NQ4 ? tid : 0) % (D / 4));
+    float qf[4] = {qv.x, qv.y, qv.z, qv.w};
+    // here, not inside the branch below (where the compiler would sink the
+    // query load, behind the keys and values)
+    asm volatile("" : "+v"(qf[0]), "+v"(qf[1]), "+v"(qf[2]), "+v"(qf[3]));
+    _Float16 hv[3][4];
 #pragma unroll
     for (int u = 0; u < 4; u++) {
       const _Float16 h1 = (_Float16)qf[u];
       const float r1 = qf[u] - (float)h1;  // exact
       const _Float16 h2 = (_Float16)r1;
-      Qh[(0 * GROUP + h) * QP + d0 + u] = h1;
-      Qh[(1 * GROUP + h) * QP + d0 + u] = h2;
-      Qh[(2 * GROUP + h) * QP + d0 + u] = (_Float16)(r1 - (float)h2);
+      hv[0][u] = h1;
+      hv[1][u] = h2;
+      hv[2][u] = (_Float16)(r1 - (float)h2);
     }
-  }
+    if (tid < NQ4) {
 #pragma unroll
-  for (int j = 0; j < PER; j++) {
-    const int i = tid + j * 256;
-    const int key = i / PIECES, pc = i % PIECES;
-    *(uint4*)(Vr + key * QP + pc * 8) = vraw[j];
+      for (int k = 0; k < 3; k++)
+#pragma unroll
+        for (int u = 0; u < 4; u++) Qh[(k * GROUP + h) * QP + d0 + u] = hv[k][u];
+    }
   }
   __syncthreads();
 
@@ -1101,6 +1118,14 @@ __global__ __launch_bounds__(256) void attend_mfma_kernel(
       const bool live = key < nk && (!kv_index || kv_cell(kv_index, index_stride, t, start + key) >= 0);
       if (lm < GROUP) Ss[lm * KK + key] = live ? sc * scale : -INFINITY;
     }
+  }
+  // the values into LDS once the scores are out (they are read after the
+  // softmax barrier)
+#pragma unroll
+  for (int j = 0; j < PER; j++) {
+    const int i = tid + j * 256;
+    const int key = i / PIECES, pc = i % PIECES;
+    *(att_h8*)(Vr + key * QP + pc * 8) = vraw[j];
   }
   __syncthreads();
   const int64_t slot0 = ((int64_t)t * heads + (int64_t)kvh * GROUP) * max_chunks;
@@ -1661,8 +1686,12 @@ int launch_attend(hipStream_t s, const float* q, int64_t q_stride, const uint16_
     hipLaunchKernelGGL((attend_wide_q8_kernel<G, DD, 512>), grid, dim3(512), 0, s, q, q_stride,              \
                        (const __half*)k_cache, (const __half*)v_cache, cache_stride, qrow, heads, kv_heads,   \
                        scale, pos_dev, count_host, chunks, part_acc, part_ml, kv_index, index_stride);        \
+  else if (G <= 4 && kv_index)                                                                               \
+    hipLaunchKernelGGL((attend_mfma_kernel<(G <= 4 ? G : 4), DD, true>), grid, dim3(256), 0, s, q, q_stride,  \
+                       (const __half*)k_cache, (const __half*)v_cache, cache_stride, heads, kv_heads, scale,   \
+                       pos_dev, count_host, chunks, part_acc, part_ml, kv_index, index_stride);               \
   else if (G <= 4)                                                                                           \
-    hipLaunchKernelGGL((attend_mfma_kernel<(G <= 4 ? G : 4), DD>), grid, dim3(256), 0, s, q, q_stride,        \
+    hipLaunchKernelGGL((attend_mfma_kernel<(G <= 4 ? G : 4), DD, false>), grid, dim3(256), 0, s, q, q_stride, \
                        (const __half*)k_cache, (const __half*)v_cache, cache_stride, heads, kv_heads, scale,   \
                        pos_dev, count_host, chunks, part_acc, part_ml, kv_index, index_stride);               \
   else if (tokens == 1)                                                                                      \
