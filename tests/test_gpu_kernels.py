@@ -206,6 +206,12 @@ def test_matmul_tokens_epilogues(ctx, kind, tokens):
     (oracle.Q6_K, 2048, 5120, 1),
     (oracle.Q6_K, 2048, 8192, 1),
     (oracle.Q6_K, 4096, 11008, 1),
+    # one token, at most 4096 columns: 2048 waves each walk rows w, w + 2048,
+    # ... through a ring of three pieces, so these row counts end a wave's
+    # walk at each of the ring's three positions
+    (oracle.Q6_K, 4097, 4096, 1),
+    (oracle.Q6_K, 6145, 1024, 1),
+    (oracle.Q6_K, 10241, 2048, 1),
     # Q6_K rows of 2 and 6 superblocks at a batch: not whole 8-byte words,
     # so not the f16 tile
     (oracle.Q6_K, 200, 512, 4),
