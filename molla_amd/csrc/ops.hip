@@ -798,9 +798,12 @@ __global__ __launch_bounds__(256) void store_kv_q8_kernel(const float* __restric
 // latency, not a position load followed by one.  Each wave holds slice c's
 // (max, sum) in lane c, derives the weights exp(m_c - M) there, and every
 // thread takes the weights lane by lane (readlane) while it folds the values
-// in slice order: no LDS and no barrier.  Slices past the first 64 come in
-// further rounds of 64.
-constexpr int kMergeBatch = 64;
+// in slice order: no LDS and no barrier.  B, the slices a round takes, is
+// the workspace's slice count rounded up to a multiple of 8 (at most 64,
+// further rounds past it): each up-front load is an instruction of every
+// thread, and 64 of them where 36 slices are live made a decode step
+// 12-32 us slower (batch 1 to 8) than 40 or 48.
+template <int B>
 __global__ void attend_merge_kernel(const float* __restrict__ part_acc, const float* __restrict__ part_ml,
                                     int heads, int head_dim, const int32_t* __restrict__ pos_dev,
                                     int count_host, int max_chunks, float* __restrict__ out,
@@ -811,32 +814,32 @@ __global__ void attend_merge_kernel(const float* __restrict__ part_acc, const fl
   const bool live = d < head_dim;
   const float* pa = part_acc + slot * head_dim + min(d, head_dim - 1);
   const float2* pml = (const float2*)part_ml + slot;
-  float a[kMergeBatch];
+  float a[B];
 #pragma unroll
-  for (int k = 0; k < kMergeBatch; k++) a[k] = pa[(int64_t)min(k, max_chunks - 1) * head_dim];
+  for (int k = 0; k < B; k++) a[k] = pa[(int64_t)min(k, max_chunks - 1) * head_dim];
   float2 ml = pml[min(lane, max_chunks - 1)];
   const int count = pos_dev ? pos_dev[t] + 1 : count_host;  // a position p attends over p + 1 slots
   const int kk = attn_slice(head_dim);
   const int chunks = min((count + kk - 1) / kk, max_chunks);
   // the largest slice max over every round
   float M = lane < chunks ? ml.x : -INFINITY;
-  for (int c0 = kMergeBatch; c0 < chunks; c0 += kMergeBatch) {
+  for (int c0 = B; c0 < chunks; c0 += B) {
     const int c = c0 + lane;
     if (c < chunks) M = fmaxf(M, pml[c].x);
   }
   M = lanes::reduce<64>(M, lanes::Max{});
   float o = 0.0f, L = 0.0f;
-  for (int c0 = 0; c0 < chunks; c0 += kMergeBatch) {
+  for (int c0 = 0; c0 < chunks; c0 += B) {
     if (c0 > 0) {
 #pragma unroll
-      for (int k = 0; k < kMergeBatch; k++) a[k] = pa[(int64_t)min(c0 + k, chunks - 1) * head_dim];
+      for (int k = 0; k < B; k++) a[k] = pa[(int64_t)min(c0 + k, chunks - 1) * head_dim];
       ml = pml[min(c0 + lane, chunks - 1)];
     }
-    const int n = min(chunks - c0, kMergeBatch);
+    const int n = min(chunks - c0, B);
     const float w = lane < n ? expf(ml.x - M) : 0.0f;
     L += lane < n ? ml.y * w : 0.0f;
 #pragma unroll
-    for (int k = 0; k < kMergeBatch; k++) {
+    for (int k = 0; k < B; k++) {
       if (k < n) o = fmaf(a[k], __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), k)), o);
     }
   }
@@ -1650,6 +1653,28 @@ int launch_store_kv(hipStream_t s, const float* k, const float* v, int32_t kv_wi
   return hip_check(hipGetLastError(), "store_kv launch");
 }
 
+// attend_merge_kernel with B the slice count rounded up to 8 (at most 64)
+static int launch_merge(hipStream_t s, const float* part_acc, const float* part_ml, int heads, int head_dim,
+                        const int32_t* pos_dev, int count_host, int chunks, int tokens, float* out, void* xq_out,
+                        void* hx_out) {
+  const dim3 grid(heads, tokens), block(head_dim < 64 ? 64 : head_dim);
+#define MI_MERGE(B)                                                                                    \
+  hipLaunchKernelGGL(attend_merge_kernel<B>, grid, block, 0, s, part_acc, part_ml, heads, head_dim, pos_dev, \
+                     count_host, chunks, out, (uint8_t*)xq_out, (uint8_t*)hx_out)
+  switch ((std::min(chunks, 64) + 7) / 8) {
+    case 1: MI_MERGE(8); break;
+    case 2: MI_MERGE(16); break;
+    case 3: MI_MERGE(24); break;
+    case 4: MI_MERGE(32); break;
+    case 5: MI_MERGE(40); break;
+    case 6: MI_MERGE(48); break;
+    case 7: MI_MERGE(56); break;
+    default: MI_MERGE(64); break;
+  }
+#undef MI_MERGE
+  return hip_check(hipGetLastError(), "attend_merge launch");
+}
+
 size_t attend_workspace(int32_t heads, int32_t head_dim, int32_t max_count, int32_t tokens) {
   const int kk = attn_slice(head_dim);
   const int64_t chunks = (max_count + kk - 1) / kk;
@@ -1715,10 +1740,8 @@ int launch_attend(hipStream_t s, const float* q, int64_t q_stride, const uint16_
 #undef MI_WIDE
     int rc = hip_check(hipGetLastError(), "attend_wide launch");
     if (rc) return rc;
-    hipLaunchKernelGGL(attend_merge_kernel, dim3(heads, tokens), dim3(head_dim < 64 ? 64 : head_dim), 0, s,
-                       part_acc, part_ml, heads, head_dim, pos_dev, count_host, chunks, out, (uint8_t*)xq_out,
-                       (uint8_t*)hx_out);
-    return hip_check(hipGetLastError(), "attend_merge launch");
+    return launch_merge(s, part_acc, part_ml, heads, head_dim, pos_dev, count_host, chunks, tokens, out, xq_out,
+                        hx_out);
   }
   // one sequence's chunk (its tokens share one cache): 16 tokens per block
   // over one staged slice (f16 form; the q8 kernel takes one token a block)
@@ -1752,10 +1775,8 @@ int launch_attend(hipStream_t s, const float* q, int64_t q_stride, const uint16_
 #undef MI_CHUNK
     int rc = hip_check(hipGetLastError(), "attend_chunk launch");
     if (rc) return rc;
-    hipLaunchKernelGGL(attend_merge_kernel, dim3(heads, tokens), dim3(head_dim < 64 ? 64 : head_dim), 0, s,
-                       part_acc, part_ml, heads, head_dim, pos_dev, count_host, chunks, out, (uint8_t*)xq_out,
-                       (uint8_t*)hx_out);
-    return hip_check(hipGetLastError(), "attend_merge launch");
+    return launch_merge(s, part_acc, part_ml, heads, head_dim, pos_dev, count_host, chunks, tokens, out, xq_out,
+                        hx_out);
   }
   const int tq = (one_seq && tokens > kMaxTokens && form != MI_CACHE_Q8) ? 16 : 1;
   dim3 grid(chunks, kv_heads, (tokens + tq - 1) / tq);
@@ -1783,10 +1804,8 @@ int launch_attend(hipStream_t s, const float* q, int64_t q_stride, const uint16_
 #undef MI_ATTEND
   int rc = hip_check(hipGetLastError(), "attend_split launch");
   if (rc) return rc;
-  hipLaunchKernelGGL(attend_merge_kernel, dim3(heads, tokens), dim3(head_dim < 64 ? 64 : head_dim), 0, s,
-                     part_acc, part_ml, heads, head_dim, pos_dev,
-                     count_host, chunks, out, (uint8_t*)xq_out, (uint8_t*)hx_out);
-  return hip_check(hipGetLastError(), "attend_merge launch");
+  return launch_merge(s, part_acc, part_ml, heads, head_dim, pos_dev, count_host, chunks, tokens, out, xq_out,
+                      hx_out);
 }
 
 int launch_argmax(hipStream_t s, const float* x, int32_t n, int32_t tokens, int32_t* out) {
