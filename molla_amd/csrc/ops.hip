@@ -27,6 +27,10 @@ namespace {
 // fixed-point conversion is shuffle-heavy and one CU doing a whole row was
 // the slowest part.  All loads are issued before any arithmetic.
 constexpr int kNormThreads = 256;
+#ifndef MI_NORM_VEC
+#define MI_NORM_VEC 1
+#endif
+constexpr bool kNormVec = MI_NORM_VEC;
 
 // With `trig`, the last block also writes (cos, sin) of the angle of pair p at
 // pos[0] for p < pairs, in float64 as rope.mojo:253-285, for the layer's fused
@@ -58,7 +62,36 @@ __global__ __launch_bounds__(NT) void rms_norm_kernel(const float* __restrict__ 
   const int mine = blockIdx.x * NT + threadIdx.x;
   const bool live = mine < n;
   float xv[PER];
-  if constexpr (NS > 0) {
+  __shared__ float own[(NS > 0 && kNormVec) ? NT : 1];
+  if constexpr (NS > 0 && kNormVec) {
+    // 16-byte loads: thread t sums values 4 (t + NT q) .. +4, q < PER / 4
+    // (4 times fewer load instructions than one value a load, which bound
+    // the launch), and leaves the ones of its block's slice in LDS for the
+    // thread that owns them
+    typedef float nf4 __attribute__((ext_vector_type(4)));
+    nf4 pv[NS + 1][PER / 4];
+#pragma unroll
+    for (int j = 0; j <= NS; j++)
+#pragma unroll
+      for (int q = 0; q < PER / 4; q++) {
+        const int i = min(4 * ((int)threadIdx.x + q * NT), n - 4);
+        pv[j][q] = *(const nf4*)(xr + j * pstride + i);
+      }
+#pragma unroll
+    for (int q = 0; q < PER / 4; q++) {
+      nf4 v = pv[0][q];
+#pragma unroll
+      for (int j = 1; j < NS; j++) v += pv[j][q];
+      const int i0 = 4 * ((int)threadIdx.x + q * NT);
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const float xe = i0 + e < n ? pv[NS][q][e] + v[e] : 0.0f;
+        xv[4 * q + e] = xe;
+        const int r = i0 + e - (int)blockIdx.x * NT;
+        if (r >= 0 && r < NT) own[r] = xe;
+      }
+    }
+  } else if constexpr (NS > 0) {
     float pv[NS + 1][PER];
 #pragma unroll
     for (int j = 0; j <= NS; j++)
@@ -83,7 +116,8 @@ __global__ __launch_bounds__(NT) void rms_norm_kernel(const float* __restrict__ 
   }
   const float gm = live ? gain[mine] : 0.0f;
   // this thread's own value is one it already loaded for the sum (a second
-  // load of it measured a microsecond slower)
+  // load of it measured a microsecond slower); in the 16-byte form it comes
+  // from LDS after the barrier below
   float xm = xv[0];
 #pragma unroll
   for (int k = 1; k < PER; k++)
@@ -99,6 +133,7 @@ __global__ __launch_bounds__(NT) void rms_norm_kernel(const float* __restrict__ 
 #pragma unroll
   for (int i = 0; i < NT / kWave; i++) sum += part[i];
   const float scale = (float)(1.0 / sqrt(sum / (double)n + (double)eps));
+  if constexpr (NS > 0 && kNormVec) xm = live ? own[threadIdx.x] : 0.0f;
   const float v = xm * scale * gm;
   if constexpr (NS > 0) {
     if (live) out[(int64_t)t * n + mine] = xm;
