@@ -1150,7 +1150,10 @@ __global__ __launch_bounds__(256) void attend_mfma_kernel(
     // its three halves added in order
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-      const float s2 = __shfl(sacc[i], lane + GROUP), s3 = __shfl(sacc[i], lane + 2 * GROUP);
+      // (row shifts within the lane's 16-lane row: lanes lm < GROUP read
+      // lm + GROUP and lm + 2 GROUP)
+      const float s2 = __uint_as_float(lanes::dpp<0x100 + GROUP>(__float_as_uint(sacc[i])));
+      const float s3 = __uint_as_float(lanes::dpp<0x100 + 2 * GROUP>(__float_as_uint(sacc[i])));
       const float sc = (sacc[i] + s2) + s3;
       const int key = 16 * wave + 4 * lk + i;
       const bool live = key < nk && (!kv_index || kv_cell(kv_index, index_stride, t, start + key) >= 0);
@@ -1214,8 +1217,12 @@ __global__ __launch_bounds__(256) void attend_mfma_kernel(
         // rows 0..3 in lanes lk = 0, rows 4..7 in lanes lk = 1
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-          const float lo = __shfl(oacc[i], lane + 16);
-          if (lk == 0) part_acc[(slot0 + (int64_t)i * max_chunks + c) * D + dim] = (oacc[i] + lo) * kPDrop;
+          // row 0 (lk = 0) and row 1 swapped across: p[1] of a row-0 lane is
+          // its row-1 partner's value
+          const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(oacc[i]), __float_as_uint(oacc[i]), false,
+                                                          false);
+          const float hi = __uint_as_float(p[0]), lo = __uint_as_float(p[1]);
+          if (lk == 0) part_acc[(slot0 + (int64_t)i * max_chunks + c) * D + dim] = (hi + lo) * kPDrop;
         }
       } else if constexpr (GROUP == 2) {
         if (lk == 0) {
